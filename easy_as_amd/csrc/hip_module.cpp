@@ -1,0 +1,783 @@
+// hip_module.cpp — CPython binding `easy_as_amd._hip` over the C ABI in
+// include/eas_hip.h.
+//
+// It exposes the method names the reference runtime requires of its native
+// module (eas/runtime/metal_ext.py:22-33: is_available, compile, launch,
+// synchronize, alloc_buffer, copy_from_host, copy_to_host, dlpack_import,
+// dlpack_export, queue_synchronize) plus launch_async / launch_tg /
+// launch_tg_async, and the HIP-specific compile_to_code / load / launch_timed
+// / wrap_pointer / device_props / kernel_attrs.
+//
+// Objects crossing into Python are PyCapsules:
+//   "eas._hip.kernel"  -> eas_hip_kernel*       (module unloaded on destruction)
+//   "eas._hip.buffer"  -> Buffer                (memory freed / DLPack deleter run)
+//   "eas._hip.pending" -> Pending               (event + keepalives of a launch)
+// Launches take workgroup counts: HIP has no non-uniform dispatchThreads, so the
+// Python runtime converts thread counts and passes the true extents as hidden
+// kernel arguments.
+
+#define PY_SSIZE_T_CLEAN
+#include <Python.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "eas_hip.h"
+
+namespace {
+
+const char* kKernelCap = "eas._hip.kernel";
+const char* kBufferCap = "eas._hip.buffer";
+const char* kPendingCap = "eas._hip.pending";
+
+struct Buffer {
+  void* ptr;
+  size_t nbytes;
+  int storage;         // EAS_HIP_STORAGE_*
+  bool owns;           // free with eas_hip_free on destruction
+  void* dl_managed;    // imported DLManagedTensor to delete on destruction
+  PyObject* owner;     // object kept alive by a wrapped pointer
+};
+
+struct Pending {
+  void* event;
+  std::vector<PyObject*> keepalive;
+};
+
+PyObject* raise_status(int rc) {
+  PyObject* exc = PyExc_RuntimeError;
+  if (rc == EAS_HIP_ERR_INVALID) exc = PyExc_ValueError;
+  if (rc == EAS_HIP_ERR_NOMEM) exc = PyExc_MemoryError;
+  PyErr_SetString(exc, eas_hip_last_error());
+  return nullptr;
+}
+
+void kernel_destructor(PyObject* cap) {
+  auto* k = static_cast<eas_hip_kernel*>(PyCapsule_GetPointer(cap, kKernelCap));
+  if (k) eas_hip_kernel_release(k);
+  else PyErr_Clear();
+}
+
+void buffer_destructor(PyObject* cap) {
+  auto* b = static_cast<Buffer*>(PyCapsule_GetPointer(cap, kBufferCap));
+  if (!b) {
+    PyErr_Clear();
+    return;
+  }
+  if (b->dl_managed) eas_hip_dlpack_delete(b->dl_managed);
+  else if (b->owns) eas_hip_free(b->ptr, b->storage);
+  Py_XDECREF(b->owner);
+  delete b;
+}
+
+void release_pending(Pending* p) {
+  if (p->event) {
+    Py_BEGIN_ALLOW_THREADS
+    eas_hip_event_synchronize(p->event);
+    Py_END_ALLOW_THREADS
+    eas_hip_event_destroy(p->event);
+    p->event = nullptr;
+  }
+  for (PyObject* o : p->keepalive) Py_XDECREF(o);
+  p->keepalive.clear();
+}
+
+void pending_destructor(PyObject* cap) {
+  auto* p = static_cast<Pending*>(PyCapsule_GetPointer(cap, kPendingCap));
+  if (!p) {
+    PyErr_Clear();
+    return;
+  }
+  release_pending(p);
+  delete p;
+}
+
+Buffer* as_buffer(PyObject* obj) {
+  if (!PyCapsule_IsValid(obj, kBufferCap)) return nullptr;
+  return static_cast<Buffer*>(PyCapsule_GetPointer(obj, kBufferCap));
+}
+
+PyObject* new_buffer(void* ptr, size_t nbytes, int storage, bool owns, void* dl, PyObject* owner) {
+  auto* b = new Buffer{ptr, nbytes, storage, owns, dl, owner};
+  Py_XINCREF(owner);
+  PyObject* cap = PyCapsule_New(b, kBufferCap, buffer_destructor);
+  if (!cap) {
+    Py_XDECREF(owner);
+    delete b;
+  }
+  return cap;
+}
+
+bool parse_dim3(PyObject* obj, uint32_t out[3], const char* what) {
+  out[0] = out[1] = out[2] = 1;
+  if (PyLong_Check(obj)) {
+    unsigned long long v = PyLong_AsUnsignedLongLong(obj);
+    if (PyErr_Occurred()) return false;
+    if (v > 0xFFFFFFFFull) {
+      PyErr_Format(PyExc_OverflowError, "%s too large", what);
+      return false;
+    }
+    out[0] = (uint32_t)v;
+    return true;
+  }
+  PyObject* seq = PySequence_Fast(obj, "expected an int or a tuple/list of ints");
+  if (!seq) return false;
+  Py_ssize_t n = PySequence_Fast_GET_SIZE(seq);
+  if (n < 1 || n > 3) {
+    Py_DECREF(seq);
+    PyErr_Format(PyExc_ValueError, "%s must have 1..3 dims", what);
+    return false;
+  }
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject* it = PySequence_Fast_GET_ITEM(seq, i);
+    if (!PyLong_Check(it)) {
+      Py_DECREF(seq);
+      PyErr_Format(PyExc_TypeError, "%s dim %zd must be int", what, i);
+      return false;
+    }
+    unsigned long long v = PyLong_AsUnsignedLongLong(it);
+    if (PyErr_Occurred() || v > 0xFFFFFFFFull) {
+      Py_DECREF(seq);
+      if (!PyErr_Occurred()) PyErr_Format(PyExc_OverflowError, "%s too large", what);
+      return false;
+    }
+    out[i] = (uint32_t)v;
+  }
+  Py_DECREF(seq);
+  return true;
+}
+
+void append_aligned(std::vector<uint8_t>& blob, const void* data, size_t size, size_t align) {
+  size_t off = (blob.size() + align - 1) / align * align;
+  blob.resize(off + size);
+  memcpy(blob.data() + off, data, size);
+}
+
+// Pack argv into a kernel-argument blob at natural alignment; buffer capsules
+// become device pointers (and are appended to `keep`), bytes are copied raw,
+// int -> u32, float -> f32.  Mirrors bind_args_fast (_metal.mm:855-951).
+bool pack_args(PyObject* argv_obj, PyObject* writable_obj, std::vector<uint8_t>& blob, std::vector<PyObject*>* keep) {
+  PyObject* argv = PySequence_Fast(argv_obj, "argv must be a sequence");
+  if (!argv) return false;
+  PyObject* writable = PySequence_Fast(writable_obj, "writable must be a sequence");
+  if (!writable) {
+    Py_DECREF(argv);
+    return false;
+  }
+  bool ok = true;
+  const Py_ssize_t n = PySequence_Fast_GET_SIZE(argv);
+  if (PySequence_Fast_GET_SIZE(writable) != n) {
+    PyErr_SetString(PyExc_ValueError, "writable must have same length as argv");
+    ok = false;
+  }
+  for (Py_ssize_t i = 0; ok && i < n; ++i) {
+    PyObject* obj = PySequence_Fast_GET_ITEM(argv, i);
+    int want_write = PyObject_IsTrue(PySequence_Fast_GET_ITEM(writable, i));
+    if (want_write < 0) {
+      ok = false;
+      break;
+    }
+    if (Buffer* b = as_buffer(obj)) {
+      uint64_t p = (uint64_t)(uintptr_t)b->ptr;
+      append_aligned(blob, &p, 8, 8);
+      if (keep) {
+        Py_INCREF(obj);
+        keep->push_back(obj);
+      }
+      continue;
+    }
+    if (want_write) {
+      PyErr_Format(PyExc_TypeError, "writable arg %zd must be a buffer capsule (use alloc_buffer/dlpack_import)", i);
+      ok = false;
+      break;
+    }
+    if (PyBytes_Check(obj) || PyByteArray_Check(obj)) {
+      const char* data = PyBytes_Check(obj) ? PyBytes_AS_STRING(obj) : PyByteArray_AS_STRING(obj);
+      Py_ssize_t len = PyBytes_Check(obj) ? PyBytes_GET_SIZE(obj) : PyByteArray_GET_SIZE(obj);
+      if (len <= 0) {
+        PyErr_SetString(PyExc_ValueError, "scalar bytes cannot be empty");
+        ok = false;
+        break;
+      }
+      size_t align = 1;
+      while (align < 8 && (size_t)len % (align * 2) == 0) align *= 2;
+      append_aligned(blob, data, (size_t)len, align);
+      continue;
+    }
+    if (PyLong_Check(obj)) {
+      unsigned long long v = PyLong_AsUnsignedLongLong(obj);
+      if (PyErr_Occurred()) {
+        ok = false;
+        break;
+      }
+      if (v > 0xFFFFFFFFull) {
+        PyErr_SetString(PyExc_OverflowError, "int scalar too large (expected uint32); pass bytes for larger types");
+        ok = false;
+        break;
+      }
+      uint32_t u = (uint32_t)v;
+      append_aligned(blob, &u, 4, 4);
+      continue;
+    }
+    if (PyFloat_Check(obj)) {
+      float f = (float)PyFloat_AsDouble(obj);
+      append_aligned(blob, &f, 4, 4);
+      continue;
+    }
+    PyErr_Format(PyExc_TypeError, "unsupported arg %zd type (expected buffer capsule or scalar bytes/int/float)", i);
+    ok = false;
+  }
+  Py_DECREF(writable);
+  Py_DECREF(argv);
+  if (!ok && keep) {
+    for (PyObject* o : *keep) Py_DECREF(o);
+    keep->clear();
+  }
+  return ok;
+}
+
+eas_hip_kernel* as_kernel(PyObject* cap) {
+  return static_cast<eas_hip_kernel*>(PyCapsule_GetPointer(cap, kKernelCap));
+}
+
+void* as_stream(PyObject* obj) {
+  if (!obj || obj == Py_None) return nullptr;
+  return PyLong_AsVoidPtr(obj);
+}
+
+// ---------------------------------------------------------------------------
+
+PyObject* py_is_available(PyObject*, PyObject*) { return PyBool_FromLong(eas_hip_is_available()); }
+
+PyObject* py_device_props(PyObject*, PyObject* args) {
+  int dev = -1;
+  if (!PyArg_ParseTuple(args, "|i", &dev)) return nullptr;
+  eas_hip_device_props p;
+  int rc = eas_hip_device_props_get(dev, &p);
+  if (rc) return raise_status(rc);
+  return Py_BuildValue("{s:s,s:i,s:i,s:i,s:i,s:K,s:K,s:i,s:i}", "arch", p.arch, "compute_units", p.compute_units,
+                       "clock_khz", p.clock_khz, "memory_clock_khz", p.memory_clock_khz, "memory_bus_width",
+                       p.memory_bus_width, "total_global_mem", (unsigned long long)p.total_global_mem, "lds_per_block",
+                       (unsigned long long)p.lds_per_block, "warp_size", p.warp_size, "max_threads_per_block",
+                       p.max_threads_per_block);
+}
+
+bool collect_options(PyObject* opts, std::vector<std::string>& store, std::vector<const char*>& ptrs) {
+  if (!opts || opts == Py_None) return true;
+  PyObject* seq = PySequence_Fast(opts, "options must be a sequence of str");
+  if (!seq) return false;
+  for (Py_ssize_t i = 0; i < PySequence_Fast_GET_SIZE(seq); ++i) {
+    const char* s = PyUnicode_AsUTF8(PySequence_Fast_GET_ITEM(seq, i));
+    if (!s) {
+      Py_DECREF(seq);
+      return false;
+    }
+    store.emplace_back(s);
+  }
+  Py_DECREF(seq);
+  for (auto& s : store) ptrs.push_back(s.c_str());
+  return true;
+}
+
+// compile_to_code(src, name, options) -> bytes (code object); no GPU required.
+PyObject* py_compile_to_code(PyObject*, PyObject* args) {
+  const char* src;
+  const char* name;
+  PyObject* opts = nullptr;
+  if (!PyArg_ParseTuple(args, "ss|O", &src, &name, &opts)) return nullptr;
+  std::vector<std::string> store;
+  std::vector<const char*> ptrs;
+  if (!collect_options(opts, store, ptrs)) return nullptr;
+  void* code = nullptr;
+  size_t size = 0;
+  std::string log(1 << 16, '\0');
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = eas_hip_compile_source(src, name, ptrs.data(), (int)ptrs.size(), &code, &size, &log[0], log.size());
+  Py_END_ALLOW_THREADS
+  if (rc) {
+    if (rc == EAS_HIP_ERR_COMPILE) {
+      PyErr_Format(PyExc_RuntimeError, "HIP compile failed: %s\n%s", eas_hip_last_error(), log.c_str());
+      return nullptr;
+    }
+    return raise_status(rc);
+  }
+  PyObject* out = PyBytes_FromStringAndSize(static_cast<const char*>(code), (Py_ssize_t)size);
+  eas_hip_free_host(code);
+  return out;
+}
+
+// load(code: bytes, name) -> kernel capsule
+PyObject* py_load(PyObject*, PyObject* args) {
+  Py_buffer code;
+  const char* name;
+  if (!PyArg_ParseTuple(args, "y*s", &code, &name)) return nullptr;
+  eas_hip_kernel* k = nullptr;
+  int rc = eas_hip_kernel_load(code.buf, (size_t)code.len, name, &k);
+  PyBuffer_Release(&code);
+  if (rc) return raise_status(rc);
+  return PyCapsule_New(k, kKernelCap, kernel_destructor);
+}
+
+// compile(src, name, options=None) -> kernel capsule (reference: compile(msl, name))
+PyObject* py_compile(PyObject* self, PyObject* args) {
+  const char* src;
+  const char* name;
+  PyObject* opts = nullptr;
+  if (!PyArg_ParseTuple(args, "ss|O", &src, &name, &opts)) return nullptr;
+  PyObject* code = py_compile_to_code(self, args);
+  if (!code) return nullptr;
+  eas_hip_kernel* k = nullptr;
+  int rc = eas_hip_kernel_load(PyBytes_AS_STRING(code), (size_t)PyBytes_GET_SIZE(code), name, &k);
+  Py_DECREF(code);
+  if (rc) return raise_status(rc);
+  return PyCapsule_New(k, kKernelCap, kernel_destructor);
+}
+
+PyObject* py_kernel_attrs(PyObject*, PyObject* args) {
+  PyObject* cap;
+  if (!PyArg_ParseTuple(args, "O", &cap)) return nullptr;
+  eas_hip_kernel* k = as_kernel(cap);
+  if (!k) return nullptr;
+  int mt, lds, vg, sg, priv;
+  int rc = eas_hip_kernel_attrs(k, &mt, &lds, &vg, &sg, &priv);
+  if (rc) return raise_status(rc);
+  return Py_BuildValue("{s:i,s:i,s:i,s:i}", "max_threads_per_block", mt, "static_lds_bytes", lds, "num_vgprs", vg,
+                       "private_bytes", priv);
+}
+
+// alloc_buffer(nbytes, storage="private") -> buffer capsule
+PyObject* py_alloc_buffer(PyObject*, PyObject* args) {
+  long long nbytes;
+  const char* storage = "private";
+  if (!PyArg_ParseTuple(args, "L|s", &nbytes, &storage)) return nullptr;
+  if (nbytes <= 0) {
+    PyErr_SetString(PyExc_ValueError, "nbytes must be > 0");
+    return nullptr;
+  }
+  int kind;
+  if (!strcmp(storage, "private")) kind = EAS_HIP_STORAGE_DEVICE;
+  else if (!strcmp(storage, "shared")) kind = EAS_HIP_STORAGE_SHARED;
+  else {
+    PyErr_SetString(PyExc_ValueError, "storage must be 'private' or 'shared'");
+    return nullptr;
+  }
+  void* p = nullptr;
+  int rc = eas_hip_alloc((size_t)nbytes, kind, &p);
+  if (rc) return raise_status(rc);
+  PyObject* cap = new_buffer(p, (size_t)nbytes, kind, true, nullptr, nullptr);
+  if (!cap) eas_hip_free(p, kind);
+  return cap;
+}
+
+// wrap_pointer(ptr, nbytes, owner=None) -> non-owning buffer capsule over device memory
+PyObject* py_wrap_pointer(PyObject*, PyObject* args) {
+  unsigned long long ptr;
+  long long nbytes;
+  PyObject* owner = Py_None;
+  if (!PyArg_ParseTuple(args, "KL|O", &ptr, &nbytes, &owner)) return nullptr;
+  if (nbytes < 0) {
+    PyErr_SetString(PyExc_ValueError, "nbytes must be >= 0");
+    return nullptr;
+  }
+  return new_buffer((void*)(uintptr_t)ptr, (size_t)nbytes, EAS_HIP_STORAGE_DEVICE, false, nullptr,
+                    owner == Py_None ? nullptr : owner);
+}
+
+PyObject* py_buffer_info(PyObject*, PyObject* args) {
+  PyObject* cap;
+  if (!PyArg_ParseTuple(args, "O", &cap)) return nullptr;
+  Buffer* b = as_buffer(cap);
+  if (!b) {
+    PyErr_SetString(PyExc_TypeError, "expected a buffer capsule");
+    return nullptr;
+  }
+  return Py_BuildValue("(KKs)", (unsigned long long)(uintptr_t)b->ptr, (unsigned long long)b->nbytes,
+                       b->storage == EAS_HIP_STORAGE_SHARED ? "shared" : "private");
+}
+
+// copy_from_host(buf, src) / copy_to_host(buf, dst): synchronous, size-checked.
+PyObject* copy_impl(PyObject* args, bool to_device) {
+  PyObject* cap;
+  PyObject* host;
+  if (!PyArg_ParseTuple(args, "OO", &cap, &host)) return nullptr;
+  Buffer* b = as_buffer(cap);
+  if (!b) {
+    PyErr_SetString(PyExc_TypeError, "expected a buffer capsule");
+    return nullptr;
+  }
+  Py_buffer view;
+  if (PyObject_GetBuffer(host, &view, to_device ? PyBUF_C_CONTIGUOUS : (PyBUF_C_CONTIGUOUS | PyBUF_WRITABLE)) != 0)
+    return nullptr;
+  size_t n = (size_t)view.len;
+  int rc = EAS_HIP_OK;
+  if (n == 0) {
+    PyBuffer_Release(&view);
+    PyErr_SetString(PyExc_ValueError, "host buffer is empty");
+    return nullptr;
+  }
+  if (to_device && n > b->nbytes) {
+    PyBuffer_Release(&view);
+    PyErr_SetString(PyExc_ValueError, "source is larger than destination buffer");
+    return nullptr;
+  }
+  if (!to_device && n < b->nbytes) {
+    PyBuffer_Release(&view);
+    PyErr_SetString(PyExc_ValueError, "destination is smaller than source buffer");
+    return nullptr;
+  }
+  size_t count = to_device ? n : b->nbytes;
+  if (b->storage == EAS_HIP_STORAGE_SHARED) {
+    // Pinned host memory: make prior GPU writes visible, then a plain memcpy.
+    Py_BEGIN_ALLOW_THREADS
+    rc = eas_hip_device_synchronize();
+    if (!rc) {
+      if (to_device) memcpy(b->ptr, view.buf, count);
+      else memcpy(view.buf, b->ptr, count);
+    }
+    Py_END_ALLOW_THREADS
+  } else {
+    Py_BEGIN_ALLOW_THREADS
+    rc = to_device ? eas_hip_copy_h2d(b->ptr, view.buf, count) : eas_hip_copy_d2h(view.buf, b->ptr, count);
+    Py_END_ALLOW_THREADS
+  }
+  PyBuffer_Release(&view);
+  if (rc) return raise_status(rc);
+  Py_RETURN_NONE;
+}
+
+PyObject* py_copy_from_host(PyObject*, PyObject* args) { return copy_impl(args, true); }
+PyObject* py_copy_to_host(PyObject*, PyObject* args) { return copy_impl(args, false); }
+
+// copy_buffer(dst, src, nbytes): device-to-device copy.
+PyObject* py_copy_buffer(PyObject*, PyObject* args) {
+  PyObject *dcap, *scap;
+  long long n;
+  if (!PyArg_ParseTuple(args, "OOL", &dcap, &scap, &n)) return nullptr;
+  Buffer* d = as_buffer(dcap);
+  Buffer* s = as_buffer(scap);
+  if (!d || !s) {
+    PyErr_SetString(PyExc_TypeError, "expected buffer capsules");
+    return nullptr;
+  }
+  if (n < 0 || (size_t)n > d->nbytes || (size_t)n > s->nbytes) {
+    PyErr_SetString(PyExc_ValueError, "copy size exceeds a buffer");
+    return nullptr;
+  }
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = eas_hip_copy_d2d(d->ptr, s->ptr, (size_t)n);
+  Py_END_ALLOW_THREADS
+  if (rc) return raise_status(rc);
+  Py_RETURN_NONE;
+}
+
+struct LaunchArgs {
+  PyObject* kernel = nullptr;
+  PyObject* argv = nullptr;
+  PyObject* writable = nullptr;
+  PyObject* grid = nullptr;
+  PyObject* block = nullptr;
+  int repeat = 1;
+  unsigned int lds = 0;
+  PyObject* stream = nullptr;
+  uint32_t g[3], b[3];
+  eas_hip_kernel* k = nullptr;
+};
+
+bool parse_launch(PyObject* args, PyObject* kwargs, LaunchArgs& a) {
+  static const char* kw[] = {"kernel", "argv", "writable", "grid", "block", "repeat", "lds", "stream", nullptr};
+  if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOOO|iIO", const_cast<char**>(kw), &a.kernel, &a.argv, &a.writable,
+                                   &a.grid, &a.block, &a.repeat, &a.lds, &a.stream))
+    return false;
+  if (a.repeat <= 0) {
+    PyErr_SetString(PyExc_ValueError, "repeat must be > 0");
+    return false;
+  }
+  a.k = as_kernel(a.kernel);
+  if (!a.k) return false;
+  if (!parse_dim3(a.grid, a.g, "grid") || !parse_dim3(a.block, a.b, "block")) return false;
+  if (a.g[0] == 0 || a.g[1] == 0 || a.g[2] == 0) {
+    PyErr_SetString(PyExc_ValueError, "grid dims must be > 0");
+    return false;
+  }
+  if (a.b[0] == 0 || a.b[1] == 0 || a.b[2] == 0) {
+    PyErr_SetString(PyExc_ValueError, "block dims must be > 0");
+    return false;
+  }
+  if ((uint64_t)a.b[0] * a.b[1] * a.b[2] > 1024) {
+    PyErr_Format(PyExc_ValueError, "threads_per_threadgroup too large: %llu",
+                 (unsigned long long)a.b[0] * a.b[1] * a.b[2]);
+    return false;
+  }
+  return true;
+}
+
+// launch(kernel, argv, writable, grid, block, repeat=1, lds=0, stream=None):
+// enqueue and wait (GIL released while waiting), like the reference's sync launch.
+PyObject* launch_impl(PyObject* args, PyObject* kwargs, bool async) {
+  LaunchArgs a;
+  if (!parse_launch(args, kwargs, a)) return nullptr;
+  std::vector<uint8_t> blob;
+  auto* pending = async ? new Pending{nullptr, {}} : nullptr;
+  if (!pack_args(a.argv, a.writable, blob, pending ? &pending->keepalive : nullptr)) {
+    delete pending;
+    return nullptr;
+  }
+  void* stream = as_stream(a.stream);
+  if (PyErr_Occurred()) {
+    if (pending) release_pending(pending);
+    delete pending;
+    return nullptr;
+  }
+  int rc = eas_hip_launch(a.k, blob.data(), blob.size(), a.g, a.b, a.lds, stream, a.repeat);
+  if (rc) {
+    if (pending) release_pending(pending);
+    delete pending;
+    return raise_status(rc);
+  }
+  if (!async) {
+    Py_BEGIN_ALLOW_THREADS
+    rc = eas_hip_stream_synchronize(stream);
+    Py_END_ALLOW_THREADS
+    if (rc) return raise_status(rc);
+    Py_RETURN_NONE;
+  }
+  Py_INCREF(a.kernel);
+  pending->keepalive.push_back(a.kernel);
+  rc = eas_hip_event_create(&pending->event);
+  if (!rc) rc = eas_hip_event_record(pending->event, stream);
+  if (rc) {
+    release_pending(pending);
+    delete pending;
+    return raise_status(rc);
+  }
+  PyObject* cap = PyCapsule_New(pending, kPendingCap, pending_destructor);
+  if (!cap) {
+    release_pending(pending);
+    delete pending;
+  }
+  return cap;
+}
+
+PyObject* py_launch(PyObject*, PyObject* args, PyObject* kw) { return launch_impl(args, kw, false); }
+PyObject* py_launch_async(PyObject*, PyObject* args, PyObject* kw) { return launch_impl(args, kw, true); }
+
+// launch_timed(kernel, argv, writable, grid, block, repeat=1, lds=0, stream=None, warmup=0) -> mean ms per launch
+PyObject* py_launch_timed(PyObject*, PyObject* args, PyObject* kwargs) {
+  PyObject* warm_obj = kwargs ? PyDict_GetItemString(kwargs, "warmup") : nullptr;
+  long warmup = 0;
+  PyObject* kw2 = nullptr;
+  if (warm_obj) {
+    warmup = PyLong_AsLong(warm_obj);
+    if (PyErr_Occurred()) return nullptr;
+    kw2 = PyDict_Copy(kwargs);
+    if (!kw2) return nullptr;
+    PyDict_DelItemString(kw2, "warmup");
+  }
+  LaunchArgs a;
+  bool ok = parse_launch(args, kw2 ? kw2 : kwargs, a);
+  Py_XDECREF(kw2);
+  if (!ok) return nullptr;
+  if (warmup < 0) {
+    PyErr_SetString(PyExc_ValueError, "warmup must be >= 0");
+    return nullptr;
+  }
+  std::vector<uint8_t> blob;
+  if (!pack_args(a.argv, a.writable, blob, nullptr)) return nullptr;
+  void* stream = as_stream(a.stream);
+  if (PyErr_Occurred()) return nullptr;
+  float ms = 0.f;
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = eas_hip_launch_timed(a.k, blob.data(), blob.size(), a.g, a.b, a.lds, stream, (int)warmup, a.repeat, &ms);
+  Py_END_ALLOW_THREADS
+  if (rc) return raise_status(rc);
+  return PyFloat_FromDouble((double)ms);
+}
+
+PyObject* py_synchronize(PyObject*, PyObject* args) {
+  PyObject* cap;
+  if (!PyArg_ParseTuple(args, "O", &cap)) return nullptr;
+  auto* p = static_cast<Pending*>(PyCapsule_GetPointer(cap, kPendingCap));
+  if (!p) return nullptr;
+  int rc = EAS_HIP_OK;
+  if (p->event) {
+    Py_BEGIN_ALLOW_THREADS
+    rc = eas_hip_event_synchronize(p->event);
+    Py_END_ALLOW_THREADS
+  }
+  release_pending(p);
+  if (rc) return raise_status(rc);
+  Py_RETURN_NONE;
+}
+
+PyObject* py_queue_synchronize(PyObject*, PyObject* args) {
+  PyObject* stream = nullptr;
+  if (!PyArg_ParseTuple(args, "|O", &stream)) return nullptr;
+  void* s = as_stream(stream);
+  if (PyErr_Occurred()) return nullptr;
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = s ? eas_hip_stream_synchronize(s) : eas_hip_device_synchronize();
+  Py_END_ALLOW_THREADS
+  if (rc) return raise_status(rc);
+  Py_RETURN_NONE;
+}
+
+// dlpack_import(capsule 'dltensor') -> (buffer capsule, shape tuple, dtype bits).
+// Takes ownership (capsule renamed 'used_dltensor'); the deleter runs when the
+// buffer capsule dies.  Reference: _metal.mm:530-638.
+PyObject* py_dlpack_import(PyObject*, PyObject* args) {
+  PyObject* cap;
+  if (!PyArg_ParseTuple(args, "O", &cap)) return nullptr;
+  if (!PyCapsule_CheckExact(cap)) {
+    PyErr_SetString(PyExc_TypeError, "expected a DLPack capsule (PyCapsule)");
+    return nullptr;
+  }
+  const char* name = PyCapsule_GetName(cap);
+  if (!name || strcmp(name, "dltensor") != 0) {
+    PyErr_SetString(PyExc_ValueError, "expected a DLPack capsule with name 'dltensor'");
+    return nullptr;
+  }
+  void* managed = PyCapsule_GetPointer(cap, "dltensor");
+  if (!managed) return nullptr;
+  void* data = nullptr;
+  uint64_t nbytes = 0;
+  int bits = 0, ndim = 0, dev_type = 0, dev_id = 0;
+  int64_t shape[16];
+  int rc = eas_hip_dlpack_view(managed, &data, &nbytes, &bits, &ndim, shape, 16, &dev_type, &dev_id);
+  if (rc) {
+    PyErr_SetString(strstr(eas_hip_last_error(), "only supports") ? PyExc_TypeError : PyExc_ValueError,
+                    eas_hip_last_error());
+    return nullptr;
+  }
+  if (dev_type != 10) {
+    PyErr_Format(PyExc_ValueError, "dlpack_import expects kDLROCM device_type=10, got %d", dev_type);
+    return nullptr;
+  }
+  if (PyCapsule_SetName(cap, "used_dltensor") != 0) return nullptr;
+  if (PyCapsule_SetDestructor(cap, nullptr) != 0) return nullptr;
+  PyObject* buf = new_buffer(data, (size_t)nbytes, EAS_HIP_STORAGE_DEVICE, false, managed, nullptr);
+  if (!buf) return nullptr;
+  PyObject* shp = PyTuple_New(ndim);
+  for (int i = 0; shp && i < ndim; ++i) PyTuple_SET_ITEM(shp, i, PyLong_FromLongLong(shape[i]));
+  if (!shp) {
+    Py_DECREF(buf);
+    return nullptr;
+  }
+  return Py_BuildValue("(NNi)", buf, shp, bits);
+}
+
+void export_release(void* ctx) {
+  PyGILState_STATE st = PyGILState_Ensure();
+  Py_XDECREF(static_cast<PyObject*>(ctx));
+  PyGILState_Release(st);
+}
+
+void dltensor_capsule_destructor(PyObject* cap) {
+  // Only an unconsumed capsule still owns its tensor.
+  if (!PyCapsule_IsValid(cap, "dltensor")) return;
+  void* m = PyCapsule_GetPointer(cap, "dltensor");
+  if (m) eas_hip_dlpack_delete(m);
+}
+
+// dlpack_export(buf, shape, dtype_bits) -> 'dltensor' capsule (kDLROCM).
+// Waits for the device first, like the reference's full-queue sync (_metal.mm:786-793).
+PyObject* py_dlpack_export(PyObject*, PyObject* args) {
+  PyObject* cap;
+  PyObject* shape_obj;
+  int bits = 32;
+  int device_id = 0;
+  if (!PyArg_ParseTuple(args, "OO|ii", &cap, &shape_obj, &bits, &device_id)) return nullptr;
+  Buffer* b = as_buffer(cap);
+  if (!b) {
+    PyErr_SetString(PyExc_TypeError, "expected a buffer capsule");
+    return nullptr;
+  }
+  PyObject* seq = PySequence_Fast(shape_obj, "shape must be a sequence of ints");
+  if (!seq) return nullptr;
+  Py_ssize_t ndim = PySequence_Fast_GET_SIZE(seq);
+  if (ndim <= 0 || ndim > 8) {
+    Py_DECREF(seq);
+    PyErr_SetString(PyExc_ValueError, "shape must have 1..8 dims");
+    return nullptr;
+  }
+  int64_t shape[8];
+  unsigned long long numel = 1;
+  for (Py_ssize_t i = 0; i < ndim; ++i) {
+    long long d = PyLong_AsLongLong(PySequence_Fast_GET_ITEM(seq, i));
+    if (PyErr_Occurred() || d < 0) {
+      Py_DECREF(seq);
+      if (!PyErr_Occurred()) PyErr_SetString(PyExc_ValueError, "invalid shape");
+      return nullptr;
+    }
+    shape[i] = d;
+    numel *= (unsigned long long)d;
+  }
+  Py_DECREF(seq);
+  if (bits != 16 && bits != 32) {
+    PyErr_SetString(PyExc_ValueError, "dtype_bits must be 16 or 32");
+    return nullptr;
+  }
+  if (numel * (unsigned long long)(bits / 8) > b->nbytes) {
+    PyErr_SetString(PyExc_ValueError, "shape exceeds buffer view size");
+    return nullptr;
+  }
+  int rc;
+  Py_BEGIN_ALLOW_THREADS
+  rc = eas_hip_device_synchronize();
+  Py_END_ALLOW_THREADS
+  if (rc) return raise_status(rc);
+  void* managed = nullptr;
+  Py_INCREF(cap);
+  rc = eas_hip_dlpack_make(b->ptr, device_id, shape, (int)ndim, bits, export_release, cap, &managed);
+  if (rc) {
+    Py_DECREF(cap);
+    return raise_status(rc);
+  }
+  PyObject* out = PyCapsule_New(managed, "dltensor", dltensor_capsule_destructor);
+  if (!out) eas_hip_dlpack_delete(managed);
+  return out;
+}
+
+PyMethodDef kMethods[] = {
+    {"is_available", py_is_available, METH_NOARGS, "1 if a HIP GPU is usable."},
+    {"device_props", py_device_props, METH_VARARGS, "Properties of a device (default: current)."},
+    {"compile_to_code", py_compile_to_code, METH_VARARGS, "hiprtc: source -> code object bytes (no GPU needed)."},
+    {"load", py_load, METH_VARARGS, "Load a code object and look up a kernel."},
+    {"compile", py_compile, METH_VARARGS, "compile_to_code + load."},
+    {"kernel_attrs", py_kernel_attrs, METH_VARARGS, "Static resources of a loaded kernel."},
+    {"alloc_buffer", py_alloc_buffer, METH_VARARGS, "Allocate device ('private') or pinned ('shared') memory."},
+    {"wrap_pointer", py_wrap_pointer, METH_VARARGS, "Non-owning buffer capsule over existing device memory."},
+    {"buffer_info", py_buffer_info, METH_VARARGS, "(ptr, nbytes, storage) of a buffer capsule."},
+    {"copy_from_host", py_copy_from_host, METH_VARARGS, "Synchronous host -> buffer copy."},
+    {"copy_to_host", py_copy_to_host, METH_VARARGS, "Synchronous buffer -> host copy."},
+    {"copy_buffer", py_copy_buffer, METH_VARARGS, "Synchronous buffer -> buffer copy."},
+    {"launch", (PyCFunction)(void (*)(void))py_launch, METH_VARARGS | METH_KEYWORDS, "Launch and wait."},
+    {"launch_async", (PyCFunction)(void (*)(void))py_launch_async, METH_VARARGS | METH_KEYWORDS,
+     "Launch; returns a pending capsule."},
+    {"launch_tg", (PyCFunction)(void (*)(void))py_launch, METH_VARARGS | METH_KEYWORDS,
+     "Alias of launch (HIP always dispatches workgroups)."},
+    {"launch_tg_async", (PyCFunction)(void (*)(void))py_launch_async, METH_VARARGS | METH_KEYWORDS,
+     "Alias of launch_async."},
+    {"launch_timed", (PyCFunction)(void (*)(void))py_launch_timed, METH_VARARGS | METH_KEYWORDS,
+     "Event-timed repeat launches; mean ms per launch."},
+    {"synchronize", py_synchronize, METH_VARARGS, "Wait for a pending launch and drop its keepalives."},
+    {"queue_synchronize", py_queue_synchronize, METH_VARARGS, "Wait for a stream (default: whole device)."},
+    {"dlpack_import", py_dlpack_import, METH_VARARGS, "Zero-copy import of a kDLROCM DLPack capsule."},
+    {"dlpack_export", py_dlpack_export, METH_VARARGS, "Export a buffer as a kDLROCM DLPack capsule."},
+    {nullptr, nullptr, 0, nullptr},
+};
+
+PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_hip", "MI355X (gfx950) HIP backend of eas.", -1, kMethods};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__hip(void) {
+  PyObject* m = PyModule_Create(&kModule);
+  if (m) PyModule_AddIntConstant(m, "ABI_VERSION", eas_hip_abi_version());
+  return m;
+}

@@ -1,0 +1,208 @@
+"""``@eas.kernel``: argument binding, constexpr split, specialisation cache, launch.
+
+Public behaviour follows the reference launcher (``eas/kernel.py:13-332``):
+
+* parameters annotated ``eas.constexpr`` are meta params (trace-time literals);
+* ``_sync``, ``_grid`` (int, tuple or ``callable(meta, runtime_args)``),
+  ``_tptg``, ``_shape`` and ``_nthreads`` are per-call launch options;
+* a specialisation is cached on ``(sorted meta, runtime-arg signature)``;
+  scalar argument *values* never trigger a recompile;
+* with an ``@eas.autotune`` spec every config is benchmarked once per key.
+"""
+
+from __future__ import annotations
+
+import inspect
+from typing import Any, Callable, Mapping
+
+from .autotune import AutotuneSpec, Config
+from .compiler import CompiledKernel, compile as _compile, runtime_arg_signature
+from .meta import constexpr
+from .runtime import get_runtime
+
+_OPTION_NAMES = ("_sync", "_shape", "_grid", "_tptg", "_nthreads")
+
+
+def _dims(value: Any, what: str, *, lo: int, max_dims: int, pad: bool) -> tuple[int, ...]:
+    if isinstance(value, int):
+        dims = [int(value)]
+    elif isinstance(value, (tuple, list)):
+        dims = [int(x) for x in value]
+    else:
+        kinds = "int/tuple/list or callable" if what == "_grid" else "int or tuple/list of ints"
+        raise TypeError(f"{what} must be {kinds}, got {type(value)!r}")
+    if not 1 <= len(dims) <= max_dims:
+        raise ValueError(f"{what} must have 1..{max_dims} dims" if max_dims == 3 else f"{what} must have >= 1 dim")
+    if any(d < lo for d in dims):
+        raise ValueError(f"{what} dims must be {'> 0' if lo == 1 else '>= 0'}")
+    if pad:
+        dims += [1] * (3 - len(dims))
+    return tuple(dims)
+
+
+class Kernel:
+    def __init__(self, fn: Callable[..., Any]):
+        self.fn = fn
+        self.name = fn.__name__
+        self.sig = inspect.signature(fn)
+        annotations = inspect.get_annotations(fn, eval_str=True)
+        self.meta_params = {
+            name for name, p in self.sig.parameters.items() if annotations.get(name, p.annotation) is constexpr
+        }
+        self._cache: dict[tuple[Any, Any], CompiledKernel] = {}
+        self._autotune_spec: AutotuneSpec | None = None
+        self._tuned_cache: dict[tuple[Any, ...], Config] = {}
+
+    def _set_autotune_spec(self, spec: AutotuneSpec) -> None:
+        self._autotune_spec = spec
+
+    # -- options ----------------------------------------------------------------
+    @staticmethod
+    def _extract_runtime_options(kwargs: dict[str, Any]) -> dict[str, Any]:
+        """Pop the ``_``-prefixed launch options out of the call's kwargs."""
+        sync = kwargs.pop("_sync", True)
+        if not isinstance(sync, bool):
+            raise TypeError(f"_sync must be bool, got {type(sync)!r}")
+        nthreads = kwargs.pop("_nthreads", None)
+        if nthreads is not None:
+            try:
+                nthreads = int(nthreads)
+            except Exception as e:
+                raise TypeError(f"_nthreads must be an int-like value, got {type(nthreads)!r}") from e
+            if nthreads < 0:
+                raise ValueError("_nthreads must be >= 0")
+        return {
+            "sync": sync,
+            "nthreads": nthreads,
+            "grid": kwargs.pop("_grid", None),
+            "shape": kwargs.pop("_shape", None),
+            "tptg": kwargs.pop("_tptg", None),
+        }
+
+    @staticmethod
+    def _normalize_runtime_options(raw: dict[str, Any], meta: dict[str, Any], runtime_args: dict[str, Any]) -> dict[str, Any]:
+        """Validate options and bring grid/tptg to 3-tuples (a callable grid is evaluated)."""
+        shape = raw.get("shape")
+        grid = raw.get("grid")
+        if callable(grid):
+            grid = grid(meta, runtime_args)
+        tptg = raw.get("tptg")
+        return {
+            "sync": bool(raw["sync"]),
+            "nthreads": raw["nthreads"],
+            "grid": None if grid is None else _dims(grid, "_grid", lo=0, max_dims=3, pad=True),
+            "shape": None if shape is None else _dims(shape, "_shape", lo=0, max_dims=1 << 30, pad=False),
+            "tptg": None if tptg is None else _dims(tptg, "_tptg", lo=1, max_dims=3, pad=True),
+        }
+
+    @staticmethod
+    def _check_tptg(ck: CompiledKernel, tptg: tuple[int, ...] | None) -> None:
+        """``_tptg`` must equal the threadgroup shape the kernel was compiled for."""
+        if tptg is None:
+            return
+        expected = (int(ck.block_size), 1, 1) if ck.launch_mode == "thread" else (1, 1, 1)
+        if tuple(int(x) for x in tptg) != expected:
+            raise ValueError(f"_tptg must match kernel launch mode: expected {expected}, got {tuple(tptg)}")
+
+    # -- binding / specialisation --------------------------------------------------
+    def _bind_and_split(self, /, *args: Any, **kwargs: Any) -> tuple[dict[str, Any], dict[str, Any]]:
+        bound = self.sig.bind(*args, **kwargs)
+        bound.apply_defaults()
+        meta = {k: bound.arguments.pop(k) for k in list(bound.arguments) if k in self.meta_params}
+        return meta, dict(bound.arguments)
+
+    def _compile_from_split(self, meta: dict[str, Any], runtime_args: dict[str, Any]) -> CompiledKernel:
+        key = (tuple(sorted(meta.items())), runtime_arg_signature(runtime_args))
+        ck = self._cache.get(key)
+        if ck is None:
+            ck = _compile(self.fn, runtime_args, meta)
+            self._cache[key] = ck
+        return ck
+
+    # -- autotune ------------------------------------------------------------------
+    @staticmethod
+    def _autotune_key(spec: AutotuneSpec, meta: Mapping[str, Any], runtime_args: Mapping[str, Any]) -> tuple[Any, ...]:
+        def norm(v: Any) -> Any:
+            if isinstance(v, (bool, int, float, str, type(None))):
+                return v
+            if isinstance(v, (tuple, list)):
+                return tuple(norm(x) for x in v)
+            if isinstance(v, dict):
+                return tuple(sorted((str(k), norm(x)) for k, x in v.items()))
+            for cast in (int, float):
+                try:
+                    return cast(v)
+                except Exception:
+                    pass
+            shape = getattr(v, "shape", None)
+            if shape is not None:
+                try:
+                    return ("shape", tuple(int(d) for d in shape))
+                except Exception:
+                    pass
+            raise TypeError(f"autotune key value must be hashable/normalizable, got {type(v)!r}")
+
+        key = []
+        for name in spec.key:
+            if name in meta:
+                key.append(norm(meta[name]))
+            elif name in runtime_args:
+                key.append(norm(runtime_args[name]))
+            else:
+                raise KeyError(f"autotune key {name!r} not found in args/meta")
+        return tuple(key)
+
+    def _autotune_select(self, spec: AutotuneSpec, meta: dict[str, Any], runtime_args: dict[str, Any],
+                         raw_opts: dict[str, Any]) -> tuple[dict[str, Any], dict[str, Any]]:
+        key = self._autotune_key(spec, meta, runtime_args)
+        best = self._tuned_cache.get(key)
+        if best is None:
+            bench = getattr(get_runtime(), "benchmark", None)
+            if not callable(bench):
+                raise RuntimeError("autotune requires a runtime with benchmark(); use the HIP runtime (EAS_BACKEND=auto|hip)")
+            best_t: float | None = None
+            for cfg in spec.configs:
+                m = {**meta, **dict(cfg.meta)}
+                opts = self._normalize_runtime_options(raw_opts, m, runtime_args)
+                ck = self._compile_from_split(m, runtime_args)
+                t = float(bench(ck, runtime_args, m, repeat=spec.repeat, warmup=spec.warmup,
+                                nthreads=opts["nthreads"], grid=opts["grid"], tptg=opts["tptg"], shape=opts["shape"]))
+                if best_t is None or t < best_t:
+                    best_t, best = t, cfg
+            assert best is not None
+            self._tuned_cache[key] = best
+        meta_best = {**meta, **dict(best.meta)}
+        return meta_best, self._normalize_runtime_options(raw_opts, meta_best, runtime_args)
+
+    # -- public ------------------------------------------------------------------
+    def _prepare(self, args: tuple[Any, ...], kwargs: dict[str, Any]) -> tuple[CompiledKernel, dict, dict, dict, dict]:
+        raw = self._extract_runtime_options(kwargs)
+        meta, runtime_args = self._bind_and_split(*args, **kwargs)
+        spec = self._autotune_spec
+        if spec is not None:
+            meta, opts = self._autotune_select(spec, meta, runtime_args, raw)
+        else:
+            opts = self._normalize_runtime_options(raw, meta, runtime_args)
+        ck = self._compile_from_split(meta, runtime_args)
+        if raw.get("tptg") is not None:
+            self._check_tptg(ck, opts["tptg"])
+        return ck, meta, runtime_args, opts, raw
+
+    def compile(self, /, *args: Any, **kwargs: Any) -> CompiledKernel:
+        return self._prepare(args, dict(kwargs))[0]
+
+    def __call__(self, /, *args: Any, **kwargs: Any) -> None:
+        ck, meta, runtime_args, opts, _ = self._prepare(args, dict(kwargs))
+        get_runtime().run(ck, runtime_args, meta, **opts)
+
+    def to_hip(self, /, *args: Any, **kwargs: Any) -> str:
+        """The generated gfx950 HIP C++ source for this specialisation (reference: ``to_msl``)."""
+        return self.compile(*args, **kwargs).src
+
+
+def kernel(fn: Callable[..., Any]) -> Kernel:
+    k = Kernel(fn)
+    spec = getattr(fn, "__eas_autotune_spec__", None)
+    if isinstance(spec, AutotuneSpec):
+        k._set_autotune_spec(spec)
+    return k

@@ -1,0 +1,363 @@
+"""``HipRuntime``: runs compiled eas kernels on an MI355X through ``easy_as_amd._hip``.
+
+Replaces the reference's ``MetalRuntime`` (``eas/runtime/metal.py``):
+
+* ``run`` maps the reference launch (programs for SPMD kernels, threadgroups or
+  a 1-D thread count for thread kernels; ``metal.py:244-352``) onto HIP
+  workgroups using the kernel's :class:`~easy_as_amd.codegen.hip.Geometry`,
+  packs the arguments (``metal.py:142-242``) and launches;
+* code objects are compiled once per source with hiprtc for gfx950 and cached
+  in memory and on disk;
+* ``benchmark`` times ``repeat`` launches between HIP events (the reference
+  wall-clocks one command buffer, ``metal.py:362-506``).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import os
+import struct
+import weakref
+from collections import deque
+from pathlib import Path
+from typing import Any, Mapping
+
+import numpy as np
+
+from ..ir import DType, IRModule
+from .grid import infer_grid, infer_nthreads
+from .hip_ext import load_hip_ext
+
+TARGET_ARCH = "gfx950"
+
+COMPILE_OPTIONS = (
+    f"--offload-arch={TARGET_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-ffp-contract=off",
+    # packed FP32 (v_pk_*_f32) is disabled for all HIP code of this project
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+)
+
+
+def _cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def pack_scalar(dtype: DType, value: Any) -> bytes:
+    """Kernel-argument bytes of a scalar (reference ``metal.py:28-38``)."""
+    if dtype == DType.U32:
+        v = int(value)
+        if not 0 <= v < (1 << 32):
+            raise OverflowError(f"u32 scalar out of range: {v}")
+        return struct.pack("<I", v)
+    if dtype == DType.F16:
+        return np.float16(value).tobytes()
+    if dtype == DType.F32:
+        return struct.pack("<f", float(value))
+    if dtype == DType.BOOL:
+        return struct.pack("<?", bool(value))
+    raise ValueError(f"unsupported scalar dtype: {dtype}")
+
+
+def _cache_dir() -> Path:
+    d = os.environ.get("EAS_HIP_CACHE_DIR")
+    return Path(d) if d else Path.home() / ".cache" / "easy_as_amd"
+
+
+def compile_code(mod: Any, src: str, entry: str, options: tuple[str, ...] = COMPILE_OPTIONS) -> bytes:
+    """hiprtc-compile ``src`` to a gfx950 code object, through the on-disk cache."""
+    key = hashlib.sha256("\0".join((src, entry, *options, str(getattr(mod, "ABI_VERSION", 0)))).encode()).hexdigest()
+    path = _cache_dir() / f"{key}.co"
+    if os.environ.get("EAS_HIP_DISABLE_CACHE", "") not in ("", "0") or not path.exists():
+        code = mod.compile_to_code(src, f"{entry}.hip", list(options))
+        try:
+            path.parent.mkdir(parents=True, exist_ok=True)
+            tmp = path.with_suffix(f".{os.getpid()}.tmp")
+            tmp.write_bytes(code)
+            os.replace(tmp, path)
+        except OSError:
+            pass
+        return code
+    return path.read_bytes()
+
+
+class LaunchPlan:
+    """A concrete HIP dispatch: workgroup grid, block and hidden u32 arguments."""
+
+    __slots__ = ("grid", "block", "hidden")
+
+    def __init__(self, grid: tuple[int, int, int], block: tuple[int, int, int], hidden: tuple[int, ...]) -> None:
+        self.grid = grid
+        self.block = block
+        self.hidden = hidden
+
+
+def plan_launch(
+    ck: Any,
+    runtime_args: Mapping[str, Any],
+    *,
+    nthreads: int | None = None,
+    grid: tuple[int, int, int] | None = None,
+    tptg: tuple[int, int, int] | None = None,
+    shape: tuple[int, ...] | None = None,
+) -> LaunchPlan | None:
+    """Reference launch semantics -> HIP dispatch (``None`` when nothing runs).
+
+    Reference rules (``metal.py:256-326``): ``_tptg`` must equal (BLOCK,1,1) in
+    thread mode and (1,1,1) in SPMD; without ``_grid`` a 2-D/3-D grid is
+    inferred from ``_shape``/H/W/D, else a 1-D extent from ``_nthreads``/N
+    (thread mode: that many threads; SPMD: ceil(N/BLOCK) programs); any zero
+    extent launches nothing.
+    """
+    ir: IRModule = ck.ir
+    block = int(ck.block_size)
+    mode = str(ck.launch_mode)
+    expected = (block, 1, 1) if mode == "thread" else (1, 1, 1)
+    if tptg is not None and tuple(int(x) for x in tptg) != expected:
+        raise ValueError(f"tptg must match kernel launch mode: expected {expected}, got {tuple(tptg)}")
+    live_x: int | None = None
+    if grid is None:
+        inferred = infer_grid(ir, runtime_args, block, shape=shape)
+        if inferred is None:
+            n = infer_nthreads(runtime_args, nthreads=nthreads)
+            if n == 0:
+                return None
+            groups = (_cdiv(n, block), 1, 1)
+            live_x = n if mode == "thread" else None
+        else:
+            groups = tuple(int(g) for g in inferred)  # type: ignore[assignment]
+    else:
+        groups = tuple(int(g) for g in grid)  # type: ignore[assignment]
+        if any(g < 0 for g in groups):
+            raise ValueError("grid dims must be >= 0")
+    if any(g == 0 for g in groups):
+        return None
+    geo = ck.geometry
+    if geo.kind == "spmd":
+        per_wg = geo.programs_per_wg * geo.unroll
+        return LaunchPlan((_cdiv(groups[0], per_wg), groups[1], groups[2]), (geo.wg_size, 1, 1), (groups[0],))
+    if geo.kind == "thread":
+        live = live_x if live_x is not None else groups[0] * block
+        return LaunchPlan(groups, (block, 1, 1), (live,))  # type: ignore[arg-type]
+    if geo.kind == "gemm":
+        from ..codegen.gemm_lift import plan_gemm
+
+        return plan_gemm(geo, groups, runtime_args, live_x)
+    raise ValueError(f"unknown kernel geometry: {geo.kind!r}")
+
+
+def _is_eas_tensor(v: Any) -> bool:
+    return bool(getattr(v, "__eas_tensor__", False))
+
+
+class HipRuntime:
+    """Process-wide HIP runtime (one per process, like the reference's MetalRuntime)."""
+
+    def __init__(self, ext: Any | None = None) -> None:
+        self._hip = ext
+        self._available: bool | None = None if ext is None else True
+        self._kernels: dict[tuple[str, str], Any] = {}
+        self._pending: deque[Any] = deque()
+        self._max_in_flight: int | None = None
+        self._ptr_cache: dict[int, tuple[weakref.ref, Any]] = {}
+        self._torch: Any = None
+        self._torch_probed = False
+        self._arch_checked = ext is not None
+
+    # -- plumbing ------------------------------------------------------------
+    def is_available(self) -> bool:
+        if self._available is None:
+            mod = load_hip_ext(require=False)
+            try:
+                self._available = bool(mod is not None and mod.is_available())
+            except Exception:
+                self._available = False
+        return bool(self._available)
+
+    def _mod(self) -> Any:
+        if self._hip is None:
+            self._hip = load_hip_ext(require=True)
+        if not self._arch_checked:
+            arch = self._hip.device_props()["arch"]
+            if arch != TARGET_ARCH:
+                raise RuntimeError(f"this backend targets {TARGET_ARCH} (MI355X); the current device is {arch}")
+            self._arch_checked = True
+        return self._hip
+
+    def _torch_mod(self) -> Any:
+        if not self._torch_probed:
+            self._torch_probed = True
+            try:
+                import torch  # type: ignore
+
+                self._torch = torch
+            except Exception:
+                self._torch = None
+        return self._torch
+
+    def _max_pending(self) -> int:
+        if self._max_in_flight is None:
+            try:
+                self._max_in_flight = max(0, int(os.environ.get("EAS_MAX_IN_FLIGHT", "256").strip() or 256))
+            except ValueError:
+                self._max_in_flight = 256
+        return self._max_in_flight
+
+    def kernel_handle(self, ck: Any) -> Any:
+        """Loaded kernel for ``ck`` (compiled once per source; disk-cached)."""
+        entry = ck.geometry.entry if ck.geometry is not None else ck.ir.name
+        key = (ck.src, entry)
+        k = self._kernels.get(key)
+        if k is None:
+            mod = self._mod()
+            if callable(getattr(mod, "compile_to_code", None)) and callable(getattr(mod, "load", None)):
+                k = mod.load(compile_code(mod, ck.src, entry), entry)
+            else:
+                k = mod.compile(ck.src, entry)
+            self._kernels[key] = k
+        return k
+
+    # -- arguments ---------------------------------------------------------------
+    def _torch_pointer(self, t: Any) -> Any:
+        key = id(t)
+        hit = self._ptr_cache.get(key)
+        if hit is not None and hit[0]() is t:
+            return hit[1]
+        buf = self._mod().wrap_pointer(int(t.data_ptr()), int(t.numel() * t.element_size()), t)
+        try:
+            weakref.finalize(t, self._ptr_cache.pop, key, None)
+            self._ptr_cache[key] = (weakref.ref(t), buf)
+        except TypeError:
+            pass
+        return buf
+
+    def build_argv(self, ir: IRModule, runtime_args: Mapping[str, Any], writes: frozenset[str]) -> tuple[list, list, list, Any]:
+        """Argument list for ``_hip.launch`` plus host copy-backs and the stream to use."""
+        mod = self._mod()
+        torch = self._torch_mod()
+        argv: list[Any] = []
+        writable: list[bool] = []
+        copy_back: list[tuple[Any, np.ndarray]] = []
+        staged: dict[int, Any] = {}
+        stream = None
+        for arg in ir.args:
+            v = runtime_args[arg.name]
+            if arg.kind == "scalar":
+                argv.append(pack_scalar(arg.dtype, v))
+                writable.append(False)
+                continue
+            want = np.float16 if arg.dtype == DType.F16 else np.float32
+            w = arg.name in writes
+            if torch is not None and isinstance(v, torch.Tensor):
+                t = v.detach()
+                if t.dtype != (torch.float16 if arg.dtype == DType.F16 else torch.float32):
+                    raise TypeError(f"{arg.name!r} must be {np.dtype(want).name}, got {t.dtype}")
+                if t.device.type == "cuda":
+                    if not t.is_contiguous():
+                        raise ValueError(f"{arg.name!r} must be contiguous")
+                    argv.append(self._torch_pointer(t))
+                    writable.append(w)
+                    stream = torch.cuda.current_stream(t.device).cuda_stream
+                    continue
+                if t.device.type != "cpu":
+                    raise TypeError(f"unsupported torch device for {arg.name!r}: {t.device}")
+                v = t.contiguous().numpy()
+            if _is_eas_tensor(v):
+                if v.device == "hip":
+                    if np.dtype(v.dtype) != np.dtype(want):
+                        raise TypeError(f"{arg.name!r} dtype mismatch: expected {np.dtype(want)}, got {v.dtype}")
+                    argv.append(v._hip_buffer())
+                    writable.append(w)
+                    continue
+                v = v.numpy()
+            if isinstance(v, np.ndarray):
+                if v.dtype != want:
+                    raise TypeError(f"{arg.name!r} must be {np.dtype(want).name}, got {v.dtype}")
+                if not v.flags.c_contiguous:
+                    raise ValueError(f"{arg.name!r} must be C-contiguous")
+                buf = staged.get(id(v))
+                if buf is None:
+                    buf = mod.alloc_buffer(max(int(v.nbytes), 1), "private")
+                    if v.nbytes:
+                        mod.copy_from_host(buf, v)
+                    staged[id(v)] = buf
+                    if w and v.nbytes:
+                        copy_back.append((buf, v))
+                argv.append(buf)
+                writable.append(w)
+                continue
+            raise TypeError(f"expected numpy.ndarray, eas.Tensor or torch.Tensor for {arg.name!r}, got {type(v)!r}")
+        return argv, writable, copy_back, stream
+
+    # -- launching ------------------------------------------------------------------
+    def run(
+        self,
+        ck: Any,
+        runtime_args: Mapping[str, Any],
+        meta: Mapping[str, Any],
+        *,
+        sync: bool = True,
+        nthreads: int | None = None,
+        grid: tuple[int, int, int] | None = None,
+        tptg: tuple[int, int, int] | None = None,
+        shape: tuple[int, ...] | None = None,
+    ) -> None:
+        _ = meta
+        plan = plan_launch(ck, runtime_args, nthreads=nthreads, grid=grid, tptg=tptg, shape=shape)
+        if plan is None:
+            return
+        argv, writable, copy_back, stream = self.build_argv(ck.ir, runtime_args, ck.writes)
+        argv += [struct.pack("<I", h) for h in plan.hidden]
+        writable += [False] * len(plan.hidden)
+        mod = self._mod()
+        kernel = self.kernel_handle(ck)
+        if sync or copy_back:
+            mod.launch(kernel, argv, writable, plan.grid, plan.block, stream=stream)
+            for buf, arr in copy_back:
+                mod.copy_to_host(buf, arr)
+            return
+        self._pending.append(mod.launch_async(kernel, argv, writable, plan.grid, plan.block, stream=stream))
+        limit = self._max_pending()
+        while limit and len(self._pending) > limit:
+            mod.synchronize(self._pending.popleft())
+
+    def synchronize(self) -> None:
+        mod = self._hip
+        while self._pending:
+            mod.synchronize(self._pending.popleft())
+
+    def benchmark(
+        self,
+        ck: Any,
+        runtime_args: Mapping[str, Any],
+        meta: Mapping[str, Any],
+        *,
+        repeat: int,
+        warmup: int = 0,
+        nthreads: int | None = None,
+        grid: tuple[int, int, int] | None = None,
+        tptg: tuple[int, int, int] | None = None,
+        shape: tuple[int, ...] | None = None,
+        **_: Any,
+    ) -> float:
+        """Seconds per launch: ``warmup`` untimed launches, then ``repeat`` launches
+        between HIP events on the launch stream."""
+        _ = meta
+        if repeat <= 0:
+            raise ValueError("repeat must be > 0")
+        if warmup < 0:
+            raise ValueError("warmup must be >= 0")
+        self.synchronize()
+        plan = plan_launch(ck, runtime_args, nthreads=nthreads, grid=grid, tptg=tptg, shape=shape)
+        if plan is None:
+            return 0.0
+        argv, writable, copy_back, stream = self.build_argv(ck.ir, runtime_args, ck.writes)
+        if copy_back:
+            raise ValueError("benchmark() with numpy outputs is not supported; use eas.Tensor(device='hip') or "
+                             "torch GPU tensors for device-resident timing")
+        argv += [struct.pack("<I", h) for h in plan.hidden]
+        writable += [False] * len(plan.hidden)
+        ms = self._mod().launch_timed(self.kernel_handle(ck), argv, writable, plan.grid, plan.block,
+                                      repeat=int(repeat), warmup=int(warmup), stream=stream)
+        return float(ms) * 1e-3

@@ -1,0 +1,117 @@
+"""Oracle arithmetic: closed forms the eas hot path must reproduce.
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` as the checker; the product
+(``easy_as_amd``) never imports anything under ``oracle/``.
+
+* ``add_f32``      — binary32 RNE addition (examples/add.py:23-31).
+* ``fmaf``         — correctly rounded f32 fused multiply-add, via the C
+                     restatement ``oracle/fmaf.c`` (glibc ``fmaf``);
+                     the fused op comes from eas/compiler.py:1019-1096.
+* ``fmaf_rto``     — an independent numpy implementation of the same function
+                     (exact product in binary64, TwoSum, round-to-odd, then one
+                     RNE rounding to binary32: Boldo & Melquiond, "Emulation of
+                     FMA and correctly rounded sums: proved algorithms using
+                     rounding to odd", IEEE TC 2008).  Used only to pin
+                     ``fmaf``; the two must agree bit for bit.
+* ``matmul_ref``   — float64 matmul reference (tests/test_matmul.py:55).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "liboracle.so"
+
+_lib: ctypes.CDLL | None = None
+
+
+def build() -> Path:
+    """Compile oracle/fmaf.c (gcc) into oracle/_build/liboracle.so."""
+    subprocess.run(["make", "-C", str(HERE)], check=True, stdout=subprocess.DEVNULL)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        fp = ctypes.POINTER(ctypes.c_float)
+        L.eas_oracle_add_f32.argtypes = [fp, fp, fp, ctypes.c_size_t]
+        L.eas_oracle_fmaf.argtypes = [fp, fp, fp, fp, ctypes.c_size_t]
+        L.eas_oracle_dot_f32.argtypes = [fp, ctypes.c_size_t, fp, ctypes.c_size_t, ctypes.c_size_t]
+        L.eas_oracle_dot_f32.restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+def _f32(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def _ptr(x: np.ndarray) -> ctypes._Pointer:
+    return x.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def add_f32(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a, b = np.broadcast_arrays(_f32(a), _f32(b))
+    a, b = _f32(a), _f32(b)
+    out = np.empty_like(a)
+    lib().eas_oracle_add_f32(_ptr(a), _ptr(b), _ptr(out), a.size)
+    return out
+
+
+def fmaf(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """Correctly rounded ``a*b+c`` in binary32 (C fmaf), broadcasting numpy-style."""
+    a, b, c = np.broadcast_arrays(_f32(a), _f32(b), _f32(c))
+    a, b, c = _f32(a), _f32(b), _f32(c)
+    out = np.empty_like(a)
+    lib().eas_oracle_fmaf(_ptr(a), _ptr(b), _ptr(c), _ptr(out), a.size)
+    return out
+
+
+def fmaf_rto(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """Correctly rounded binary32 fma without an fma instruction (see module doc)."""
+    a64 = np.asarray(a, np.float32).astype(np.float64)
+    b64 = np.asarray(b, np.float32).astype(np.float64)
+    c64 = np.asarray(c, np.float32).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        p = a64 * b64  # exact: 24+24 significant bits fit in 53
+        s = p + c64
+        # TwoSum: e = (p + c) - s exactly
+        bb = s - p
+        e = (p - (s - bb)) + (c64 - bb)
+        finite = np.isfinite(s) & np.isfinite(e)
+        bits = s.view(np.int64)
+        inexact = finite & (e != 0)
+        even = (bits & 1) == 0
+        # round to odd: an inexact result with an even last bit moves one ulp toward the exact value
+        fix = inexact & even
+        toward = np.where(e > 0, np.inf, -np.inf)
+        s = np.where(fix, np.nextafter(s, toward), s)
+    return s.astype(np.float32)
+
+
+def dot_f32(a: np.ndarray, b: np.ndarray) -> np.float32:
+    """One dot product with the reference's accumulation order (fma per k, k ascending)."""
+    a, b = _f32(a), _f32(b)
+    return np.float32(lib().eas_oracle_dot_f32(_ptr(a), 1, _ptr(b), 1, a.size))
+
+
+def matmul_ref(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """float64 matmul of the given (already rounded) operands."""
+    return np.asarray(a, np.float64) @ np.asarray(b, np.float64)
+
+
+def rel_err(c: np.ndarray, ref: np.ndarray) -> float:
+    """``max|C - R| / max|R|`` — the matmul parity metric."""
+    ref = np.asarray(ref, np.float64)
+    denom = float(np.max(np.abs(ref))) or 1.0
+    return float(np.max(np.abs(np.asarray(c, np.float64) - ref))) / denom

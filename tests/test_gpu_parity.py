@@ -1,0 +1,312 @@
+"""GPU parity: the HIP path against the oracle on seeded inputs.
+
+Bit-exact for f32 add / fma and integer index work; matmul within
+``max|C-R|/max|R| <= 1e-5*sqrt(K)`` (f32) and ``<= 2e-2`` (f16 inputs, f32
+accumulate).  Counterparts of the reference's device tests (test_add.py,
+test_fma.py, test_matmul*.py, test_threadgroup_memory.py, test_local_and_lane_id.py,
+test_callable_grid.py, test_tptg_override.py, test_grid_infer.py,
+test_dot_dynamic_k.py, test_kernel_cache.py, test_tensor.py, test_torch_interop.py).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import eas
+import kernels as K
+from conftest import seeded_normal
+from oracle import interp, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits_equal(x: np.ndarray, y: np.ndarray) -> bool:
+    x, y = np.asarray(x), np.asarray(y)
+    return x.shape == y.shape and x.dtype == y.dtype and np.array_equal(x.view(np.uint8), y.view(np.uint8))
+
+
+# -- elementwise ------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("n", [1, 255, 1031, 4099, 1 << 20])
+@pytest.mark.parametrize("block", [256, 1024])
+def test_add_numpy_bit_exact(gpu_runtime, n, block):
+    a, b = seeded_normal(0, n), seeded_normal(1, n)
+    c = np.full(n, np.nan, np.float32)
+    K.add_kernel(a, b, c, n, BLOCK=block)
+    assert _bits_equal(c, ops.add_f32(a, b))
+
+
+def test_add_golden_fixture(gpu_runtime):
+    from pathlib import Path
+
+    g = np.load(Path(__file__).parent / "golden" / "add_f32_n1031.npz")
+    c = np.zeros_like(g["a"])
+    K.add_kernel(g["a"], g["b"], c, int(g["a"].size), BLOCK=256)
+    assert _bits_equal(c, g["c"])
+
+
+def test_add_masked_tail_leaves_rest_untouched(gpu_runtime):
+    n, cap = 1031, 2048
+    a, b = seeded_normal(0, cap), seeded_normal(1, cap)
+    c = np.full(cap, 7.0, np.float32)
+    K.add_kernel(a, b, c, n, BLOCK=256)
+    assert _bits_equal(c[:n], ops.add_f32(a[:n], b[:n]))
+    assert np.all(c[n:] == 7.0)
+
+
+def test_add_f16_bit_exact(gpu_runtime):
+    n = 4099
+    a, b = seeded_normal(0, n, np.float16), seeded_normal(1, n, np.float16)
+    c = np.zeros(n, np.float16)
+    K.add_kernel(a, b, c, n, BLOCK=256)
+    assert _bits_equal(c, (a.astype(np.float32) + b.astype(np.float32)).astype(np.float16))
+
+
+def test_add_device_tensors_and_unaligned_view(gpu_runtime):
+    n = 4099
+    a_np, b_np = seeded_normal(0, n), seeded_normal(1, n)
+    a, b = eas.tensor(a_np, device="hip"), eas.tensor(b_np, device="hip")
+    c = eas.empty_like(a)
+    K.add_kernel(a, b, c, n, BLOCK=256)
+    assert _bits_equal(c.numpy(), ops.add_f32(a_np, b_np))
+
+
+@pytest.mark.parametrize("n", [1031, 1 << 20])
+def test_fma_spmd_bit_exact_vs_fmaf(gpu_runtime, n):
+    a, b, c = seeded_normal(0, n), seeded_normal(1, n), seeded_normal(2, n)
+    d = np.zeros(n, np.float32)
+    K.fma_kernel(a, b, c, d, n, BLOCK=256)
+    assert _bits_equal(d, ops.fmaf(a, b, c))
+
+
+def test_fma_thread_mode_and_explicit(gpu_runtime):
+    n = 1031
+    a, b, c = seeded_normal(0, n), seeded_normal(1, n), seeded_normal(2, n)
+    d = np.zeros(n, np.float32)
+    K.simple_fma_kernel(a, b, c, d, n, BLOCK=256)
+    assert _bits_equal(d, ops.fmaf(a, b, c))
+    d2 = np.zeros(n, np.float32)
+    K.explicit_fma_kernel(a, b, c, d2, n, BLOCK=256)
+    assert _bits_equal(d2, ops.fmaf(a, b, c))
+
+
+def test_fma_known_answer_differs_from_two_roundings(gpu_runtime):
+    # (1+2^-23)(1-2^-23) - 1 = -2^-46 exactly; mul-then-add gives 0.
+    e = np.float32(2.0 ** -23)
+    a = np.array([1 + e] * 4, np.float32)
+    b = np.array([1 - e] * 4, np.float32)
+    c = np.array([-1.0] * 4, np.float32)
+    d = np.zeros(4, np.float32)
+    K.fma_kernel(a, b, c, d, 4, BLOCK=256)
+    assert np.all(d == np.float32(-(2.0 ** -46)))
+
+
+def test_unfused_mul_add_rounds_twice(gpu_runtime):
+    n = 1031
+    a, b, c = seeded_normal(0, n), seeded_normal(1, n), seeded_normal(2, n)
+    d, e = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    K.multi_use_mul_kernel(a, b, c, d, e, n, BLOCK=128)
+    prod = (a * b).astype(np.float32)
+    assert _bits_equal(d, (prod + c).astype(np.float32))
+    assert _bits_equal(e, prod)
+
+
+def test_axpy_scalar_runtime_arg_and_cache(gpu_runtime):
+    n = 1031
+    a, b = seeded_normal(0, n), seeded_normal(1, n)
+    for alpha in (2.0, 3.5):
+        c = np.zeros(n, np.float32)
+        K.axpy_kernel(a, b, c, n, alpha, BLOCK=256)
+        assert _bits_equal(c, ops.fmaf(a, np.float32(alpha), b))
+
+
+def test_spmd_lanes_exchange_through_threadgroup_memory(gpu_runtime):
+    n = 1000
+    a = seeded_normal(0, n)
+    out = np.zeros(n, np.float32)
+    K.spmd_tg_rotate_kernel(a, out, n, BLOCK=256)
+    ref = interp.run_kernel(K.spmd_tg_rotate_kernel, a, np.zeros(n, np.float32), n, BLOCK=256)["out"]
+    assert _bits_equal(out, ref)
+
+
+def test_nontemporal_and_unrolled_spmd_variants(gpu_runtime, monkeypatch):
+    n = (1 << 16) + 5
+    a, b = seeded_normal(0, n), seeded_normal(1, n)
+    for env in ({"EAS_HIP_SPMD_NT": "1"}, {"EAS_HIP_SPMD_UNROLL": "4"}, {"EAS_HIP_SPMD_LPT": "16"}):
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        kern = eas.kernel(K.add_kernel.fn)
+        c = np.zeros(n, np.float32)
+        kern(a, b, c, n, BLOCK=1024)
+        assert _bits_equal(c, ops.add_f32(a, b)), env
+        for k in env:
+            monkeypatch.delenv(k)
+
+
+# -- thread mode / index known answers -----------------------------------------------
+
+
+def test_local_and_lane_and_sg_ids(gpu_runtime):
+    n = 128 * 3
+    out = np.zeros(n, np.float32)
+    K.local_id_kernel(out, n, BLOCK=128)
+    assert np.array_equal(out, (np.arange(n) % 128).astype(np.float32))
+    out = np.zeros(256, np.float32)
+    K.lane_id_kernel(out, 256, BLOCK=256)
+    assert np.array_equal(out, (np.arange(256) % 32).astype(np.float32))
+    out = np.zeros(256, np.float32)
+    K.sg_id_kernel(out, 256, BLOCK=256)
+    assert np.array_equal(out, (np.arange(256) // 32).astype(np.float32))
+
+
+def test_callable_grid(gpu_runtime):
+    h, w, block = 5, 10, 4
+    out = np.zeros(h * w, np.float32)
+    K.grid_callable_kernel(out, h, w, BLOCK=block, _grid=lambda meta, args: (K.cdiv(args["W"], meta["BLOCK"]), args["H"], 1))
+    assert np.array_equal(out.reshape(h, w), np.repeat(np.arange(h, dtype=np.float32), w).reshape(h, w))
+
+
+def test_tptg_must_match_and_arange(gpu_runtime):
+    n = 1024 + 7
+    out = np.zeros(n, np.float32)
+    with pytest.raises(ValueError):
+        K.tptg_independent_kernel(out, n, BLOCK=256, _tptg=64)
+    with pytest.raises(ValueError):
+        K.tptg_independent_kernel(out, n, BLOCK=256, _tptg=(128, 1, 1))
+    K.tptg_independent_kernel(out, n, BLOCK=256, _tptg=(256, 1, 1))
+    assert np.array_equal(out, np.arange(n, dtype=np.float32))
+
+
+def test_threadgroup_copy_exact(gpu_runtime):
+    n = 4096 + 7
+    a = seeded_normal(0, n)
+    out = np.zeros(n, np.float32)
+    K.tg_copy_kernel(a, out, n, BLOCK=256)
+    assert _bits_equal(out, a)
+
+
+def test_grid_inferred_from_hw(gpu_runtime):
+    h, w = 11, 77
+    a, b = seeded_normal(0, h * w), seeded_normal(1, h * w)
+    c = eas.empty(h * w, device="hip")
+    K.add2d_hw_kernel(eas.tensor(a, device="hip"), eas.tensor(b, device="hip"), c, h, w, BLOCK=32)
+    assert _bits_equal(c.numpy(), ops.add_f32(a, b))
+
+
+@pytest.mark.parametrize("k", [7, 31, 64])
+def test_dot_dynamic_k_partial_workgroup(gpu_runtime, k):
+    m = 33
+    a2, x = seeded_normal(0, m * k).reshape(m, k), seeded_normal(1, k)
+    y = np.zeros(m, np.float32)
+    K.gemv_dot_kernel(a2.reshape(-1), x, y, m, k, m, BLOCK=64)
+    ref = np.array([ops.dot_f32(a2[r], x) for r in range(m)], np.float32)
+    assert _bits_equal(y, ref)
+
+
+def test_dot_f16_tn4(gpu_runtime):
+    kk, groups = 8, 16
+    a = seeded_normal(0, kk, np.float16)
+    b = seeded_normal(1, groups * 4 + kk, np.float16)
+    out = np.zeros(groups * 4, np.float32)
+    K.dot_f16_tn4_kernel(a, b, out, kk, BLOCK=128, _grid=(groups, 1, 1))
+    ref = interp.run_kernel(K.dot_f16_tn4_kernel, a, b, np.zeros(groups * 4, np.float32), kk, BLOCK=128, _grid=(groups, 1, 1))["out"]
+    assert _bits_equal(out, ref)
+
+
+# -- matmul ------------------------------------------------------------------------------
+
+
+def test_naive_matmul_bit_exact_vs_oracle(gpu_runtime):
+    m, n, k, block = 32, 100, 16, 64
+    a2, b2 = seeded_normal(0, m * k).reshape(m, k), seeded_normal(1, k * n).reshape(k, n)
+    c = np.zeros(m * n, np.float32)
+    K.matmul_kernel(a2.reshape(-1), b2.reshape(-1), c, m, n, BLOCK=block, K=k, _grid=(m, K.cdiv(n, block)))
+    ref = interp.run_kernel(K.matmul_kernel, a2.reshape(-1), b2.reshape(-1), np.zeros(m * n, np.float32), m, n,
+                            BLOCK=block, K=k, _grid=(m, K.cdiv(n, block)))["c"]
+    assert _bits_equal(c, ref)
+    assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
+
+
+@pytest.mark.parametrize("mnk", [(33, 65, 48), (64, 64, 32), (17, 130, 31)])
+def test_tiled_matmul_cases(gpu_runtime, mnk):
+    m, n, k = mnk
+    bm, bn, bk, nt = 16, 64, 16, 256
+    a2 = seeded_normal(0, m * k).reshape(m, k) / np.float32(math.sqrt(k))
+    b2 = seeded_normal(1, k * n).reshape(k, n)
+    c = np.zeros(m * n, np.float32)
+    K.matmul_tiled_kernel(a2.reshape(-1), b2.reshape(-1), c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
+                          _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
+    ref = interp.run_kernel(K.matmul_tiled_kernel, a2.reshape(-1), b2.reshape(-1), np.zeros(m * n, np.float32), m, n,
+                            0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt, _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1))["c"]
+    assert _bits_equal(c, ref)
+    assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
+
+
+@pytest.mark.parametrize("mnk", [(64, 64, 64), (40, 72, 24), (33, 17, 16)])
+def test_mma_matmul_small(gpu_runtime, mnk):
+    m, n, k = mnk
+    bm, bn, bk = 32, 32, 8
+    nt = (bm // 8) * (bn // 8) * 32
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, m * k).astype(np.float16)
+    b = rng.uniform(-1, 1, k * n).astype(np.float16)
+    c = np.zeros(m * n, np.float32)
+    K.matmul_mma_kernel(a, b, c, m, n, BM=bm, BN=bn, BK=bk, K=k, NT=nt, _grid=K.mma_grid, _tptg=(nt, 1, 1))
+    ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
+    assert ops.rel_err(c.reshape(m, n), ref) <= 2e-2
+    assert ops.rel_err(c.reshape(m, n), ref) <= 1e-5 * math.sqrt(k)  # f32 accumulation of exact products
+
+
+# -- interop ------------------------------------------------------------------------------
+
+
+def test_torch_rocm_tensors_zero_copy(gpu_runtime):
+    import torch
+
+    n = 4096 + 3
+    a = torch.randn(n, device="cuda", dtype=torch.float32)
+    b = torch.randn(n, device="cuda", dtype=torch.float32)
+    c = torch.empty_like(a)
+    K.add_kernel(a, b, c, n, BLOCK=256)
+    torch.cuda.synchronize()
+    assert _bits_equal(c.cpu().numpy(), ops.add_f32(a.cpu().numpy(), b.cpu().numpy()))
+
+
+def test_dlpack_roundtrip_with_torch(gpu_runtime):
+    import torch
+
+    x = torch.arange(1024, device="cuda", dtype=torch.float32)
+    t = eas.tensor(x, device="hip")
+    assert t.device == "hip" and t.shape == (1024,)
+    y = t.to_torch("hip")
+    assert y.device.type == "cuda" and torch.equal(y, x)
+    y.add_(1.0)  # shares memory with x
+    torch.cuda.synchronize()
+    assert float(x[5].item()) == 6.0
+    host = eas.tensor(np.ones(8, np.float16), device="hip").to("cpu")
+    assert host.dtype == np.float16 and np.all(host.numpy() == 1)
+
+
+def test_async_launches_and_synchronize(gpu_runtime):
+    n = 1 << 16
+    a, b = seeded_normal(0, n), seeded_normal(1, n)
+    ta, tb = eas.tensor(a, device="hip"), eas.tensor(b, device="hip")
+    outs = [eas.empty(n, device="hip") for _ in range(4)]
+    for o in outs:
+        K.add_kernel(ta, tb, o, n, BLOCK=256, _sync=False)
+    gpu_runtime.synchronize()
+    for o in outs:
+        assert _bits_equal(o.numpy(), ops.add_f32(a, b))
+
+
+def test_benchmark_returns_positive_seconds(gpu_runtime):
+    n = 1 << 20
+    a = eas.tensor(seeded_normal(0, n), device="hip")
+    c = eas.empty(n, device="hip")
+    ck = K.add_kernel.compile(a, a, c, n, BLOCK=256)
+    t = gpu_runtime.benchmark(ck, {"a": a, "b": a, "c": c, "N": n}, {"BLOCK": 256}, repeat=5, warmup=2)
+    assert 0.0 < t < 1.0
