@@ -7,17 +7,19 @@ resident in HBM.  A step is one launch over the whole array; W untimed steps,
 then exactly K steps between device synchronisations.
 
 Prints ONE JSON line: the driver's fields plus ``roofline`` (achieved HBM GB/s
-of the add kernel from HIP events on its launch stream, vs 8 TB/s) and
-``cpu_baseline`` (the oracle's C restatement of the same add, one core, on a
-bounded sample).  Secondary measurements (fma, other BLOCK) ride along under
-``extra``.
+of the kernel from HIP events on its launch stream, vs 8 TB/s) and
+``cpu_baseline`` (the oracle's C restatement of the same arithmetic, one core,
+on a bounded sample).  Secondary measurements ride along under ``extra``.
+
+``--workload copy|fma|read|write`` measures the other elementwise kernels the same way
+(``copy`` is the known-size kernel that calibrates HBM byte counters; ``read`` and
+``write`` measure one-direction HBM streaming on the same GPU).
 """
 
 from __future__ import annotations
 
 import argparse
 import json
-import os
 import sys
 import time
 from pathlib import Path
@@ -29,8 +31,17 @@ sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
-N_ADD = 1 << 28
+N_ELEM = 1 << 28
 PRIMARY_BLOCK = 256
+
+# name -> (kernel attribute in tests/kernels.py, input count, algorithmic bytes per element)
+WORKLOADS = {
+    "add": ("add_kernel", 2, 12),
+    "fma": ("fma_kernel", 3, 16),
+    "copy": ("copy_kernel", 1, 8),
+    "read": ("read_kernel", 1, 4),
+    "write": ("fill_kernel", 0, 4),
+}
 
 
 def _log(msg: str) -> None:
@@ -57,23 +68,40 @@ def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch) -> tuple[f
     return wall_ms, ev_ms
 
 
-def _cpu_baseline(seconds: float = 10.0) -> dict:
+def _cpu_baseline(workload: str, seconds: float = 10.0) -> dict:
     from oracle import ops
 
     n = 1 << 26
-    a, b = _inputs(n, (0, 1))
-    ops.add_f32(a[:1024], b[:1024])
+    a, b, c = _inputs(n, (0, 1, 2))
+    fn = {"add": lambda: ops.add_f32(a, b), "fma": lambda: ops.fmaf(a, b, c), "copy": lambda: a.copy(),
+          "read": lambda: float(a.sum()), "write": lambda: c.fill(1.0)}[workload]
+    per = WORKLOADS[workload][2]
+    fn()
     reps = 0
     t0 = time.perf_counter()
     while True:
-        ops.add_f32(a, b)
+        fn()
         reps += 1
         el = time.perf_counter() - t0
         if el >= seconds or reps >= 200:
             break
-    gbs = 12.0 * n * reps / el / 1e9
-    return {"value": round(gbs, 2), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle add_f32 (oracle/fmaf.c, gcc -O2, 1 thread) over N=2^26 float32, {reps} reps, {el:.1f} s"}
+    what = {"add": "add_f32", "fma": "fmaf", "copy": "numpy copy", "read": "numpy sum", "write": "numpy fill"}[workload]
+    return {"value": round(per * n * reps / el / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle {what} (oracle/fmaf.c, gcc -O2, 1 thread) over N=2^26 float32, {reps} reps, {el:.1f} s"}
+
+
+def _oracle_out(workload: str, hosts: list[np.ndarray]) -> np.ndarray:
+    from oracle import ops
+
+    if workload == "add":
+        return ops.add_f32(hosts[0], hosts[1])
+    if workload == "fma":
+        return ops.fmaf(hosts[0], hosts[1], hosts[2])
+    if workload == "read":
+        return np.zeros(N_ELEM, np.float32)
+    if workload == "write":
+        return np.ones(N_ELEM, np.float32)
+    return hosts[0]
 
 
 def main() -> int:
@@ -81,6 +109,8 @@ def main() -> int:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="add")
+    p.add_argument("--block", type=int, default=PRIMARY_BLOCK)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
     args = p.parse_args()
@@ -91,58 +121,68 @@ def main() -> int:
 
     import torch
 
-    import eas
     import kernels as K
     from easy_as_amd.runtime import get_runtime
-    from oracle import ops
 
     rt = get_runtime("hip")
     dev = torch.device("cuda:0")
-    _log(f"device {torch.cuda.get_device_name(0)}; generating inputs N=2^28")
-    a_h, b_h = _inputs(N_ADD, (0, 1))
-    a = torch.from_numpy(a_h).to(dev)
-    b = torch.from_numpy(b_h).to(dev)
-    c = torch.empty_like(a)
-    rargs = {"a": a, "b": b, "c": c, "N": N_ADD}
+    kname, nin, per_elem = WORKLOADS[args.workload]
+    kern = getattr(K, kname)
+    _log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}; generating inputs N=2^28")
+    hosts = _inputs(N_ELEM, tuple(range(nin)))
+    ins = [torch.from_numpy(h).to(dev) for h in hosts]
+    out = torch.zeros(N_ELEM, dtype=torch.float32, device=dev)
+    names = list(kern.sig.parameters)[: nin + 1]
+    rargs = dict(zip(names, ins + [out]))
+    rargs["N"] = N_ELEM
 
-    results = {}
-    for block in (256, 1024):
-        ck = K.add_kernel.compile(a, b, c, N_ADD, BLOCK=block)
+    def measure(block: int) -> tuple[float, float]:
+        ck = kern.compile(*ins, out, N_ELEM, BLOCK=block)
         wall_ms, ev_ms = _time_kernel(rt, ck, rargs, {"BLOCK": block}, args.steps, args.warmup, torch)
-        results[block] = (wall_ms, ev_ms)
-        _log(f"add BLOCK={block}: wall {wall_ms:.4f} ms/step, event {ev_ms:.4f} ms/launch, "
-             f"{12 * N_ADD / ev_ms / 1e6:.1f} GB/s")
+        _log(f"{args.workload} BLOCK={block}: wall {wall_ms:.4f} ms/step, event {ev_ms:.4f} ms/launch, "
+             f"{per_elem * N_ELEM / ev_ms / 1e6:.1f} GB/s")
+        return wall_ms, ev_ms
 
-    # parity of the measured output (last launch was BLOCK=1024; redo the primary config)
-    K.add_kernel(a, b, c, N_ADD, BLOCK=PRIMARY_BLOCK)
+    wall_ms, ev_ms = measure(args.block)
+    extra: dict = {}
+    if not args.no_extra and args.workload == "add":
+        other = 1024 if args.block != 1024 else 256
+        extra[f"add_block{other}_gbs"] = round(per_elem * N_ELEM / measure(other)[1] / 1e6, 1)
+
+    # parity of the measured configuration over every output element
+    kern(*ins, out, N_ELEM, BLOCK=args.block)
     torch.cuda.synchronize()
-    got = c.cpu().numpy()
-    exact = bool(np.array_equal(got.view(np.uint32), ops.add_f32(a_h, b_h).view(np.uint32)))
+    got = out.cpu().numpy()
+    exact = bool(np.array_equal(got.view(np.uint32), _oracle_out(args.workload, hosts).view(np.uint32)))
     _log(f"parity vs oracle over all 2^28 outputs: {'bit-exact' if exact else 'MISMATCH'}")
 
-    wall_ms, ev_ms = results[PRIMARY_BLOCK]
-    bytes_per_launch = 12 * N_ADD
-    value = bytes_per_launch / (wall_ms * 1e-3) / 1e9
-    achieved = bytes_per_launch / (ev_ms * 1e-3) / 1e9
-
-    extra: dict = {"add_block1024_gbs": round(12 * N_ADD / results[1024][1] / 1e6, 1)}
-    if not args.no_extra:
-        c_h = _inputs(N_ADD, (2,))[0]
-        cc = torch.from_numpy(c_h).to(dev)
-        d = torch.empty_like(a)
-        fargs = {"a": a, "b": b, "c": cc, "d": d, "N": N_ADD}
-        ckf = K.fma_kernel.compile(a, b, cc, d, N_ADD, BLOCK=PRIMARY_BLOCK)
-        fw, fe = _time_kernel(rt, ckf, fargs, {"BLOCK": PRIMARY_BLOCK}, args.steps, args.warmup, torch)
-        d_h = d.cpu().numpy()
-        fexact = bool(np.array_equal(d_h.view(np.uint32), ops.fmaf(a_h, b_h, c_h).view(np.uint32)))
-        extra["fma_n2e28"] = {"GB/s": round(16 * N_ADD / fe / 1e6, 1), "frac": round(16 * N_ADD / fe / 1e6 / HBM_PEAK_GBS, 4),
+    if not args.no_extra and args.workload == "add":
+        fh = _inputs(N_ELEM, (2,))[0]
+        cc = torch.from_numpy(fh).to(dev)
+        d = torch.empty_like(out)
+        fargs = {"a": ins[0], "b": ins[1], "c": cc, "d": d, "N": N_ELEM}
+        ckf = K.fma_kernel.compile(ins[0], ins[1], cc, d, N_ELEM, BLOCK=args.block)
+        _, fe = _time_kernel(rt, ckf, fargs, {"BLOCK": args.block}, args.steps, args.warmup, torch)
+        fexact = bool(np.array_equal(d.cpu().numpy().view(np.uint32),
+                                     _oracle_out("fma", [hosts[0], hosts[1], fh]).view(np.uint32)))
+        extra["fma_n2e28"] = {"GB/s": round(16 * N_ELEM / fe / 1e6, 1), "frac": round(16 * N_ELEM / fe / 1e6 / HBM_PEAK_GBS, 4),
                               "parity": "bit-exact vs fmaf" if fexact else "MISMATCH"}
-        _log(f"fma: event {fe:.4f} ms/launch, {16 * N_ADD / fe / 1e6:.1f} GB/s, parity {extra['fma_n2e28']['parity']}")
+        _log(f"fma: event {fe:.4f} ms/launch, {16 * N_ELEM / fe / 1e6:.1f} GB/s, parity {extra['fma_n2e28']['parity']}")
         del cc, d
 
-    cpu = None if args.no_cpu_baseline else _cpu_baseline()
+    bytes_per_launch = per_elem * N_ELEM
+    traffic = None
+    pmc = ROOT / "profiles" / f"{args.workload}_f32_n2e28.pmc.json"
+    if pmc.exists() and args.block == PRIMARY_BLOCK:
+        # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes,
+        # each scaled by the reading of a known-size copy (see that file).
+        traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
+    value = bytes_per_launch / (wall_ms * 1e-3) / 1e9
+    achieved = bytes_per_launch / (ev_ms * 1e-3) / 1e9
+    expr = {"add": "c=a+b", "fma": "d=a*b+c (fused, one rounding)", "copy": "c=a", "read": "read a",
+            "write": "c=1"}[args.workload]
     line = {
-        "metric": "fp32 add GB/s @N=2^28 (eas SPMD kernel, one MI355X)",
+        "metric": f"fp32 {args.workload} GB/s @N=2^28 (eas SPMD kernel, one MI355X)",
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -153,13 +193,14 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (N(0,1) float32, seeds 0/1)",
-        "config": {"workload": "fp32 add c=a+b via @eas.kernel SPMD (mk.arange, masked tail), N=2^28, BLOCK=256",
-                   "N": N_ADD, "BLOCK": PRIMARY_BLOCK, "parallelism": "single GPU"},
+        "data": f"synthetic (N(0,1) float32, seeds {list(range(nin))})",
+        "config": {"workload": f"fp32 {args.workload} {expr} via @eas.kernel SPMD (mk.arange, masked tail), "
+                               f"N=2^28, BLOCK={args.block}",
+                   "N": N_ELEM, "BLOCK": args.block, "parallelism": "single GPU"},
         "parity": "bit-exact vs oracle (all 2^28 outputs)" if exact else "MISMATCH",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
-        "cpu_baseline": cpu,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": None if args.no_cpu_baseline else _cpu_baseline(args.workload),
         "extra": extra,
     }
     print(json.dumps(line), flush=True)

@@ -101,6 +101,7 @@ def plan_launch(
     grid: tuple[int, int, int] | None = None,
     tptg: tuple[int, int, int] | None = None,
     shape: tuple[int, ...] | None = None,
+    compute_units: int = 256,
 ) -> LaunchPlan | None:
     """Reference launch semantics -> HIP dispatch (``None`` when nothing runs).
 
@@ -136,7 +137,11 @@ def plan_launch(
     geo = ck.geometry
     if geo.kind == "spmd":
         per_wg = geo.programs_per_wg * geo.unroll
-        return LaunchPlan((_cdiv(groups[0], per_wg), groups[1], groups[2]), (geo.wg_size, 1, 1), (groups[0],))
+        nblocks = _cdiv(groups[0], per_wg)
+        persist = int(geo.params.get("persistent_wg_per_cu", 0) or 0)
+        if persist:
+            nblocks = min(nblocks, persist * compute_units)
+        return LaunchPlan((nblocks, groups[1], groups[2]), (geo.wg_size, 1, 1), (groups[0],))
     if geo.kind == "thread":
         live = live_x if live_x is not None else groups[0] * block
         return LaunchPlan(groups, (block, 1, 1), (live,))  # type: ignore[arg-type]
@@ -164,6 +169,7 @@ class HipRuntime:
         self._torch: Any = None
         self._torch_probed = False
         self._arch_checked = ext is not None
+        self._cus = 256
 
     # -- plumbing ------------------------------------------------------------
     def is_available(self) -> bool:
@@ -179,9 +185,10 @@ class HipRuntime:
         if self._hip is None:
             self._hip = load_hip_ext(require=True)
         if not self._arch_checked:
-            arch = self._hip.device_props()["arch"]
-            if arch != TARGET_ARCH:
-                raise RuntimeError(f"this backend targets {TARGET_ARCH} (MI355X); the current device is {arch}")
+            props = self._hip.device_props()
+            if props["arch"] != TARGET_ARCH:
+                raise RuntimeError(f"this backend targets {TARGET_ARCH} (MI355X); the current device is {props['arch']}")
+            self._cus = int(props["compute_units"])
             self._arch_checked = True
         return self._hip
 
@@ -304,7 +311,9 @@ class HipRuntime:
         shape: tuple[int, ...] | None = None,
     ) -> None:
         _ = meta
-        plan = plan_launch(ck, runtime_args, nthreads=nthreads, grid=grid, tptg=tptg, shape=shape)
+        self._mod()
+        plan = plan_launch(ck, runtime_args, nthreads=nthreads, grid=grid, tptg=tptg, shape=shape,
+                           compute_units=self._cus)
         if plan is None:
             return
         argv, writable, copy_back, stream = self.build_argv(ck.ir, runtime_args, ck.writes)
@@ -349,7 +358,9 @@ class HipRuntime:
         if warmup < 0:
             raise ValueError("warmup must be >= 0")
         self.synchronize()
-        plan = plan_launch(ck, runtime_args, nthreads=nthreads, grid=grid, tptg=tptg, shape=shape)
+        self._mod()
+        plan = plan_launch(ck, runtime_args, nthreads=nthreads, grid=grid, tptg=tptg, shape=shape,
+                           compute_units=self._cus)
         if plan is None:
             return 0.0
         argv, writable, copy_back, stream = self.build_argv(ck.ir, runtime_args, ck.writes)

@@ -31,6 +31,33 @@ def add_kernel(a, b, c, N, BLOCK: eas.constexpr):
 
 
 @eas.kernel
+def copy_kernel(a, c, N, BLOCK: eas.constexpr):
+    """c = a: a plain copy of known size, used to calibrate HBM byte counters."""
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.arange(0, BLOCK)
+    mask = offs < N
+    mk.store(c, offs, mk.load(a, offs, mask), mask)
+
+
+@eas.kernel
+def read_kernel(a, c, N, BLOCK: eas.constexpr):
+    """Reads a; writes c only where a < -3e38 (never for N(0,1) data): HBM read traffic alone."""
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.arange(0, BLOCK)
+    mask = offs < N
+    x = mk.load(a, offs, mask)
+    mk.store(c, offs, x, mask & (x < -3.0e38))
+
+
+@eas.kernel
+def fill_kernel(c, N, BLOCK: eas.constexpr):
+    """c = 1.0: HBM write traffic alone."""
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.arange(0, BLOCK)
+    mk.store(c, offs, 1.0, offs < N)
+
+
+@eas.kernel
 def fma_kernel(a, b, c, d, N, BLOCK: eas.constexpr):
     """d = a * b + c; the IR pass fuses it into one fma (single rounding)."""
     pid = mk.program_id(0)
