@@ -1,15 +1,764 @@
-"""Recognise tile-GEMM kernels in the IR and replace them with a tuned MFMA GEMM.
+"""Lift tile-GEMM kernels written with ``mk.mma`` to a tuned gfx950 MFMA GEMM.
 
-Placeholder: no kernel is lifted yet, every thread-mode kernel takes the
-literal lowering.
+The reference's simdgroup-MMA matmul (``examples/matmul_simdgroup.py:29-127``)
+computes one 8x8 fragment per 32-lane simdgroup with tiny tiles
+(``NT = (BM/8)(BN/8)*32 <= 1024``); lowered literally it cannot feed MI355X's
+matrix cores.  This module *proves* that a kernel's IR computes a dense GEMM and,
+only then, replaces it with a hand-written MFMA kernel (``v_mfma_f32_32x32x16_f16``,
+LDS-staged f16 tiles, B transposed in registers on its way into LDS).
+
+Proof method (no pattern matching on source text): the IR is executed
+symbolically for all NT threads of one threadgroup at once.  Thread ids are
+concrete; ``program_id`` values and u32 scalar arguments stay symbolic, so every
+index is a polynomial in those symbols with per-thread integer coefficients,
+and every mask is a concrete per-thread part plus affine atoms ``p < 0``.
+Threadgroup memory is tracked slot by slot (which load, for which thread, last
+wrote it).  At each ``mma`` the fragment slots are resolved to global loads and
+decoded into (row, k) / (k, col) positions; at the end every copied-out output
+element is matched to its fragment.  The kernel is lifted only if, for every
+output element of the threadgroup's tile,
+
+    C[row*ldc + col] = sum_{k in [0, K)} f16(A[row*K + k]) * f16(B[k*ldb + col])
+
+with rows/cols of the tile ``TM*pid_r + r`` / ``TN*pid_c + c`` (r < TM, c < TN),
+each k exactly once, A/B elements masked only by ``row < M`` / ``col < N`` and
+stores masked only by those, ``ldb == ldc`` the same scalar as the column bound.
+Anything else (other side effects, symbolic K, data-dependent indices, stale or
+uninitialised tile slots) leaves the kernel to the literal lowering.  The lifted
+kernel computes exactly the rectangle the launched grid covers, so partial grids
+(``_grid`` smaller than the matrix) keep their meaning; it needs M*K, K*N and
+M*N below 2^32 (the u32 index range the reference computes in).
 """
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Any
 
-from ..ir import IRModule
+import numpy as np
+
+from ..ir import DType, IRModule, Inst, ValueRef
+
+Mono = tuple[str, ...]
+
+
+class Unsupported(Exception):
+    """The kernel is not (provably) a dense tile GEMM."""
+
+
+# ---------------------------------------------------------------------------
+# symbolic integers: polynomials with per-thread coefficients
+# ---------------------------------------------------------------------------
+
+
+class Poly:
+    __slots__ = ("t",)
+
+    def __init__(self, terms: dict[Mono, np.ndarray]) -> None:
+        self.t = {m: c for m, c in terms.items() if np.any(c)}
+
+    @staticmethod
+    def const(v: Any, n: int) -> "Poly":
+        return Poly({(): np.full(n, int(v), dtype=np.int64)})
+
+    def concrete(self) -> np.ndarray | None:
+        keys = set(self.t)
+        if keys <= {()}:
+            c = self.t.get(())
+            return c if c is not None else None
+        return None
+
+    def add(self, o: "Poly", sign: int = 1) -> "Poly":
+        out = dict(self.t)
+        for m, c in o.t.items():
+            out[m] = out[m] + sign * c if m in out else sign * c
+        return Poly(out)
+
+    def mul(self, o: "Poly") -> "Poly":
+        out: dict[Mono, np.ndarray] = {}
+        for m1, c1 in self.t.items():
+            for m2, c2 in o.t.items():
+                m = tuple(sorted(m1 + m2))
+                out[m] = out[m] + c1 * c2 if m in out else c1 * c2
+        if any(len(m) > 3 for m in out):
+            raise Unsupported("index polynomial of degree > 3")
+        return Poly(out)
+
+
+def _concrete_of(p: Poly, n: int) -> np.ndarray:
+    c = p.concrete()
+    if c is None:
+        if p.t:
+            raise Unsupported("symbolic value where a thread-only value is required")
+        return np.zeros(n, dtype=np.int64)
+    return c
+
+
+@dataclass
+class Cond:
+    """Mask: ``base`` (per thread) AND every atom ``poly < 0``."""
+
+    base: np.ndarray
+    atoms: list[Poly]
+
+
+@dataclass
+class Rec:
+    """A float value produced by one instruction for all threads."""
+
+    kind: str            # "gload" | "lds" | "frag"
+    buf: str = ""        # global buffer name (gload)
+    off: Poly | None = None
+    cond: Cond | None = None
+    to_f16: bool = False
+    src_rec: np.ndarray | None = None   # lds: record id per thread
+    src_thr: np.ndarray | None = None   # lds: writer thread per thread
+    frag: Any = None                    # frag: (sg, i, j) arrays per thread
+
+
+@dataclass
+class Frag:
+    steps: list[tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]]  # (A rec, A thr, B rec, B thr) per step
+
+
+@dataclass(frozen=True)
+class GemmSpec:
+    a: str
+    b: str
+    c: str
+    m_sym: str
+    n_sym: str
+    K: int
+    TM: int
+    TN: int
+    row_axis: int          # program_id axis indexing tile rows (the other indexes cols)
+    a_dtype: DType
+    b_dtype: DType
+    c_dtype: DType
+    c_f16: bool            # output rounded to f16
+
+
+# ---------------------------------------------------------------------------
+# symbolic execution
+# ---------------------------------------------------------------------------
+
+
+class _SymExec:
+    def __init__(self, ir: IRModule, nt: int) -> None:
+        self.ir = ir
+        self.n = nt
+        self.ints: dict[int, Poly] = {}
+        self.bools: dict[int, Cond] = {}
+        self.floats: dict[int, int] = {}   # value id -> record id
+        self.recs: list[Rec] = []
+        self.frags: dict[int, Frag] = {}
+        self.tg: dict[int, tuple[np.ndarray, np.ndarray, DType]] = {}
+        self.global_bufs: dict[int, str] = {}
+        self.scalars: dict[int, str] = {}
+        self.stores: list[tuple[str, Poly, Cond, int]] = []
+        self.frag_stores: list[tuple[int, int, np.ndarray, np.ndarray]] = []  # (tg id, frag id, base, stride)
+        self.loaded: set[str] = set()
+        self.stored: set[str] = set()
+
+    def run(self) -> None:
+        for inst in self.ir.insts:
+            self.step(inst)
+
+    # -- helpers ------------------------------------------------------------
+    def ip(self, ref: ValueRef) -> Poly:
+        p = self.ints.get(ref.id)
+        if p is None:
+            raise Unsupported(f"u32 value v{ref.id} is not an index expression")
+        return p
+
+    def bc(self, ref: ValueRef) -> Cond:
+        c = self.bools.get(ref.id)
+        if c is None:
+            raise Unsupported(f"bool value v{ref.id} is not a mask expression")
+        return c
+
+    def uniform_sg(self, arr: np.ndarray, what: str) -> np.ndarray:
+        per = arr.reshape(-1, 32)
+        if np.any(per != per[:, :1]):
+            raise Unsupported(f"{what} differs across a simdgroup")
+        return per[:, 0]
+
+    def new_rec(self, r: Rec) -> int:
+        self.recs.append(r)
+        return len(self.recs) - 1
+
+    # -- instructions ------------------------------------------------------------
+    def step(self, inst: Inst) -> None:
+        op, out, a = inst.op, inst.out, inst.args
+        n = self.n
+        tids = np.arange(n, dtype=np.int64)
+        if op == "arg":
+            name, kind, dt = a
+            if kind == "buffer":
+                self.global_bufs[out.id] = name
+            elif dt == DType.U32:
+                self.ints[out.id] = Poly({(name,): np.ones(n, np.int64)})
+                self.scalars[out.id] = name
+            return
+        if op == "const":
+            v = a[0]
+            if out.dtype == DType.U32:
+                self.ints[out.id] = Poly.const(v, n)
+            elif out.dtype == DType.BOOL:
+                self.bools[out.id] = Cond(np.full(n, bool(v)), [])
+            return  # float consts only matter if used, which is unsupported below
+        if op == "program_id":
+            self.ints[out.id] = Poly({(f"%p{int(a[0])}",): np.ones(n, np.int64)})
+            return
+        if op == "thread_id":
+            raise Unsupported("global thread ids are not tile-GEMM indexing")
+        if op == "tid":
+            self.ints[out.id] = Poly({(): tids + int(a[0])})
+            return
+        if op == "local_id":
+            self.ints[out.id] = Poly({(): tids if int(a[0]) == 0 else np.zeros(n, np.int64)})
+            return
+        if op == "lane_id":
+            self.ints[out.id] = Poly({(): tids % 32})
+            return
+        if op == "sg_id":
+            self.ints[out.id] = Poly({(): tids // 32})
+            return
+        if op in ("add", "mul") and out.dtype == DType.U32:
+            x, y = self.ip(a[0]), self.ip(a[1])
+            self.ints[out.id] = x.add(y) if op == "add" else x.mul(y)
+            return
+        if op in ("floordiv", "mod"):
+            x, y = _concrete_of(self.ip(a[0]), n), _concrete_of(self.ip(a[1]), n)
+            if np.any(y <= 0) or np.any(x < 0):
+                raise Unsupported("division by zero / negative in index math")
+            self.ints[out.id] = Poly({(): x // y if op == "floordiv" else x % y})
+            return
+        if op == "lt" and a[0].dtype == DType.U32:
+            d = self.ip(a[0]).add(self.ip(a[1]), -1)
+            c = d.concrete()
+            if c is not None or not d.t:
+                self.bools[out.id] = Cond((c if c is not None else np.zeros(n, np.int64)) < 0, [])
+            else:
+                self.bools[out.id] = Cond(np.ones(n, bool), [d])
+            return
+        if op == "and":
+            x, y = self.bc(a[0]), self.bc(a[1])
+            self.bools[out.id] = Cond(x.base & y.base, x.atoms + y.atoms)
+            return
+        if op == "or":
+            x, y = self.bc(a[0]), self.bc(a[1])
+            if x.atoms or y.atoms:
+                raise Unsupported("disjunction of symbolic conditions")
+            self.bools[out.id] = Cond(x.base | y.base, [])
+            return
+        if op == "not":
+            x = self.bc(a[0])
+            if x.atoms:
+                raise Unsupported("negated symbolic condition")
+            self.bools[out.id] = Cond(~x.base, [])
+            return
+        if op == "where" and out.dtype == DType.U32:
+            c = self.bc(a[0])
+            if c.atoms:
+                raise Unsupported("data-dependent select in index math")
+            x, y = _concrete_of(self.ip(a[1]), n), _concrete_of(self.ip(a[2]), n)
+            self.ints[out.id] = Poly({(): np.where(c.base, x, y)})
+            return
+        if op == "cast":
+            src = a[0]
+            if out.dtype == DType.F16 and src.dtype == DType.F32 and src.id in self.floats:
+                r = self.recs[self.floats[src.id]]
+                if r.kind != "gload" and r.kind != "lds":
+                    raise Unsupported("cast of a computed float")
+                self.floats[out.id] = self.new_rec(Rec(**{**r.__dict__, "to_f16": True}))
+                return
+            raise Unsupported(f"cast {src.dtype}->{out.dtype} in a GEMM kernel")
+        if op == "alloc_tg":
+            size = int(a[0])
+            self.tg[out.id] = (np.full(size, -1, np.int64), np.zeros(size, np.int64), out.dtype)
+            return
+        if op == "barrier":
+            return
+        if op == "load":
+            buf, off, mask = a
+            cond = self.bc(mask)
+            if buf.id in self.global_bufs:
+                name = self.global_bufs[buf.id]
+                self.loaded.add(name)
+                self.floats[out.id] = self.new_rec(Rec("gload", buf=name, off=self.ip(off), cond=cond))
+                return
+            if buf.id in self.tg:
+                if cond.atoms:
+                    raise Unsupported("symbolic mask on a threadgroup load")
+                slots = _concrete_of(self.ip(off), n)
+                recs, thrs, _ = self.tg[buf.id]
+                if np.any(slots >= recs.size):
+                    raise Unsupported("threadgroup load out of range")
+                sr = np.where(cond.base, recs[slots], -2)
+                st = thrs[slots]
+                if np.any(sr == -1):
+                    raise Unsupported("read of an unwritten threadgroup slot")
+                self.floats[out.id] = self.new_rec(Rec("lds", src_rec=sr, src_thr=st))
+                return
+            raise Unsupported("load from an unknown buffer")
+        if op == "store":
+            buf, off, val, mask = a
+            cond = self.bc(mask)
+            if val.id not in self.floats:
+                raise Unsupported("stored value is not a tracked float")
+            rid = self.floats[val.id]
+            if buf.id in self.tg:
+                if cond.atoms:
+                    raise Unsupported("symbolic mask on a threadgroup store")
+                if self.recs[rid].kind != "gload":
+                    raise Unsupported("threadgroup store of a non-load value")
+                slots = _concrete_of(self.ip(off), n)
+                recs, thrs, _ = self.tg[buf.id]
+                w = np.nonzero(cond.base)[0]
+                if np.any(slots[w] >= recs.size):
+                    raise Unsupported("threadgroup store out of range")
+                if np.unique(slots[w]).size != w.size:
+                    raise Unsupported("two threads store one threadgroup slot")
+                recs[slots[w]] = rid
+                thrs[slots[w]] = w
+                return
+            if buf.id in self.global_bufs:
+                name = self.global_bufs[buf.id]
+                self.stored.add(name)
+                self.stores.append((name, self.ip(off), cond, rid))
+                return
+            raise Unsupported("store to an unknown buffer")
+        if op == "mma_zero":
+            self.frags[out.id] = Frag([])
+            return
+        if op == "mma":
+            a_buf, a_base, a_st, b_buf, b_base, b_st, acc = a
+            if a_buf.id not in self.tg or b_buf.id not in self.tg:
+                raise Unsupported("mma operands must come from threadgroup memory")
+            if self.tg[a_buf.id][2] != DType.F16 or self.tg[b_buf.id][2] != DType.F16:
+                raise Unsupported("only f16 threadgroup tiles are lifted")
+            prev = self.frags.get(acc.id)
+            if prev is None:
+                raise Unsupported("mma accumulator chain not rooted at mma_zero")
+            ab = self.uniform_sg(_concrete_of(self.ip(a_base), n), "mma a_base")
+            ast = self.uniform_sg(_concrete_of(self.ip(a_st), n), "mma a_stride")
+            bb = self.uniform_sg(_concrete_of(self.ip(b_base), n), "mma b_base")
+            bst = self.uniform_sg(_concrete_of(self.ip(b_st), n), "mma b_stride")
+            r8 = np.arange(8)
+            a_slots = ab[:, None, None] + r8[None, :, None] * ast[:, None, None] + r8[None, None, :]  # (S, i, k)
+            b_slots = bb[:, None, None] + r8[None, :, None] * bst[:, None, None] + r8[None, None, :]  # (S, k, j)
+            ar, at, _ = self.tg[a_buf.id]
+            br, bt, _ = self.tg[b_buf.id]
+            if a_slots.max() >= ar.size or b_slots.max() >= br.size or a_slots.min() < 0:
+                raise Unsupported("mma fragment outside its threadgroup tile")
+            if np.any(ar[a_slots] < 0) or np.any(br[b_slots] < 0):
+                raise Unsupported("mma reads an unwritten threadgroup slot")
+            self.frags[out.id] = Frag(prev.steps + [(ar[a_slots].copy(), at[a_slots].copy(), br[b_slots].copy(), bt[b_slots].copy())])
+            return
+        if op == "mma_store":
+            c_buf, c_base, c_st, frag = a
+            if c_buf.id not in self.tg:
+                raise Unsupported("mma_store outside threadgroup memory")
+            f = self.frags.get(frag.id)
+            if f is None:
+                raise Unsupported("mma_store of an unknown fragment")
+            base = self.uniform_sg(_concrete_of(self.ip(c_base), n), "mma_store base")
+            st = self.uniform_sg(_concrete_of(self.ip(c_st), n), "mma_store stride")
+            fid = self.new_rec(Rec("frag", frag=(f, base, st)))
+            recs, thrs, _ = self.tg[c_buf.id]
+            r8 = np.arange(8)
+            slots = base[:, None, None] + r8[None, :, None] * st[:, None, None] + r8[None, None, :]  # (S, i, j)
+            if slots.max() >= recs.size:
+                raise Unsupported("mma_store outside its threadgroup tile")
+            flat = slots.reshape(-1)
+            if np.unique(flat).size != flat.size:
+                raise Unsupported("overlapping fragment stores")
+            recs[flat] = fid
+            thrs[flat] = np.arange(flat.size)  # encodes (sg, i, j) as sg*64 + i*8 + j
+            return
+        raise Unsupported(f"op {op!r} is not part of a tile GEMM")
+
+
+# ---------------------------------------------------------------------------
+# decoding of gathered element positions
+# ---------------------------------------------------------------------------
+
+
+def _gather_poly(recs: list[Rec], rid: np.ndarray, thr: np.ndarray, attr: str) -> dict[Mono, np.ndarray]:
+    """Coefficients of rec.<attr> (a Poly) at (record, thread) pairs, shape of ``rid``."""
+    out: dict[Mono, np.ndarray] = {}
+    for r in np.unique(rid):
+        sel = rid == r
+        p: Poly = getattr(recs[int(r)], attr)
+        for m, c in p.t.items():
+            arr = out.setdefault(m, np.zeros(rid.shape, np.int64))
+            arr[sel] = c[thr[sel]]
+    return out
+
+
+def _poly_sub(x: dict[Mono, np.ndarray], y: dict[Mono, np.ndarray], shape: tuple[int, ...]) -> dict[Mono, np.ndarray]:
+    out = {m: c.copy() for m, c in x.items()}
+    for m, c in y.items():
+        out[m] = out.get(m, np.zeros(shape, np.int64)) - c
+    return {m: c for m, c in out.items() if np.any(c)}
+
+
+def _uniform_step(d: dict[Mono, np.ndarray]) -> dict[Mono, int]:
+    """A difference that must be the same integer polynomial for every element."""
+    out = {}
+    for m, c in d.items():
+        if np.any(c != c.flat[0]):
+            raise Unsupported("non-uniform stride between fragment elements")
+        out[m] = int(c.flat[0])
+    return out
+
+
+def _split(off: dict[Mono, np.ndarray], stride: dict[Mono, int], shape) -> tuple[dict[Mono, np.ndarray], dict[Mono, np.ndarray]]:
+    """Decompose ``off = stride * major + minor``.
+
+    A literal stride L splits the constant term by div/mod (minor in [0, L))
+    and requires every symbolic term to be a multiple of L (it belongs to the
+    major index).  A scalar-argument stride X moves the terms containing X to
+    the major index (X removed) and leaves the rest as the minor index.
+    """
+    zero = np.zeros(shape, np.int64)
+    if set(stride) == {()}:
+        L = stride[()]
+        if L <= 0:
+            raise Unsupported("non-positive row stride")
+        c0 = off.get((), zero)
+        major = {(): c0 // L}
+        for m, c in off.items():
+            if m == ():
+                continue
+            if np.any(c % L):
+                raise Unsupported("index not a multiple of the row stride")
+            major[m] = c // L
+        return {m: c for m, c in major.items() if np.any(c)}, {(): c0 % L}
+    if len(stride) == 1:
+        (sm, sc), = stride.items()
+        if len(sm) != 1 or sc != 1 or sm[0].startswith("%p"):
+            raise Unsupported("row stride must be a literal or one scalar argument")
+        sym = sm[0]
+        major: dict[Mono, np.ndarray] = {}
+        minor: dict[Mono, np.ndarray] = {}
+        for m, c in off.items():
+            if sym in m:
+                rest = list(m)
+                rest.remove(sym)
+                if sym in rest:
+                    raise Unsupported("index quadratic in the row stride")
+                major[tuple(rest)] = c
+            else:
+                minor[m] = c
+        return major, minor
+    raise Unsupported("unsupported row stride")
+
+
+def _concrete_part(p: dict[Mono, np.ndarray], shape, what: str) -> np.ndarray:
+    if set(p) - {()}:
+        raise Unsupported(f"{what} index is symbolic")
+    return p.get((), np.zeros(shape, np.int64))
+
+
+def _same(p: dict[Mono, np.ndarray], q: dict[Mono, np.ndarray]) -> bool:
+    keys = set(p) | set(q)
+    for m in keys:
+        a = p.get(m)
+        b = q.get(m)
+        if a is None and b is None:
+            continue
+        if a is None:
+            a = np.zeros_like(b)
+        if b is None:
+            b = np.zeros_like(a)
+        if not np.array_equal(a, b):
+            return False
+    return True
+
+
+def _as_tile(p: dict[Mono, np.ndarray], what: str) -> tuple[str, int, np.ndarray]:
+    """``p = T * %p<axis> + r`` with r concrete; returns (axis symbol, T, r)."""
+    syms = [m for m in p if m != ()]
+    if len(syms) != 1 or len(syms[0]) != 1 or not syms[0][0].startswith("%p"):
+        raise Unsupported(f"{what} index is not tile*program_id + offset")
+    T = p[syms[0]]
+    if np.any(T != T.flat[0]) or T.flat[0] <= 0:
+        raise Unsupported(f"{what} tile size differs")
+    r = p.get((), np.zeros(T.shape, np.int64))
+    return syms[0][0], int(T.flat[0]), r
+
+
+def _atoms_match(recs: list[Rec], rid: np.ndarray, thr: np.ndarray, expect: dict[Mono, np.ndarray], bound_sym: str | None,
+                 valid: np.ndarray) -> str | None:
+    """Every element's symbolic mask is empty or exactly ``expect - bound_sym < 0``;
+    returns the bound symbol found (or ``bound_sym``)."""
+    found = bound_sym
+    for r in np.unique(rid[valid]):
+        sel = (rid == r) & valid
+        cond = recs[int(r)].cond
+        uniq: list[Poly] = []
+        for atom in cond.atoms:
+            if not any(set(atom.t) == set(u.t) and all(np.array_equal(atom.t[m], u.t[m]) for m in atom.t) for u in uniq):
+                uniq.append(atom)
+        if len(uniq) > 1:
+            raise Unsupported("more than one symbolic bound on an operand")
+        for atom in uniq:
+            neg = [m for m, c in atom.t.items() if len(m) == 1 and not m[0].startswith("%p") and np.all(c[thr[sel]] == -1)]
+            if len(neg) != 1:
+                raise Unsupported("operand bound is not `index < scalar`")
+            sym = neg[0][0]
+            if found is not None and sym != found:
+                raise Unsupported("operand bounded by two different scalars")
+            found = sym
+            for m, c in atom.t.items():
+                if m == neg[0]:
+                    continue
+                want = expect.get(m)
+                got = c[thr[sel]]
+                if want is None or not np.array_equal(want[sel], got):
+                    raise Unsupported("operand bound differs from its row/col index")
+            for m, c in expect.items():
+                if m not in atom.t and np.any(c[sel]):
+                    raise Unsupported("operand bound differs from its row/col index")
+    return found
+
+
+def analyze(ir: IRModule, block: int) -> GemmSpec:
+    """Prove that ``ir`` is a dense tile GEMM; raise :class:`Unsupported` otherwise."""
+    if block % 32 or block > 1024:
+        raise Unsupported("threadgroup size must be a multiple of 32")
+    ops = {i.op for i in ir.insts}
+    if "mma" not in ops or "mma_store" not in ops:
+        raise Unsupported("no simdgroup MMA")
+    ex = _SymExec(ir, block)
+    ex.run()
+    recs = ex.recs
+    frag_recs = [r for r in recs if r.kind == "frag"]
+    if len(frag_recs) != 1:
+        raise Unsupported("expected exactly one mma_store")
+    frag, _, _ = frag_recs[0].frag
+    if not frag.steps:
+        raise Unsupported("empty mma chain")
+    if len(ex.stored) != 1 or ex.stored & ex.loaded:
+        raise Unsupported("expected one output buffer that is not read")
+    c_name = next(iter(ex.stored))
+    S = block // 32
+
+    a_buf = b_buf = None
+    lda = ldb = None
+    row_of = col_of = None       # per (S, 8) row / col polys of the fragment
+    m_sym = n_sym = None
+    ks: list[np.ndarray] = []
+    for ar, at, br, bt in frag.steps:
+        for rid in (ar, br):
+            kinds = {recs[int(r)].kind for r in np.unique(rid)}
+            if kinds != {"gload"}:
+                raise Unsupported("fragment slot not filled from global memory")
+        an = {recs[int(r)].buf for r in np.unique(ar)}
+        bn = {recs[int(r)].buf for r in np.unique(br)}
+        if len(an) != 1 or len(bn) != 1:
+            raise Unsupported("fragment mixes buffers")
+        an, bn = an.pop(), bn.pop()
+        a_buf = a_buf or an
+        b_buf = b_buf or bn
+        if (an, bn) != (a_buf, b_buf) or a_buf == b_buf or c_name in (a_buf, b_buf):
+            raise Unsupported("operand buffers change between steps")
+        shape = ar.shape
+        # liveness: the concrete part of each element's load mask; masked elements are 0
+        a_base = np.zeros(shape, bool)
+        b_base = np.zeros(shape, bool)
+        for r in np.unique(ar):
+            sel = ar == r
+            a_base[sel] = recs[int(r)].cond.base[at[sel]]
+        for r in np.unique(br):
+            sel = br == r
+            b_base[sel] = recs[int(r)].cond.base[bt[sel]]
+        if np.any(a_base != a_base[:, :1, :]) or np.any(b_base != b_base[:, :, :1]):
+            raise Unsupported("operand liveness varies along rows/cols")
+        live = a_base[:, 0, :]                                  # (S, k)
+        if not np.array_equal(live, b_base[:, :, 0]) or np.any(live != live[:1]):
+            raise Unsupported("operand masks do not agree along k")
+        lk = live[0]
+        kidx = np.nonzero(lk)[0]
+        if kidx.size == 0:
+            ks.append(np.full((S, 8), -1, np.int64))
+            continue
+        k0 = int(kidx[0])
+        pairs = np.nonzero(lk[:-1] & lk[1:])[0]
+        a_off = _gather_poly(recs, ar, at, "off")
+        b_off = _gather_poly(recs, br, bt, "off")
+        # strides between live fragment elements
+        a_row = _uniform_step(_poly_sub({m: c[:, 1:, kidx] for m, c in a_off.items()},
+                                        {m: c[:, :-1, kidx] for m, c in a_off.items()}, (S, 7, kidx.size)))
+        if pairs.size:
+            a_col = _uniform_step(_poly_sub({m: c[:, :, pairs + 1] for m, c in a_off.items()},
+                                            {m: c[:, :, pairs] for m, c in a_off.items()}, (S, 8, pairs.size)))
+            b_row = _uniform_step(_poly_sub({m: c[:, pairs + 1, :] for m, c in b_off.items()},
+                                            {m: c[:, pairs, :] for m, c in b_off.items()}, (S, pairs.size, 8)))
+            if a_col != {(): 1}:
+                raise Unsupported("A fragment columns are not contiguous")
+            if ldb is None:
+                ldb = b_row
+            if b_row != ldb:
+                raise Unsupported("B row stride changes between steps")
+        b_col = _uniform_step(_poly_sub({m: c[:, kidx, 1:] for m, c in b_off.items()},
+                                        {m: c[:, kidx, :-1] for m, c in b_off.items()}, (S, kidx.size, 7)))
+        if b_col != {(): 1}:
+            raise Unsupported("B fragment columns are not contiguous")
+        if lda is None:
+            lda = a_row
+        if a_row != lda:
+            raise Unsupported("A row stride changes between steps")
+        if ldb is None:
+            raise Unsupported("B row stride not determined")
+        a_major, a_minor = _split(a_off, lda, shape)        # A: row index, k
+        b_major, b_minor = _split(b_off, ldb, shape)        # B: k, col index
+        a_k = _concrete_part(a_minor, shape, "A's k")
+        b_k = _concrete_part(b_major, shape, "B's k")
+        for m, c in a_major.items():
+            if np.any(c[:, :, kidx] != c[:, :, k0:k0 + 1]):
+                raise Unsupported("A row index varies along k")
+        for m, c in b_minor.items():
+            if np.any(c[:, kidx, :] != c[:, k0:k0 + 1, :]):
+                raise Unsupported("B column index varies along k")
+        if not np.array_equal(a_k[:, 0, kidx], b_k[:, kidx, 0]):
+            raise Unsupported("A and B k indices are not paired")
+        ri = {m: c[:, :, k0] for m, c in a_major.items()}      # (S, i)
+        col_poly = {m: c[:, k0, :] for m, c in b_minor.items()}  # (S, j)
+        if row_of is None:
+            row_of, col_of = ri, col_poly
+        if not _same(ri, row_of):
+            raise Unsupported("A rows change between steps")
+        if not _same(col_poly, col_of):
+            raise Unsupported("B cols change between steps")
+        live3_a = np.broadcast_to(lk[None, None, :], shape)
+        live3_b = np.broadcast_to(lk[None, :, None], shape)
+        row_full = {m: np.repeat(c[:, :, None], 8, axis=2) for m, c in ri.items()}
+        col_full = {m: np.repeat(c[:, None, :], 8, axis=1) for m, c in col_of.items()}
+        m_sym = _atoms_match(recs, ar, at, row_full, m_sym, live3_a)
+        n_sym = _atoms_match(recs, br, bt, col_full, n_sym, live3_b)
+        ks.append(np.where(lk[None, :], a_k[:, 0, :], -1))
+    assert lda is not None and ldb is not None and row_of is not None and col_of is not None
+    if set(lda) != {()}:
+        raise Unsupported("A's row length (K) must be a compile-time constant")
+    K = lda[()]
+    allk = np.concatenate(ks, axis=1)        # (S, steps*8)
+    for s in range(S):
+        got = np.sort(allk[s][allk[s] >= 0])
+        if not np.array_equal(got, np.arange(K)):
+            raise Unsupported("the k steps do not cover [0, K) exactly once")
+    if len(ldb) != 1 or list(ldb)[0] == () or list(ldb.values())[0] != 1:
+        raise Unsupported("B's row stride must be a scalar argument")
+    ldb_sym = list(ldb)[0][0]
+    if n_sym is not None and n_sym != ldb_sym:
+        raise Unsupported("B's column bound differs from its row stride")
+    r_axis, TM, r_off = _as_tile(row_of, "row")
+    c_axis, TN, c_off = _as_tile(col_of, "col")
+    if r_axis == c_axis:
+        raise Unsupported("rows and cols indexed by the same program id")
+
+    # --- copy-out: every tile element stored once to C[row*ldb + col] ---
+    seen = np.zeros((S, 8, 8), np.int64)
+    frag_rid = recs.index(frag_recs[0])
+    c_f16 = None
+    for name, off, cond, rid in ex.stores:
+        r = recs[rid]
+        if r.kind != "lds":
+            raise Unsupported("output is not read back from the fragment tile")
+        sel = cond.base & (r.src_rec >= 0)
+        if np.any((r.src_rec != frag_rid) & sel):
+            raise Unsupported("output element not from the accumulator")
+        if c_f16 is None:
+            c_f16 = r.to_f16
+        if r.to_f16 != c_f16:
+            raise Unsupported("mixed output conversions")
+        t = np.nonzero(sel)[0]
+        code = r.src_thr[t]
+        sg, i, j = code // 64, (code // 8) % 8, code % 8
+        np.add.at(seen, (sg, i, j), 1)
+        offp = {m: c[t] for m, c in off.t.items()}
+        major, minor = _split(offp, ldb, t.shape)
+        want_row = {m: c[sg, i] for m, c in row_of.items()}
+        want_col = {m: c[sg, j] for m, c in col_of.items()}
+        if not (_same(major, want_row) and _same(minor, want_col)):
+            raise Unsupported("output offset is not row*ldb + col of its fragment element")
+        # store masks: at most `row < M` and `col < N`
+        for atom in cond.atoms:
+            at = {m: c[t] for m, c in atom.t.items()}
+            neg = [m for m, c in at.items() if len(m) == 1 and not m[0].startswith("%p") and np.all(c == -1)]
+            if len(neg) != 1:
+                raise Unsupported("output mask is not `index < scalar`")
+            rest = {m: c for m, c in at.items() if m != neg[0]}
+            sym = neg[0][0]
+            is_row = _same(rest, want_row)
+            is_col = _same(rest, want_col)
+            if is_row and (m_sym is None or m_sym == sym):
+                m_sym = sym
+            elif is_col and sym == ldb_sym:
+                pass
+            else:
+                raise Unsupported("output mask is not row < M / col < N")
+    if np.any(seen != 1):
+        raise Unsupported("the tile is not stored exactly once")
+    # the tile is the full rectangle [0,TM) x [0,TN)
+    rows = r_off.reshape(-1)
+    cols = c_off.reshape(-1)
+    if sorted(set(rows.tolist())) != list(range(TM)) or sorted(set(cols.tolist())) != list(range(TN)):
+        raise Unsupported("the fragments do not tile a TM x TN rectangle")
+    if m_sym is None:
+        raise Unsupported("no row bound found (M)")
+    args = {a.name: a for a in ir.args}
+    if m_sym not in args or ldb_sym not in args:
+        raise Unsupported("bounds are not kernel arguments")
+    a_dt, b_dt, c_dt = args[a_buf].dtype, args[b_buf].dtype, args[c_name].dtype
+    if c_dt == DType.F16 and not c_f16:
+        raise Unsupported("f16 output without an explicit conversion")
+    return GemmSpec(a=a_buf, b=b_buf, c=c_name, m_sym=m_sym, n_sym=ldb_sym, K=int(K), TM=TM, TN=TN,
+                    row_axis=int(r_axis[2:]), a_dtype=a_dt, b_dtype=b_dt, c_dtype=c_dt, c_f16=bool(c_f16))
+
+
+# ---------------------------------------------------------------------------
+# lowering and launch planning
+# ---------------------------------------------------------------------------
 
 
 def try_lift(ir: IRModule, block: int) -> Any:
-    return None
+    """Lowered MFMA GEMM for ``ir`` if it provably is one, else ``None``."""
+    import os
+
+    if os.environ.get("EAS_HIP_DISABLE_GEMM_LIFT", "") not in ("", "0"):
+        return None
+    if "mma" not in {i.op for i in ir.insts}:
+        return None
+    try:
+        spec = analyze(ir, block)
+    except Unsupported:
+        return None
+    from .gemm_kernels import emit_gemm
+
+    return emit_gemm(ir, block, spec)
+
+
+def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x: int | None) -> Any:
+    """Launch plan of a lifted GEMM for a reference grid ``groups``."""
+    from ..runtime.hip import LaunchPlan
+
+    if live_x is not None:
+        raise ValueError("a lifted GEMM kernel needs a 2-D grid (pass _grid=...)")
+    p = geo.params
+    M = int(runtime_args[p["m_sym"]])
+    N = int(runtime_args[p["n_sym"]])
+    K = int(p["K"])
+    if max(M * K, K * N, M * N) >= 1 << 32:
+        raise ValueError("lifted GEMM: matrix too large for u32 indexing")
+    g_rows = groups[p["row_axis"]]
+    g_cols = groups[1 - p["row_axis"]]
+    m_eff = min(M, g_rows * p["TM"])
+    n_eff = min(N, g_cols * p["TN"])
+    if m_eff == 0 or n_eff == 0:
+        return None
+    bm, bn = p["BM"], p["BN"]
+    tiles = -(-m_eff // bm) * -(-n_eff // bn)
+    return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), (m_eff, n_eff))

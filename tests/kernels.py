@@ -397,3 +397,80 @@ def matmul_mma_f16out_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexpr
 
 def mma_grid(meta, rargs):
     return (cdiv(int(rargs["N"]), int(meta["BN"])), cdiv(int(rargs["M"]), int(meta["BM"])), 1)
+
+
+@eas.kernel
+def matmul_mma_variant_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexpr, BK: eas.constexpr,
+                              K: eas.constexpr, NT: eas.constexpr, VARIANT: eas.constexpr):
+    """matmul_mma_kernel with one deliberate change selected by VARIANT (0 = none).
+
+    Used to check that the GEMM lift proves what it replaces: variants 1-8 are
+    not dense GEMMs (or not with these masks) and must keep the literal
+    lowering; variants 9-10 are GEMMs written differently and may be lifted.
+      1 last k block skipped        2 A rows shifted by one       3 column mask uses M
+      4 output stored transposed    5 B row stride is M           6 half the tile stored
+      7 A fragment stride off       8 one output element stored twice
+      9 k blocks in reverse order  10 rows on program_id(0), cols on program_id(1)
+    """
+    V = VARIANT
+    pid_n = mk.program_id(1 if V == 10 else 0)
+    pid_m = mk.program_id(0 if V == 10 else 1)
+    tid = mk.tid(0, NT)
+    sg = mk.sg_id()
+    base_m = pid_m * BM
+    base_n = pid_n * BN
+    sgn = BN // 8
+    sg_m = sg // sgn
+    sg_n = sg % sgn
+    lda = BK + 1
+    ldb = BN + 1
+    ldc = BN + 1
+    As = mk.alloc_tg_f16(BM * lda)
+    Bs = mk.alloc_tg_f16(BK * ldb)
+    Cs = mk.alloc_tg(BM * ldc)
+    acc = mk.mma_zero()
+    kblocks = list(range(0, K, BK))
+    if V == 1:
+        kblocks = kblocks[:-1]
+    if V == 9:
+        kblocks = kblocks[::-1]
+    for k0 in kblocks:
+        for i in range(0, BM * BK, NT):
+            a_idx = tid + i
+            a_r = a_idx // BK
+            a_c = a_idx % BK
+            a_row = base_m + a_r + (1 if V == 2 else 0)
+            a_col = k0 + a_c
+            in_tile = a_idx < BM * BK
+            a_mask = mk.where(in_tile, mk.where(a_row < M, a_col < K, False), False)
+            mk.store(As, a_r * lda + a_c, mk.to_f16(mk.load(a, a_row * K + a_col, a_mask)), in_tile)
+        for i in range(0, BK * BN, NT):
+            b_idx = tid + i
+            b_r = b_idx // BN
+            b_c = b_idx % BN
+            b_row = k0 + b_r
+            b_col = base_n + b_c
+            in_tile = b_idx < BK * BN
+            b_mask = mk.where(in_tile, mk.where(b_row < K, b_col < N, False), False)
+            stride = M if V == 5 else N
+            mk.store(Bs, b_r * ldb + b_c, mk.to_f16(mk.load(b, b_row * stride + b_col, b_mask)), in_tile)
+        mk.barrier()
+        for kk in range(0, BK, 8):
+            a_stride = lda + 1 if V == 7 else lda
+            acc = mk.mma(As, (sg_m * 8) * lda + kk, a_stride, Bs, kk * ldb + (sg_n * 8), ldb, acc)
+        mk.barrier()
+    mk.mma_store(Cs, (sg_m * 8) * ldc + (sg_n * 8), ldc, acc)
+    mk.barrier()
+    total = BM * BN // 2 if V == 6 else BM * BN
+    for i in range(0, total, NT):
+        c_idx = tid + i
+        r = c_idx // BN
+        cc = c_idx % BN
+        row = base_m + r
+        col = base_n + cc
+        col_bound = M if V == 3 else N
+        mask = mk.where(row < M, col < col_bound, False)
+        off = col * N + row if V == 4 else row * N + col
+        mk.store(c, off, mk.load(Cs, r * ldc + cc, True), mask)
+    if V == 8:
+        mk.store(c, base_m * N + base_n, mk.load(Cs, 0, True), mk.where(base_m < M, base_n < N, False))

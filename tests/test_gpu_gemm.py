@@ -1,0 +1,126 @@
+"""GPU parity of simdgroup-MMA matmul kernels (lifted to the MFMA GEMM, or literal).
+
+Tolerance: ``max|C - R| / max|R| <= 2e-2`` for f16 inputs with f32 accumulate,
+R = float64 matmul of the f16-rounded inputs (examples/matmul_simdgroup.py:218-222
+checks against an f16 matmul).  Products of f16 values are exact in f32, so the
+tests also hold the tighter ``1e-5 * sqrt(K)``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import kernels as K
+from oracle import interp, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(m, n, k, dtype=np.float16, seed=0):
+    rng = np.random.default_rng(seed)
+    a = rng.uniform(-1, 1, m * k).astype(dtype)
+    b = rng.uniform(-1, 1, k * n).astype(dtype)
+    return a, b
+
+
+def _mma(kern, a, b, c, m, n, k, bm=32, bn=32, bk=8, **extra):
+    nt = (bm // 8) * (bn // 8) * 32
+    kern(a, b, c, m, n, BM=bm, BN=bn, BK=bk, K=k, NT=nt, _grid=K.mma_grid, _tptg=(nt, 1, 1), **extra)
+
+
+def _check(c, a, b, m, n, k):
+    ref = ops.matmul_ref(a.reshape(m, k).astype(np.float32), b.reshape(k, n).astype(np.float32))
+    err = ops.rel_err(np.asarray(c, np.float64).reshape(m, n), ref)
+    assert err <= 2e-2
+    assert err <= 1e-5 * math.sqrt(k), err
+
+
+@pytest.mark.parametrize("mnk,tile", [((64, 64, 64), (32, 32, 8)), ((300, 520, 200), (32, 32, 8)),
+                                      ((33, 17, 100), (32, 32, 16)), ((257, 300, 72), (16, 32, 8)),
+                                      ((512, 512, 512), (32, 64, 16))])
+def test_lifted_mma_matmul_matches_f64(gpu_runtime, mnk, tile):
+    m, n, k = mnk
+    bm, bn, bk = tile
+    ck = K.matmul_mma_kernel.compile(np.zeros(1, np.float16), np.zeros(1, np.float16), np.zeros(1, np.float32),
+                                     m, n, BM=bm, BN=bn, BK=bk, K=k, NT=(bm // 8) * (bn // 8) * 32)
+    assert ck.geometry.kind == "gemm"
+    a, b = _inputs(m, n, k)
+    c = np.full(m * n, np.nan, np.float32)
+    _mma(K.matmul_mma_kernel, a, b, c, m, n, k, bm, bn, bk)
+    _check(c, a, b, m, n, k)
+
+
+def test_lifted_partial_grid_writes_only_its_rectangle(gpu_runtime):
+    m, n, k = 200, 300, 64
+    a, b = _inputs(m, n, k)
+    c = np.full(m * n, 7.0, np.float32)
+    K.matmul_mma_kernel(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512, _grid=(3, 2, 1), _tptg=(512, 1, 1))
+    ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
+    got = c.reshape(m, n)
+    assert ops.rel_err(got[:64, :96], ref[:64, :96]) <= 1e-5 * math.sqrt(k)
+    assert np.all(got[64:, :] == 7.0) and np.all(got[:, 96:] == 7.0)
+
+
+def test_lifted_f16_output_rounds_accumulator(gpu_runtime):
+    m, n, k = 96, 160, 128
+    a, b = _inputs(m, n, k)
+    c = np.zeros(m * n, np.float16)
+    _mma(K.matmul_mma_f16out_kernel, a, b, c, m, n, k)
+    ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
+    # within one f16 rounding of the f32 accumulation
+    assert ops.rel_err(c.astype(np.float64).reshape(m, n), ref) <= 2e-3
+
+
+def test_lifted_f32_inputs_are_rounded_to_f16(gpu_runtime):
+    m, n, k = 64, 96, 64
+    a, b = _inputs(m, n, k, np.float32)
+    c = np.zeros(m * n, np.float32)
+    _mma(K.matmul_mma_kernel, a, b, c, m, n, k)
+    a16, b16 = a.astype(np.float16), b.astype(np.float16)
+    _check(c, a16, b16, m, n, k)
+
+
+def test_swapped_grid_axes_variant(gpu_runtime):
+    m, n, k = 100, 70, 64
+    a, b = _inputs(m, n, k)
+    c = np.zeros(m * n, np.float32)
+    K.matmul_mma_variant_kernel(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512, VARIANT=10,
+                                _grid=(K.cdiv(m, 32), K.cdiv(n, 32), 1), _tptg=(512, 1, 1))
+    _check(c, a, b, m, n, k)
+
+
+def test_unlifted_variant_runs_literally_and_matches_oracle(gpu_runtime):
+    # VARIANT=1 skips the last k block: not a GEMM, so the literal MMA lowering runs.
+    m, n, k = 40, 48, 32
+    a, b = _inputs(m, n, k)
+    c = np.zeros(m * n, np.float32)
+    K.matmul_mma_variant_kernel(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512, VARIANT=1,
+                                _grid=K.mma_grid, _tptg=(512, 1, 1))
+    ref = interp.run_kernel(K.matmul_mma_variant_kernel, a, b, np.zeros(m * n, np.float32), m, n,
+                            BM=32, BN=32, BK=8, K=k, NT=512, VARIANT=1, _grid=K.mma_grid)["c"]
+    assert ops.rel_err(c.reshape(m, n), ref.reshape(m, n)) <= 1e-6
+    full = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
+    assert ops.rel_err(c.reshape(m, n), full) > 1e-2  # really is missing a k block
+
+
+@pytest.mark.parametrize("k", [4096, 4100])
+def test_full_size_4096_sampled_rows(gpu_runtime, k):
+    """BASELINE sizes (4096 x 4096 x K): every output row computed on the GPU;
+    a seeded sample of 48 rows checked against float64 on the host."""
+    import torch
+
+    m = n = 4096
+    a, b = _inputs(m, n, k, seed=1)
+    ta = torch.from_numpy(a).cuda()
+    tb = torch.from_numpy(b).cuda()
+    tc = torch.full((m * n,), float("nan"), device="cuda", dtype=torch.float32)
+    _mma(K.matmul_mma_kernel, ta, tb, tc, m, n, k)
+    torch.cuda.synchronize()
+    c = tc.cpu().numpy().reshape(m, n)
+    assert np.isfinite(c).all()
+    rows = np.sort(np.random.default_rng(7).choice(m, 48, replace=False))
+    ref = a.reshape(m, k)[rows].astype(np.float64) @ b.reshape(k, n).astype(np.float64)
+    assert ops.rel_err(c[rows], ref) <= 1e-5 * math.sqrt(k)
