@@ -40,7 +40,7 @@ def build_lib() -> Path:
         str(ROCM / "bin" / "hipcc"), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-shared",
         *HIP_FLAGS, "-Wall", "-Wno-unused-command-line-argument", f"-I{INCLUDE}",
         str(CSRC / "eas_hip.cpp"), "-o", str(tmp),
-        f"-L{ROCM / 'lib'}", "-lhiprtc", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
+        f"-L{ROCM / 'lib'}", "-ldl", "-lamdhip64", f"-Wl,-rpath,{ROCM / 'lib'}",
     ])
     os.replace(tmp, LIB)
     return LIB

@@ -1,23 +1,36 @@
 """gfx950 MFMA GEMM emitted for kernels that ``gemm_lift`` proved to be dense GEMMs.
 
-Design (MI355X / CDNA4):
+One workgroup of 4 waves (2 x 2) computes a 256 x 256 tile of C; each wave owns
+a 128 x 128 block held as 4 x 4 ``v_mfma_f32_32x32x16_f16`` accumulators
+(256 AGPRs).  Two bodies share one LDS array; a uniform branch picks one per
+launch:
 
-* workgroup tile BM x BN with BK = 64, waves arranged WM x WN; each wave owns a
-  (BM/WM) x (BN/WN) block of 32x32 accumulators fed by
-  ``v_mfma_f32_32x32x16_f16`` (A: 8 consecutive k per lane, B: 8 consecutive
-  k per lane, f32 accumulate in AGPRs);
-* A and B stream global -> registers -> LDS, double buffered (one barrier per
-  k-tile, next tile's loads issued before the current tile's MFMAs);
-* B is row-major (k, n) in HBM but MFMA wants k contiguous per lane: each
-  thread loads an 8(k) x 8(n) block (eight 16-byte row loads) and transposes it
-  in registers, so LDS holds B as [n][k]; the lane -> block map puts the k-group
-  fastest so every 16-lane LDS write group covers 256 distinct bytes;
-* LDS rows are padded by 16 bytes (pitch BK+8 halves) so the 32 rows a
-  fragment read touches fall in distinct banks;
-* tile order is XCD aware: workgroup w runs on XCD w % 8, so each XCD gets a
-  contiguous range of tiles, grouped 4 tile-rows high for L2 reuse;
-* interior tiles take a branch-free path; edge tiles and the K tail use masked
-  loads (zero fill) and masked stores.
+DMA body (f16 A and B; K and ldb multiples of 8, 16-byte aligned bases, each
+matrix under 2 GiB):
+
+* A and B go HBM -> LDS with ``buffer_load_dwordx4 ... lds`` (no staging
+  registers), BK = 32 per stage, a 4-stage ring (128 KB), so loads are issued
+  three stages ahead;
+* LDS holds A as [m][k] and B as [k][n] (the layouts of HBM); 16-byte chunks
+  are XOR-swizzled by row so fragment reads are bank-conflict free;
+* A fragments are ``ds_read_b128`` (8 consecutive k per lane); B fragments are
+  two ``ds_read_b64_tr_b16`` per MFMA operand, which transpose a 4(k) x 16(n)
+  block across each 16-lane group so every lane receives k-contiguous B;
+* buffer range checks give zeros for rows past M and for B rows past K; the
+  lanes of the K tail stage that would read past K in A use an offset outside
+  the range;
+* the iteration is scheduled by hand (``sched_barrier``): ks0 MFMAs overlap the
+  ks1 fragment reads; after the mid-iteration barrier the ks1 MFMAs overlap the
+  DMA issue (one every two MFMAs) and the next stage's ks0 fragment reads.
+
+Register body (any other case, including f32 inputs that MFMA consumes as f16):
+global -> registers -> LDS, BK = 64, double buffered; B is transposed in
+registers (each thread loads an 8(k) x 8(n) block) so LDS holds B as [n][k];
+edge tiles and the K tail load element by element with zero fill straight into
+LDS.
+
+Tile order is XCD aware: workgroup w runs on XCD w % 8, so each XCD gets a
+contiguous range of tiles, grouped 4 tile-rows high for L2 reuse.
 
 The kernel computes C[m, n] for m < m_eff, n < n_eff (hidden arguments: the
 rectangle the reference launch covers).  Rows of A have length K (a compile-
@@ -32,7 +45,13 @@ from .hip import PRELUDE, Geometry, Lowered, ctype
 
 _TEMPLATE = r"""
 typedef _Float16 eas_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 eas_h4 __attribute__((ext_vector_type(4)));
+typedef __fp16 eas_h4t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef float eas_f32x16 __attribute__((ext_vector_type(16)));
+typedef int eas_rsrc __attribute__((ext_vector_type(4)));
+#define EAS_LDS __attribute__((address_space(3)))
+// s_waitcnt with only vmcnt limited (gfx9 encoding: vmcnt[3:0], [15:14]; expcnt and lgkmcnt at max)
+#define EAS_WAITVM(n) (((n) & 15) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
 
 template <typename T> static __device__ __forceinline__ eas_h8 eas_load8(const T* p);
 template <> __device__ __forceinline__ eas_h8 eas_load8<_Float16>(const _Float16* p) { return *(const eas_h8*)p; }
@@ -44,32 +63,185 @@ template <> __device__ __forceinline__ eas_h8 eas_load8<float>(const float* p) {
   return v;
 }
 
-extern "C" __global__ __launch_bounds__(@THREADS@) void @NAME@(
-    @PARAMS@) {
-  constexpr int BM = @BM@, BN = @BN@, BK = 64, WM = @WM@, WN = @WN@, K = @K@;
-  constexpr int PITCH = BK + 8, NTHREADS = WM * WN * 64, TI = BM / WM / 32, TJ = BN / WN / 32;
-  constexpr int KC = BK / 8, A_IT = BM * BK / 8 / NTHREADS, NBLK = BK * BN / 64;
+// raw buffer resource: base, range in bytes (reads at or past it return 0), gfx9 word 3
+static __device__ __forceinline__ eas_rsrc eas_make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  eas_rsrc r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+// 16 bytes per lane, HBM -> LDS; lane i writes LDS bytes [lds + 16 i, lds + 16 i + 16).
+// Issued as asm so the compiler does not add vmcnt(0) before every LDS read; the
+// pipeline counts its own loads with EAS_WAITVM.
+static __device__ __forceinline__ void eas_dma16(eas_rsrc r, uint32_t voff, uint32_t lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+}
+
+template <typename CT, int K>
+static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                                                    CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
+                                                    _Float16* smem) {
+  constexpr int BM = 256, BN = 256, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
+  constexpr int STAGE_H = BM * BK;  // halves per operand per stage (16 KB)
+  _Float16* As = smem;
+  _Float16* Bs = smem + NSTAGE * STAGE_H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
+  const eas_rsrc rb = eas_make_rsrc(B, (uint32_t)K * (uint32_t)ldb * 2u);
+  // DMA instruction q = 4 wave + i writes 1 KB of a stage.  A: rows 16q + lane/4, chunk lane%4
+  // stored at chunk ^ ((row/4)%4).  B: rows (k) 2q + lane/32, chunk lane%32 stored at chunk ^ 4(row%4).
+  uint32_t a_off[4], b_off[4];
+  int a_k[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = wave * 4 + i;
+    const int r_a = 16 * q + (lane >> 2);
+    const int c_a = (lane & 3) ^ ((r_a >> 2) & 3);
+    a_off[i] = ((uint32_t)(m0 + r_a) * (uint32_t)K + (uint32_t)(c_a * 8)) * 2u;
+    a_k[i] = c_a * 8;
+    const int r_b = 2 * q + (lane >> 5);
+    const int c_b = (lane & 31) ^ (4 * (r_b & 3));
+    b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
+  }
+  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS _Float16*)As, lds_b = (uint32_t)(size_t)(EAS_LDS _Float16*)Bs;
+  auto dma_one = [&](int kt, int d) {  // d in 0..7: 0..3 A, 4..7 B
+    const int s = kt % NSTAGE, i = d & 3;
+    const uint32_t dst = (uint32_t)((s * STAGE_H + (wave * 4 + i) * 512) * 2);
+    if (d < 4) {
+      uint32_t off = a_off[i] + (uint32_t)(kt * BK * 2);
+      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: past the range -> zeros
+      eas_dma16(ra, off, lds_a + dst);
+    } else {
+      uint32_t off = b_off[i] + (uint32_t)kt * (uint32_t)(BK * 2) * (uint32_t)ldb;
+      if (K % BK != 0 && kt * BK + 2 * (wave * 4 + i) + (lane >> 5) >= K) off = 0x80000000u;  // B rows past K
+      eas_dma16(rb, off, lds_b + dst);
+    }
+  };
+  // fragment offsets (halves within a stage)
+  int fa_off[2][4], fb_off[2][4][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = wm * 128 + i * 32 + (lane & 31);
+      const int c = (2 * ks + (lane >> 5)) ^ ((r >> 2) & 3);
+      fa_off[ks][i] = r * BK + c * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // ds_read_b64_tr_b16: in each 16-lane group, source lane kq addresses row kq/4, columns 4(kq%4)..+3;
+        // result lane i receives column i for the four rows
+        const int gq = lane >> 4, kq = lane & 15;
+        const int row = 16 * ks + 8 * (gq >> 1) + 4 * h + (kq >> 2);
+        const int col = wn * 128 + j * 32 + 16 * (gq & 1) + 4 * (kq & 3);
+        const int chunk = (col >> 3) ^ (4 * (row & 3));
+        fb_off[ks][j][h] = row * BN + chunk * 8 + (col & 7);
+      }
+  }
+  eas_h8 fa[2][4], fb[2][4];
+  auto read_a = [&](int s, int ks, int i) { fa[ks][i] = *(const eas_h8*)(As + s * STAGE_H + fa_off[ks][i]); };
+  auto read_b = [&](int s, int ks, int j) {
+    const _Float16* bs = Bs + s * STAGE_H;
+    const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
+    const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
+    const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
+    fb[ks][j] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+  };
+  eas_f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (eas_f32x16){};
+  auto mfma_row = [&](int ks, int i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+  };
+  // this wave's loads of the awaited stage are done; `later` newer stages (8 loads each) may stay in flight
+  auto wait_stage = [&](int later) {
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(16));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
+    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+  };
+
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p)
+    if (p < KT)
+#pragma unroll
+      for (int d = 0; d < 8; ++d) dma_one(p, d);
+  wait_stage(KT - 1 < NSTAGE - 2 ? KT - 1 : NSTAGE - 2);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { read_b(0, 0, i); read_a(0, 0, i); }
+  for (int kt = 0; kt < KT; ++kt) {
+    const int s = kt % NSTAGE, sn = (kt + 1) % NSTAGE;
+    const bool next = kt + 1 < KT, issue = kt + NSTAGE - 1 < KT;
+    // phase A: ks0 MFMAs (set 0) while the ks1 fragments (set 1) load
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(s, 1, 0); read_b(s, 1, 1);
+    mfma_row(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(s, 1, 2); read_b(s, 1, 3);
+    mfma_row(0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(s, 1, 0); read_a(s, 1, 1);
+    mfma_row(0, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    read_a(s, 1, 2); read_a(s, 1, 3);
+    mfma_row(0, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    if (next) {
+      // stage kt+1 landed (all waves), and every wave is done with stage kt-1, whose buffer the next DMA refills
+      wait_stage(KT - 2 - kt < NSTAGE - 3 ? KT - 2 - kt : NSTAGE - 3);
+      __syncthreads();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // phase B: ks1 MFMAs (set 1); DMA of stage kt+3 and the ks0 fragments of stage kt+1 (set 0)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (issue) dma_one(kt + NSTAGE - 1, 2 * i);
+      if (next) read_b(sn, 0, i);
+      acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][i], fb[1][0], acc[i][0], 0, 0, 0);
+      acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][i], fb[1][1], acc[i][1], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (issue) dma_one(kt + NSTAGE - 1, 2 * i + 1);
+      if (next) read_a(sn, 0, i);
+      acc[i][2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][i], fb[1][2], acc[i][2], 0, 0, 0);
+      acc[i][3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][i], fb[1][3], acc[i][3], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  const bool full = (m0 + BM <= M) && (n0 + BN <= N);
+  // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 128 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
+        const int col = n0 + wn * 128 + j * 32 + (lane & 31);
+        if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
+      }
+}
+
+template <typename AT, typename BT, typename CT, int K>
+static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, const BT* __restrict__ B,
+                                                     CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
+                                                     _Float16* smem) {
+  constexpr int BM = 256, BN = 256, BK = 64, WN = 2, NTHREADS = 256, TI = 4, TJ = 4;
+  constexpr int PITCH = BK + 8, KC = BK / 8, A_IT = BM * BK / 8 / NTHREADS, NBLK = BK * BN / 64;
   constexpr int B_IT = (NBLK + NTHREADS - 1) / NTHREADS;
-  typedef @AT@ AT;
-  typedef @BT@ BT;
-  const AT* __restrict__ A = @A@;
-  const BT* __restrict__ B = @B@;
-  @CT@* __restrict__ C = @C@;
-  const int ldb = (int)@LDB@;
-  const int M = (int)__eas_m_eff, N = (int)__eas_n_eff;
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * PITCH];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[2][BN * PITCH];
+  _Float16* As0 = smem;  // [2][BM * PITCH]
+  _Float16* Bs0 = smem + 2 * BM * PITCH;  // [2][BN * PITCH]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  // XCD-contiguous, M-grouped tile order
-  const int tilesM = (M + BM - 1) / BM, tilesN = (N + BN - 1) / BN, T = tilesM * tilesN;
-  const int w = blockIdx.x;
-  const int t = (T % 8 == 0) ? (w % 8) * (T / 8) + w / 8 : w;
-  constexpr int GROUP_M = 4;
-  const int gsize = GROUP_M * tilesN, g = t / gsize, first_m = g * GROUP_M;
-  const int gm = min(tilesM - first_m, GROUP_M);
-  const int ty = first_m + (t % gsize) % gm, tx = (t % gsize) / gm;
-  const int m0 = ty * BM, n0 = tx * BN;
   // 16-byte vector loads need aligned rows and base pointers; anything else takes the masked path
   const bool mn_full = (m0 + BM <= M) && (n0 + BN <= N) && (ldb % 8 == 0) && (K % 8 == 0) &&
                        ((((uint64_t)A) | ((uint64_t)B)) % 32 == 0);
@@ -89,39 +261,13 @@ extern "C" __global__ __launch_bounds__(@THREADS@) void @NAME@(
       for (int r = 0; r < 8; ++r) rb[i][r] = eas_load8<BT>(B + (size_t)(k0 + kg * 8 + r) * ldb + n0 + nc * 8);
     }
   };
-  auto gload_masked = [&](int k0) {
+  auto sstore_regs = [&](int buf) {
+    _Float16* As = As0 + buf * BM * PITCH;
+    _Float16* Bs = Bs0 + buf * BN * PITCH;
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + NTHREADS * i, row = c / KC, kc = c % KC;
-      const int gm_ = m0 + row, gk = k0 + kc * 8;
-      eas_h8 v;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (gm_ < M && gk + e < K) ? (_Float16)A[(size_t)gm_ * K + gk + e] : (_Float16)0.0f;
-      ra[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < B_IT; ++i) {
-      const int blk = tid + NTHREADS * i, kg = blk % KC, nc = blk / KC;
-      if (NBLK % NTHREADS != 0 && blk >= NBLK) break;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int gk = k0 + kg * 8 + r, gn = n0 + nc * 8;
-        eas_h8 v;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (gk < K && gn + e < N) ? (_Float16)B[(size_t)gk * ldb + gn + e] : (_Float16)0.0f;
-        rb[i][r] = v;
-      }
-    }
-  };
-  auto gload = [&](int k0) {
-    if (mn_full && k0 + BK <= K) gload_fast(k0);
-    else gload_masked(k0);
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_IT; ++i) {
-      const int c = tid + NTHREADS * i, row = c / KC, kc = c % KC;
-      *(eas_h8*)(&As[buf][row * PITCH + kc * 8]) = ra[i];
+      *(eas_h8*)(&As[row * PITCH + kc * 8]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {
@@ -132,63 +278,144 @@ extern "C" __global__ __launch_bounds__(@THREADS@) void @NAME@(
         eas_h8 col;
 #pragma unroll
         for (int r = 0; r < 8; ++r) col[r] = rb[i][r][j];
-        *(eas_h8*)(&Bs[buf][(nc * 8 + j) * PITCH + kg * 8]) = col;
+        *(eas_h8*)(&Bs[(nc * 8 + j) * PITCH + kg * 8]) = col;
       }
     }
   };
-
+  // edge tiles and the K tail: element loads with zero fill, written straight to LDS
+  // (rolled loops keep register pressure low; these tiles are few)
+  auto sstore_masked = [&](int buf, int k0) {
+    _Float16* As = As0 + buf * BM * PITCH;
+    _Float16* Bs = Bs0 + buf * BN * PITCH;
+#pragma unroll 1
+    for (int i = 0; i < A_IT; ++i) {
+      const int c = tid + NTHREADS * i, row = c / KC, kc = c % KC;
+      const int gm_ = m0 + row, gk = k0 + kc * 8;
+      eas_h8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (gm_ < M && gk + e < K) ? (_Float16)A[(size_t)gm_ * K + gk + e] : (_Float16)0.0f;
+      *(eas_h8*)(&As[row * PITCH + kc * 8]) = v;
+    }
+#pragma unroll 1
+    for (int i = 0; i < B_IT; ++i) {
+      const int blk = tid + NTHREADS * i, kg = blk % KC, nc = blk / KC;
+      if (NBLK % NTHREADS != 0 && blk >= NBLK) break;
+      const int gn = n0 + nc * 8;
+#pragma unroll 1
+      for (int j = 0; j < 8; ++j) {
+        eas_h8 col;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int gk = k0 + kg * 8 + r;
+          col[r] = (gk < K && gn + j < N) ? (_Float16)B[(size_t)gk * ldb + gn + j] : (_Float16)0.0f;
+        }
+        *(eas_h8*)(&Bs[(nc * 8 + j) * PITCH + kg * 8]) = col;
+      }
+    }
+  };
   eas_f32x16 acc[TI][TJ];
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
     for (int j = 0; j < TJ; ++j) acc[i][j] = (eas_f32x16){};
 
-  constexpr int KT = (K + BK - 1) / BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * BK);
+  constexpr int KT = (K + BK - 1) / BK, KFULL = K / BK;
+  auto compute = [&](int kt) {
+    const _Float16* As = As0 + (kt & 1) * BM * PITCH;
+    const _Float16* Bs = Bs0 + (kt & 1) * BN * PITCH;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       eas_h8 a[TI], b[TJ];
       const int kk = ks * 16 + (lane >> 5) * 8;
 #pragma unroll
-      for (int i = 0; i < TI; ++i) a[i] = *(const eas_h8*)&As[buf][(wm * (BM / WM) + i * 32 + (lane & 31)) * PITCH + kk];
+      for (int i = 0; i < TI; ++i) a[i] = *(const eas_h8*)&As[(wm * 128 + i * 32 + (lane & 31)) * PITCH + kk];
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) b[j] = *(const eas_h8*)&Bs[buf][(wn * (BN / WN) + j * 32 + (lane & 31)) * PITCH + kk];
+      for (int j = 0; j < TJ; ++j) b[j] = *(const eas_h8*)&Bs[(wn * 128 + j * 32 + (lane & 31)) * PITCH + kk];
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < KT) sstore(buf ^ 1);
+  };
+  if (mn_full) {
+    // interior tile: full k-tiles stage through registers, loads issued before the current MFMAs
+    if (KFULL > 0) {
+      gload_fast(0);
+      sstore_regs(0);
+    } else {
+      sstore_masked(0, 0);
+    }
     __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      const bool next_fast = kt + 1 < KFULL;
+      if (next_fast) gload_fast((kt + 1) * BK);
+      compute(kt);
+      if (next_fast) sstore_regs((kt + 1) & 1);
+      else if (kt + 1 < KT) sstore_masked((kt + 1) & 1, (kt + 1) * BK);  // the K tail
+      __syncthreads();
+    }
+  } else {
+    sstore_masked(0, 0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+      compute(kt);
+      if (kt + 1 < KT) sstore_masked((kt + 1) & 1, (kt + 1) * BK);
+      __syncthreads();
+    }
   }
-  // epilogue: lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
     for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * (BM / WM) + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
-        const int col = n0 + wn * (BN / WN) + j * 32 + (lane & 31);
-        if (mn_full || (row < M && col < N)) C[(size_t)row * ldb + col] = (@CT@)acc[i][j][r];
+        const int row = m0 + wm * 128 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
+        const int col = n0 + wn * 128 + j * 32 + (lane & 31);
+        if (mn_full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
       }
+}
+
+extern "C" __global__ __launch_bounds__(256) void @NAME@(
+    @PARAMS@) {
+  constexpr int BM = 256, BN = 256, K = @K@;
+  constexpr bool F16_IN = @F16_IN@;
+  typedef @AT@ AT;
+  typedef @BT@ BT;
+  typedef @CT@ CT;
+  const AT* __restrict__ A = @A@;
+  const BT* __restrict__ B = @B@;
+  CT* __restrict__ C = @C@;
+  const int ldb = (int)@LDB@;
+  const int M = (int)__eas_m_eff, N = (int)__eas_n_eff;
+  // one LDS array for both bodies: DMA ring 4 x 2 x 16 KB, register body 2 x 2 x 256 x 72 halves
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 2 * 256 * 72];
+  // XCD-contiguous, M-grouped tile order
+  const int tilesM = (M + BM - 1) / BM, tilesN = (N + BN - 1) / BN, T = tilesM * tilesN;
+  const int w = blockIdx.x;
+  const int t = (T % 8 == 0) ? (w % 8) * (T / 8) + w / 8 : w;
+  constexpr int GROUP_M = 4;
+  const int gsize = GROUP_M * tilesN, g = t / gsize, first_m = g * GROUP_M;
+  const int gm = min(tilesM - first_m, GROUP_M);
+  const int ty = first_m + (t % gsize) % gm, tx = (t % gsize) / gm;
+  const int m0 = ty * BM, n0 = tx * BN;
+  if constexpr (F16_IN) {
+    const bool dma_ok = (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0) &&
+                        ((uint64_t)M * K * 2 < (1ull << 31)) && ((uint64_t)K * ldb * 2 < (1ull << 31));
+    if (dma_ok) {
+      eas_gemm_dma<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
+      return;
+    }
+  }
+  eas_gemm_regs<AT, BT, CT, K>(A, B, C, ldb, M, N, m0, n0, smem);
 }
 """
 
-# Tile configurations (BM, BN, WM, WN); measured on MI355X, see the DESIGN notes.
-CONFIGS = {
-    "large": (256, 256, 2, 2),
-    "medium": (128, 256, 2, 2),
-}
+TILE = (256, 256)  # BM, BN
+THREADS = 256
 
 
 def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
-    bm, bn, wm, wn = CONFIGS["large"]
+    bm, bn = TILE
     # Parameters keep the user's order (kernel arguments are positional) but get
     # private names, so user names cannot collide with the template's locals.
     params = []
@@ -201,15 +428,12 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         else:
             params.append(f"const {ctype(arg.dtype)} __eas_a{i}")
     params += ["const uint32_t __eas_m_eff", "const uint32_t __eas_n_eff"]
+    f16_in = spec.a_dtype == DType.F16 and spec.b_dtype == DType.F16
     subs = {
         "@NAME@": ir.name,
-        "@THREADS@": str(wm * wn * 64),
         "@PARAMS@": ",\n    ".join(params),
-        "@BM@": str(bm),
-        "@BN@": str(bn),
-        "@WM@": str(wm),
-        "@WN@": str(wn),
         "@K@": str(spec.K),
+        "@F16_IN@": "true" if f16_in else "false",
         "@AT@": ctype(spec.a_dtype),
         "@BT@": ctype(spec.b_dtype),
         "@CT@": ctype(spec.c_dtype),
@@ -224,8 +448,8 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
     header = (f"// Lifted from eas kernel `{ir.name}`: proven dense GEMM C[M,N] = A[M,{spec.K}] @ B[{spec.K},N]\n"
               f"// (A={spec.a}, B={spec.b}, C={spec.c}, M={spec.m_sym}, N={spec.n_sym}, reference tile "
               f"{spec.TM}x{spec.TN} rows on program_id({spec.row_axis})).\n")
-    geo = Geometry("gemm", ir.name, block, wm * wn * 64, params={
+    geo = Geometry("gemm", ir.name, block, THREADS, params={
         "m_sym": spec.m_sym, "n_sym": spec.n_sym, "K": spec.K, "TM": spec.TM, "TN": spec.TN,
-        "row_axis": spec.row_axis, "BM": bm, "BN": bn, "threads": wm * wn * 64,
+        "row_axis": spec.row_axis, "BM": bm, "BN": bn, "threads": THREADS,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

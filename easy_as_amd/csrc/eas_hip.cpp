@@ -5,16 +5,26 @@
 // hipModuleLoadData and launched with hipModuleLaunchKernel from a packed
 // kernel-argument blob.  No Python in here; see hip_module.cpp for the
 // CPython binding.
+//
+// hiprtc is loaded with dlmopen into a link namespace of its own.  A process
+// that already holds another hiprtc/comgr pair (PyTorch wheels bundle an older
+// one with the same SONAMEs) would otherwise hand us that copy, and with it an
+// older LLVM; hiprtc itself has no HIP-runtime dependency, so a private copy
+// touches no GPU state.
 
 #include "eas_hip.h"
 
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include <dlfcn.h>
+#include <link.h>
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -94,6 +104,72 @@ void export_deleter(DLManagedTensor* self) {
   delete self;
 }
 
+// ---- hiprtc, resolved at first use -----------------------------------------
+struct Rtc {
+  hiprtcResult (*create)(hiprtcProgram*, const char*, const char*, int, const char**, const char**) = nullptr;
+  hiprtcResult (*compile)(hiprtcProgram, int, const char**) = nullptr;
+  hiprtcResult (*log_size)(hiprtcProgram, size_t*) = nullptr;
+  hiprtcResult (*log)(hiprtcProgram, char*) = nullptr;
+  hiprtcResult (*code_size)(hiprtcProgram, size_t*) = nullptr;
+  hiprtcResult (*code)(hiprtcProgram, char*) = nullptr;
+  hiprtcResult (*destroy)(hiprtcProgram*) = nullptr;
+  const char* (*error_string)(hiprtcResult) = nullptr;
+  hiprtcResult (*version)(int*, int*) = nullptr;
+  std::string path;
+  std::string error;
+  bool ok = false;
+};
+
+bool bind_rtc(Rtc& r, void* h) {
+  r.create = reinterpret_cast<decltype(r.create)>(dlsym(h, "hiprtcCreateProgram"));
+  r.compile = reinterpret_cast<decltype(r.compile)>(dlsym(h, "hiprtcCompileProgram"));
+  r.log_size = reinterpret_cast<decltype(r.log_size)>(dlsym(h, "hiprtcGetProgramLogSize"));
+  r.log = reinterpret_cast<decltype(r.log)>(dlsym(h, "hiprtcGetProgramLog"));
+  r.code_size = reinterpret_cast<decltype(r.code_size)>(dlsym(h, "hiprtcGetCodeSize"));
+  r.code = reinterpret_cast<decltype(r.code)>(dlsym(h, "hiprtcGetCode"));
+  r.destroy = reinterpret_cast<decltype(r.destroy)>(dlsym(h, "hiprtcDestroyProgram"));
+  r.error_string = reinterpret_cast<decltype(r.error_string)>(dlsym(h, "hiprtcGetErrorString"));
+  r.version = reinterpret_cast<decltype(r.version)>(dlsym(h, "hiprtcVersion"));
+  return r.create && r.compile && r.log_size && r.log && r.code_size && r.code && r.destroy && r.error_string &&
+         r.version;
+}
+
+const Rtc& rtc() {
+  static Rtc r;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    std::vector<std::string> candidates;
+    if (const char* e = getenv("EAS_HIPRTC_LIB")) candidates.emplace_back(e);
+    if (const char* e = getenv("ROCM_PATH")) candidates.emplace_back(std::string(e) + "/lib/libhiprtc.so.7");
+    candidates.emplace_back("/opt/rocm/lib/libhiprtc.so.7");
+    for (const std::string& c : candidates) {
+      void* h = dlmopen(LM_ID_NEWLM, c.c_str(), RTLD_NOW | RTLD_LOCAL);
+      if (!h) {
+        const char* d = dlerror();
+        r.error += c + ": " + (d ? d : "dlmopen failed") + "; ";
+        continue;
+      }
+      if (bind_rtc(r, h)) {
+        r.path = c;
+        r.ok = true;
+        return;
+      }
+      r.error += c + ": missing hiprtc symbols; ";
+      dlclose(h);
+    }
+    // last resort: whatever hiprtc the process can load in its own namespace
+    if (void* h = dlopen("libhiprtc.so.7", RTLD_NOW | RTLD_LOCAL)) {
+      if (bind_rtc(r, h)) {
+        r.path = "libhiprtc.so.7";
+        r.ok = true;
+        return;
+      }
+    }
+    r.error += "libhiprtc.so.7: not loadable";
+  });
+  return r;
+}
+
 }  // namespace
 
 extern "C" {
@@ -135,39 +211,56 @@ int eas_hip_device_props_get(int device, eas_hip_device_props* out) {
 int eas_hip_compile_source(const char* src, const char* name, const char* const* options, int noptions, void** code,
                            size_t* code_size, char* log, size_t loglen) {
   if (!src || !code || !code_size) return fail(EAS_HIP_ERR_INVALID, "src/code/code_size must not be NULL");
+  if (noptions < 0 || (noptions > 0 && !options)) return fail(EAS_HIP_ERR_INVALID, "bad options array");
   if (log && loglen) log[0] = 0;
+  const Rtc& rt = rtc();
+  if (!rt.ok) return fail(EAS_HIP_ERR_COMPILE, "hiprtc not available: %s", rt.error.c_str());
   hiprtcProgram prog;
-  hiprtcResult r = hiprtcCreateProgram(&prog, src, name ? name : "eas_kernel.hip", 0, nullptr, nullptr);
-  if (r != HIPRTC_SUCCESS) return fail(EAS_HIP_ERR_COMPILE, "hiprtcCreateProgram: %s", hiprtcGetErrorString(r));
-  r = hiprtcCompileProgram(prog, noptions, const_cast<const char**>(options));
+  hiprtcResult r = rt.create(&prog, src, name ? name : "eas_kernel.hip", 0, nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS) return fail(EAS_HIP_ERR_COMPILE, "hiprtcCreateProgram: %s", rt.error_string(r));
+  r = rt.compile(prog, noptions, const_cast<const char**>(options));
   size_t lsz = 0;
-  hiprtcGetProgramLogSize(prog, &lsz);
+  rt.log_size(prog, &lsz);
   std::string text(lsz, '\0');
-  if (lsz) hiprtcGetProgramLog(prog, &text[0]);
+  if (lsz) rt.log(prog, &text[0]);
   if (log && loglen) {
     size_t n = text.size() < loglen - 1 ? text.size() : loglen - 1;
     memcpy(log, text.data(), n);
     log[n] = 0;
   }
   if (r != HIPRTC_SUCCESS) {
-    hiprtcDestroyProgram(&prog);
-    return fail(EAS_HIP_ERR_COMPILE, "hiprtc compile of %s failed: %s", name ? name : "kernel", hiprtcGetErrorString(r));
+    rt.destroy(&prog);
+    return fail(EAS_HIP_ERR_COMPILE, "hiprtc compile of %s failed: %s", name ? name : "kernel", rt.error_string(r));
   }
   size_t sz = 0;
-  r = hiprtcGetCodeSize(prog, &sz);
+  r = rt.code_size(prog, &sz);
   if (r != HIPRTC_SUCCESS || sz == 0) {
-    hiprtcDestroyProgram(&prog);
+    rt.destroy(&prog);
     return fail(EAS_HIP_ERR_COMPILE, "hiprtc produced no code");
   }
   void* buf = malloc(sz);
   if (!buf) {
-    hiprtcDestroyProgram(&prog);
+    rt.destroy(&prog);
     return fail(EAS_HIP_ERR_NOMEM, "out of host memory");
   }
-  hiprtcGetCode(prog, static_cast<char*>(buf));
-  hiprtcDestroyProgram(&prog);
+  rt.code(prog, static_cast<char*>(buf));
+  rt.destroy(&prog);
   *code = buf;
   *code_size = sz;
+  return EAS_HIP_OK;
+}
+
+int eas_hip_compiler_version(int* major, int* minor, char* path, size_t pathlen) {
+  if (!major || !minor) return fail(EAS_HIP_ERR_INVALID, "major/minor must not be NULL");
+  const Rtc& rt = rtc();
+  if (!rt.ok) return fail(EAS_HIP_ERR_COMPILE, "hiprtc not available: %s", rt.error.c_str());
+  hiprtcResult r = rt.version(major, minor);
+  if (r != HIPRTC_SUCCESS) return fail(EAS_HIP_ERR_COMPILE, "hiprtcVersion: %s", rt.error_string(r));
+  if (path && pathlen) {
+    size_t n = rt.path.size() < pathlen - 1 ? rt.path.size() : pathlen - 1;
+    memcpy(path, rt.path.data(), n);
+    path[n] = 0;
+  }
   return EAS_HIP_OK;
 }
 

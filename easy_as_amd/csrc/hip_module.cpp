@@ -309,6 +309,18 @@ PyObject* py_compile_to_code(PyObject*, PyObject* args) {
   return out;
 }
 
+// compiler_version() -> (major, minor, path) of the hiprtc in use; no GPU required.
+PyObject* py_compiler_version(PyObject*, PyObject*) {
+  int major = 0, minor = 0;
+  char path[1024];
+  int rc = eas_hip_compiler_version(&major, &minor, path, sizeof(path));
+  if (rc) {
+    PyErr_Format(PyExc_RuntimeError, "%s", eas_hip_last_error());
+    return nullptr;
+  }
+  return Py_BuildValue("(iis)", major, minor, path);
+}
+
 // load(code: bytes, name) -> kernel capsule
 PyObject* py_load(PyObject*, PyObject* args) {
   Py_buffer code;
@@ -747,6 +759,7 @@ PyMethodDef kMethods[] = {
     {"is_available", py_is_available, METH_NOARGS, "1 if a HIP GPU is usable."},
     {"device_props", py_device_props, METH_VARARGS, "Properties of a device (default: current)."},
     {"compile_to_code", py_compile_to_code, METH_VARARGS, "hiprtc: source -> code object bytes (no GPU needed)."},
+    {"compiler_version", py_compiler_version, METH_NOARGS, "(major, minor, path) of the hiprtc in use."},
     {"load", py_load, METH_VARARGS, "Load a code object and look up a kernel."},
     {"compile", py_compile, METH_VARARGS, "compile_to_code + load."},
     {"kernel_attrs", py_kernel_attrs, METH_VARARGS, "Static resources of a loaded kernel."},

@@ -65,9 +65,21 @@ def _cache_dir() -> Path:
     return Path(d) if d else Path.home() / ".cache" / "easy_as_amd"
 
 
+def _compiler_tag(mod: Any) -> str:
+    get = getattr(mod, "compiler_version", None)
+    if get is None:
+        return "unknown"
+    major, minor, path = get()
+    return f"hiprtc-{major}.{minor}:{path}"
+
+
 def compile_code(mod: Any, src: str, entry: str, options: tuple[str, ...] = COMPILE_OPTIONS) -> bytes:
-    """hiprtc-compile ``src`` to a gfx950 code object, through the on-disk cache."""
-    key = hashlib.sha256("\0".join((src, entry, *options, str(getattr(mod, "ABI_VERSION", 0)))).encode()).hexdigest()
+    """hiprtc-compile ``src`` to a gfx950 code object, through the on-disk cache.
+
+    The cache key covers the source, entry, options, the extension's ABI version
+    and the hiprtc version/path, so a different compiler never reuses old code."""
+    key = hashlib.sha256("\0".join((src, entry, *options, str(getattr(mod, "ABI_VERSION", 0)),
+                                     _compiler_tag(mod))).encode()).hexdigest()
     path = _cache_dir() / f"{key}.co"
     if os.environ.get("EAS_HIP_DISABLE_CACHE", "") not in ("", "0") or not path.exists():
         code = mod.compile_to_code(src, f"{entry}.hip", list(options))

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define EAS_HIP_ABI_VERSION 1
+#define EAS_HIP_ABI_VERSION 2
 
 typedef enum eas_hip_status {
   EAS_HIP_OK = 0,
@@ -81,6 +81,12 @@ int eas_hip_compile_source(const char* src, const char* name, const char* const*
 
 /* Release memory returned by eas_hip_compile_source. */
 void eas_hip_free_host(void* p);
+
+/* Version of the hiprtc that eas_hip_compile_source uses, and the path it was
+ * loaded from (copied into `path`, truncated to pathlen).  No reference
+ * counterpart: Metal's compiler is part of the OS; here the code-object cache
+ * key includes it.  Returns EAS_HIP_ERR_COMPILE if no hiprtc can be loaded. */
+int eas_hip_compiler_version(int* major, int* minor, char* path, size_t pathlen);
 
 /* Load a code object on the current device and look up `name`.
  * Replaces the library->pipeline half of `compile(src, name)` (_metal.mm:236-260). */

@@ -40,7 +40,10 @@ def _check(c, a, b, m, n, k):
 
 @pytest.mark.parametrize("mnk,tile", [((64, 64, 64), (32, 32, 8)), ((300, 520, 200), (32, 32, 8)),
                                       ((33, 17, 100), (32, 32, 16)), ((257, 300, 72), (16, 32, 8)),
-                                      ((512, 512, 512), (32, 64, 16))])
+                                      ((512, 512, 512), (32, 64, 16)),
+                                      # HBM->LDS path: M/N edge tiles, K tail of 8, K below one stage
+                                      ((257, 264, 72), (32, 32, 8)), ((130, 136, 8), (32, 32, 8)),
+                                      ((64, 520, 24), (32, 32, 8)), ((520, 256, 1000), (32, 32, 8))])
 def test_lifted_mma_matmul_matches_f64(gpu_runtime, mnk, tile):
     m, n, k = mnk
     bm, bn, bk = tile
@@ -50,6 +53,18 @@ def test_lifted_mma_matmul_matches_f64(gpu_runtime, mnk, tile):
     a, b = _inputs(m, n, k)
     c = np.full(m * n, np.nan, np.float32)
     _mma(K.matmul_mma_kernel, a, b, c, m, n, k, bm, bn, bk)
+    _check(c, a, b, m, n, k)
+
+
+def test_rows_past_k_are_never_read(gpu_runtime):
+    # B is followed by NaN padding and A rows end where the next begins: a K-tail
+    # stage that read past K would put NaN (B) or wrong values (A) into C.
+    m, n, k = 96, 128, 40
+    a, b = _inputs(m, n, k)
+    b_pad = np.concatenate([b, np.full(64 * n, np.nan, np.float16)])
+    c = np.zeros(m * n, np.float32)
+    _mma(K.matmul_mma_kernel, a, b_pad, c, m, n, k)
+    assert np.isfinite(c).all()
     _check(c, a, b, m, n, k)
 
 
