@@ -14,6 +14,12 @@ on a bounded sample).  Secondary measurements ride along under ``extra``.
 ``--workload copy|fma|read|write`` measures the other elementwise kernels the same way
 (``copy`` is the known-size kernel that calibrates HBM byte counters; ``read`` and
 ``write`` measure one-direction HBM streaming on the same GPU).
+
+``--workload mma`` makes the f16-input / f32-accumulate simdgroup-MMA matmul at
+M=N=K=4096 (configs[3]; lifted to the MFMA GEMM) the primary line, with the
+roofline against the f16 dense MFMA peak; ``mma_k4100``, ``decode``, ``prefill``,
+``tiled1024`` and ``tiled2048`` select the other matmul configurations.  The
+default run reports all of them under ``extra``.
 """
 
 from __future__ import annotations
@@ -31,6 +37,8 @@ sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2516.6  # dense f16 MFMA, MI355X
+F32_PEAK_TFLOPS = 157.3  # fp32 vector / MFMA, MI355X
 N_ELEM = 1 << 28
 PRIMARY_BLOCK = 256
 
@@ -44,6 +52,23 @@ WORKLOADS = {
 }
 
 
+# matmul configurations: (kernel in tests/kernels.py, M, N, K, A distribution, B distribution, description)
+MATMULS = {
+    "mma": ("matmul_mma_kernel", 4096, 4096, 4096, "u", "u",
+            "f16-in/f32-acc simdgroup-MMA matmul (mk.dot), M=N=K=4096, f32 out"),
+    "mma_k4100": ("matmul_mma_kernel", 4096, 4096, 4100, "u", "u",
+                  "f16-in/f32-acc simdgroup-MMA matmul (mk.dot), M=N=4096, K=4100, f32 out"),
+    "decode": ("matmul_mma_f16out_kernel", 16, 14336, 4096, "act", "w",
+               "f16 LLM decode linear M=16 N=14336 K=4096 (mk.dot), f32 acc, f16 out"),
+    "prefill": ("matmul_mma_f16out_kernel", 8192, 8192, 8192, "act", "w",
+                "f16 LLM prefill linear M=N=K=8192 (mk.dot), f32 acc, f16 out"),
+    "tiled1024": ("matmul_tiled_kernel", 1024, 1024, 1024, "n", "n",
+                  "fp32 tiled matmul (threadgroup tiles -> LDS, 32x32 tiles), M=N=K=1024"),
+    "tiled2048": ("matmul_tiled_kernel", 2048, 2048, 2048, "n", "n",
+                  "fp32 tiled matmul (threadgroup tiles -> LDS, 32x32 tiles), M=N=K=2048"),
+}
+
+
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -52,20 +77,121 @@ def _inputs(n: int, seeds: tuple[int, ...]) -> list[np.ndarray]:
     return [np.random.default_rng(s).standard_normal(n, dtype=np.float32) for s in seeds]
 
 
-def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch) -> tuple[float, float]:
+def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch, **launch) -> tuple[float, float]:
     """(wall ms/step bracketed by device syncs, HIP-event ms/launch on the launch stream)."""
     for _ in range(warmup):
-        rt.run(ck, rargs, meta, sync=False)
+        rt.run(ck, rargs, meta, sync=False, **launch)
     rt.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        rt.run(ck, rargs, meta, sync=False)
+        rt.run(ck, rargs, meta, sync=False, **launch)
     rt.synchronize()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    ev_ms = rt.benchmark(ck, rargs, meta, repeat=steps, warmup=0) * 1e3
+    ev_ms = rt.benchmark(ck, rargs, meta, repeat=steps, warmup=0, **launch) * 1e3
     return wall_ms, ev_ms
+
+
+def _matmul_inputs(name: str) -> tuple[np.ndarray, np.ndarray]:
+    _, m, n, k, da, db, _ = MATMULS[name]
+    rng_a, rng_b = np.random.default_rng(10), np.random.default_rng(11)
+
+    def draw(rng, dist, size):
+        if dist == "u":
+            return rng.uniform(-1, 1, size).astype(np.float16)
+        if dist == "act":
+            return rng.standard_normal(size, dtype=np.float32).astype(np.float16)
+        if dist == "w":
+            return (0.02 * rng.standard_normal(size, dtype=np.float32)).astype(np.float16)
+        return (rng.standard_normal(size, dtype=np.float32) / np.float32(np.sqrt(k))).astype(np.float32)
+
+    return draw(rng_a, da, m * k), draw(rng_b, db, k * n)
+
+
+def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
+    """Time one matmul configuration and check a seeded sample of its rows against float64."""
+    import kernels as K
+    from oracle import ops
+
+    kname, m, n, k, _, _, desc = MATMULS[name]
+    kern = getattr(K, kname)
+    dev = torch.device("cuda:0")
+    ha, hb = _matmul_inputs(name)
+    a, b = torch.from_numpy(ha).to(dev), torch.from_numpy(hb).to(dev)
+    tiled = kname == "matmul_tiled_kernel"
+    out_dt = torch.float32 if (tiled or kname == "matmul_mma_kernel") else torch.float16
+    c = torch.full((m * n,), float("nan"), dtype=out_dt, device=dev)
+    if tiled:
+        meta = {"BM": 32, "BN": 32, "BK": 32, "K": k, "NT": 256}
+        args = (a, b, c, m, n, 0, 0)
+        rargs = dict(zip(("a", "b", "c", "M", "N", "PID_M_BASE", "PID_N_BASE"), args))
+        grid = (K.cdiv(n, 32), K.cdiv(m, 32), 1)
+        tptg = (256, 1, 1)
+    else:
+        meta = {"BM": 32, "BN": 32, "BK": 8, "K": k, "NT": 512}
+        args = (a, b, c, m, n)
+        rargs = dict(zip(("a", "b", "c", "M", "N"), args))
+        grid = (K.cdiv(n, 32), K.cdiv(m, 32), 1)
+        tptg = (512, 1, 1)
+    t0 = time.perf_counter()
+    ck = kern.compile(*args, **meta)
+    compile_s = time.perf_counter() - t0
+    wall_ms, ev_ms = _time_kernel(rt, ck, rargs, meta, steps, warmup, torch, grid=grid, tptg=tptg)
+    flops = 2.0 * m * n * k
+    # parity: rows sampled with a fixed seed, float64 reference of the (rounded) inputs
+    c.fill_(float("nan"))
+    rt.run(ck, rargs, meta, grid=grid, tptg=tptg)
+    torch.cuda.synchronize()
+    got = c.float().cpu().numpy().reshape(m, n)
+    rows = np.sort(np.random.default_rng(7).choice(m, min(m, 32), replace=False))
+    ref = ops.matmul_ref(ha.reshape(m, k)[rows], hb.reshape(k, n))
+    err = ops.rel_err(got[rows].astype(np.float64), ref)
+    if tiled:
+        tol, tol_s = 1e-5 * np.sqrt(k), "1e-5*sqrt(K)"
+    elif out_dt == torch.float16:
+        tol, tol_s = 2e-2, "2e-2 (f16 output)"
+    else:
+        tol, tol_s = min(2e-2, 1e-5 * np.sqrt(k)), "min(2e-2, 1e-5*sqrt(K))"
+    ok = bool(np.isfinite(got).all() and err <= tol)
+    peak = F32_PEAK_TFLOPS if tiled else MFMA_F16_PEAK_TFLOPS
+    tf = flops / (ev_ms * 1e-3) / 1e12
+    bytes_min = (m * k + k * n) * ha.itemsize + m * n * (2 if out_dt == torch.float16 else 4)
+    res = {
+        "desc": desc, "kernel": ck.geometry.kind if ck.geometry is not None else "thread",
+        "TFLOP/s": round(tf, 1), "frac": round(tf / peak, 4), "peak_TFLOP/s": peak,
+        "wall_TFLOP/s": round(flops / (wall_ms * 1e-3) / 1e12, 1), "ms_per_launch": round(ev_ms, 5),
+        "min_hbm_GB/s": round(bytes_min / (ev_ms * 1e-3) / 1e9, 1),
+        "parity": f"max rel err {err:.2e} on 32 sampled rows vs float64 (tol {tol_s})" + ("" if ok else " FAIL"),
+        "parity_ok": ok, "compile_s": round(compile_s, 1),
+    }
+    _log(f"{name}: {res['TFLOP/s']} TFLOP/s ({100 * res['frac']:.1f}% of {peak}), {ev_ms:.4f} ms/launch, "
+         f"parity {res['parity']}, compile {compile_s:.1f} s")
+    del a, b, c
+    torch.cuda.empty_cache()
+    return res
+
+
+def _matmul_cpu_baseline(seconds: float = 10.0) -> dict:
+    """The oracle's float64 matmul (numpy) on 512^3 samples of the f16 inputs, one BLAS thread."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import ops
+
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1, 1, (512, 512)).astype(np.float16)
+    b = rng.uniform(-1, 1, (512, 512)).astype(np.float16)
+    with threadpool_limits(1):
+        ops.matmul_ref(a, b)
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            ops.matmul_ref(a, b)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or reps >= 2000:
+                break
+    return {"value": round(2 * 512 ** 3 * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"oracle matmul_ref (numpy float64, 1 BLAS thread) on 512x512x512 f16 inputs, {reps} reps, {el:.1f} s"}
 
 
 def _cpu_baseline(workload: str, seconds: float = 10.0) -> dict:
@@ -109,7 +235,7 @@ def main() -> int:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", choices=sorted(WORKLOADS), default="add")
+    p.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(MATMULS), default="add")
     p.add_argument("--block", type=int, default=PRIMARY_BLOCK)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
@@ -126,6 +252,8 @@ def main() -> int:
 
     rt = get_runtime("hip")
     dev = torch.device("cuda:0")
+    if args.workload in MATMULS:
+        return _matmul_main(args, rt, torch)
     kname, nin, per_elem = WORKLOADS[args.workload]
     kern = getattr(K, kname)
     _log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}; generating inputs N=2^28")
@@ -170,6 +298,12 @@ def main() -> int:
         _log(f"fma: event {fe:.4f} ms/launch, {16 * N_ELEM / fe / 1e6:.1f} GB/s, parity {extra['fma_n2e28']['parity']}")
         del cc, d
 
+    if not args.no_extra and args.workload == "add":
+        del ins, out
+        torch.cuda.empty_cache()
+        for name in ("mma", "mma_k4100", "decode", "prefill", "tiled1024", "tiled2048"):
+            extra[name] = _matmul(name, rt, torch, max(5, min(args.steps, 20)), max(2, min(args.warmup, 5)))
+
     bytes_per_launch = per_elem * N_ELEM
     traffic = None
     pmc = ROOT / "profiles" / f"{args.workload}_f32_n2e28.pmc.json"
@@ -205,6 +339,39 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0 if exact else 1
+
+
+def _matmul_main(args, rt, torch) -> int:
+    res = _matmul(args.workload, rt, torch, args.steps, args.warmup)
+    _, m, n, k, _, _, desc = MATMULS[args.workload]
+    traffic = None
+    pmc = ROOT / "profiles" / f"{args.workload}_f16.pmc.json"
+    if pmc.exists():
+        traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
+    tiled = args.workload.startswith("tiled")
+    wall_tf = res["wall_TFLOP/s"]
+    line = {
+        "metric": f"{'fp32' if tiled else 'f16'} matmul TFLOP/s @{m}x{n}x{k} (eas kernel, one MI355X)",
+        "value": wall_tf,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(2.0 * m * n * k / (wall_tf * 1e12) * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if tiled else "f16",
+        "data": "synthetic (seeded; see config)",
+        "config": {"workload": desc, "M": m, "N": n, "K": k, "parallelism": "single GPU"},
+        "parity": res["parity"],
+        "roofline": {"bound": "valu" if tiled else "mfma", "achieved": res["TFLOP/s"], "peak": res["peak_TFLOP/s"],
+                     "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic},
+        "cpu_baseline": None if args.no_cpu_baseline else _matmul_cpu_baseline(),
+        "extra": {},
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if res["parity_ok"] else 1
 
 
 if __name__ == "__main__":
