@@ -96,7 +96,7 @@ def fmaf_rto(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
         fix = inexact & even
         toward = np.where(e > 0, np.inf, -np.inf)
         s = np.where(fix, np.nextafter(s, toward), s)
-    return s.astype(np.float32)
+        return s.astype(np.float32)  # results past the binary32 range become inf
 
 
 def dot_f32(a: np.ndarray, b: np.ndarray) -> np.float32:

@@ -195,6 +195,17 @@ def tptg_independent_kernel(out, N, BLOCK: eas.constexpr):
 
 
 @eas.kernel
+def add2d_shape_kernel(a, b, c, M, N, BLOCK: eas.constexpr):
+    """2-D add whose grid comes from ``_shape`` (tests/test_grid_infer.py:25-32)."""
+    tile = mk.program_id(0)
+    row = mk.program_id(1)
+    col = tile * BLOCK + mk.tid(0, BLOCK)
+    offs = row * N + col
+    mask = mk.where(row < M, col < N, False)
+    mk.store(c, offs, mk.load(a, offs, mask) + mk.load(b, offs, mask), mask)
+
+
+@eas.kernel
 def add2d_hw_kernel(a, b, c, H, W, BLOCK: eas.constexpr):
     tile = mk.program_id(0)
     row = mk.program_id(1)

@@ -1,0 +1,284 @@
+"""Host side of the boundary, on the CPU: the C-ABI library, launch planning,
+kernel-argument packing, autotune and grid inference.
+
+No GPU compute happens here.  The C-ABI checks call only entry points that need
+no device (symbol export, ABI version, hiprtc compilation, error returns); the
+runtime checks drive ``HipRuntime`` through a recording stand-in for the
+``_hip`` extension.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import importlib
+import re
+import struct
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import eas
+import kernels as K
+from eas import mk
+from easy_as_amd.runtime.grid import infer_grid, infer_nthreads
+from easy_as_amd.runtime.hip import HipRuntime, plan_launch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "eas_hip.h"
+LIB = ROOT / "easy_as_amd" / "libeas_hip.so"
+# the module (the package re-exports a function of the same name)
+eas_kernel = importlib.import_module("easy_as_amd.kernel")
+
+
+def _declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(eas_hip_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is not built; run __graft_entry__.build()")
+    return ctypes.CDLL(str(LIB))
+
+
+# ---- C ABI -------------------------------------------------------------------
+
+def test_header_declares_the_boundary():
+    names = _declared_functions()
+    for required in ("eas_hip_is_available", "eas_hip_compile_source", "eas_hip_kernel_load", "eas_hip_launch",
+                     "eas_hip_alloc", "eas_hip_free", "eas_hip_copy_h2d", "eas_hip_copy_d2h", "eas_hip_dlpack_view",
+                     "eas_hip_dlpack_make", "eas_hip_stream_synchronize", "eas_hip_event_elapsed_ms"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version_matches_header(lib):
+    m = re.search(r"#define\s+EAS_HIP_ABI_VERSION\s+(\d+)", HEADER.read_text())
+    assert m and lib.eas_hip_abi_version() == int(m.group(1))
+
+
+def test_compile_source_without_gpu(lib):
+    lib.eas_hip_compile_source.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p),
+                                           ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
+                                           ctypes.POINTER(ctypes.c_size_t), ctypes.c_char_p, ctypes.c_size_t]
+    opts = (ctypes.c_char_p * 2)(b"--offload-arch=gfx950", b"-O3")
+    code, size = ctypes.c_void_p(), ctypes.c_size_t()
+    log = ctypes.create_string_buffer(4096)
+    src = b'extern "C" __global__ void k(float* x) { x[threadIdx.x] += 1.0f; }'
+    rc = lib.eas_hip_compile_source(src, b"k.hip", opts, 2, ctypes.byref(code), ctypes.byref(size), log, 4096)
+    assert rc == 0, log.value
+    head = ctypes.string_at(code, 4)
+    lib.eas_hip_free_host.argtypes = [ctypes.c_void_p]
+    lib.eas_hip_free_host(code)
+    assert head == b"\x7fELF" and size.value > 0
+    # a syntax error is EAS_HIP_ERR_COMPILE (-3) with the compiler log filled in
+    rc = lib.eas_hip_compile_source(b"this is not C++", b"bad.hip", opts, 2, ctypes.byref(code),
+                                    ctypes.byref(size), log, 4096)
+    assert rc == -3 and b"error" in log.value
+
+
+def test_null_arguments_are_invalid(lib):
+    lib.eas_hip_last_error.restype = ctypes.c_char_p
+    lib.eas_hip_compile_source.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+    assert lib.eas_hip_compile_source(None, None, None, 0, None, None, None, 0) == -1
+    assert b"must not be NULL" in lib.eas_hip_last_error()
+    lib.eas_hip_compiler_version.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t]
+    assert lib.eas_hip_compiler_version(None, None, None, 0) == -1
+
+
+def test_compiler_version_is_rocm_hiprtc(lib):
+    major, minor = ctypes.c_int(), ctypes.c_int()
+    path = ctypes.create_string_buffer(512)
+    lib.eas_hip_compiler_version.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                                             ctypes.c_char_p, ctypes.c_size_t]
+    assert lib.eas_hip_compiler_version(ctypes.byref(major), ctypes.byref(minor), path, 512) == 0
+    assert major.value >= 7 and path.value.endswith(b"libhiprtc.so.7")
+
+
+def test_no_device_paths_fail_cleanly(lib):
+    if lib.eas_hip_is_available() != 0:
+        pytest.skip("a GPU is visible; the no-device contract is checked only on CPU hosts")
+    buf = ctypes.c_void_p()
+    lib.eas_hip_alloc.argtypes = [ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]
+    assert lib.eas_hip_alloc(1024, 0, ctypes.byref(buf)) == -2  # EAS_HIP_ERR_NODEV
+
+
+# ---- grid inference (reference known answers) --------------------------------
+
+def test_infer_grid_from_h_w():
+    ck = K.add2d_hw_kernel.compile(np.zeros(1, np.float32), np.zeros(1, np.float32), np.zeros(1, np.float32),
+                                   17, 103, BLOCK=32)
+    assert infer_grid(ck.ir, {"H": 17, "W": 103}, ck.block_size) == (4, 17, 1)
+
+
+def test_infer_grid_from_shape_option():
+    ck = K.add2d_shape_kernel.compile(np.zeros(1, np.float32), np.zeros(1, np.float32), np.zeros(1, np.float32),
+                                      9, 65, BLOCK=16)
+    assert infer_grid(ck.ir, {}, ck.block_size, shape=(9, 65)) == (5, 9, 1)
+
+
+def test_infer_nthreads_rules():
+    assert infer_nthreads({"N": 1031}) == 1031
+    assert infer_nthreads({"N": 1031}, nthreads=7) == 7
+    with pytest.raises(Exception):
+        infer_nthreads({})
+
+
+# ---- launch planning ------------------------------------------------------------
+
+def _add_ck(block=256):
+    z = np.zeros(1, np.float32)
+    return K.add_kernel.compile(z, z, z, 1031, BLOCK=block)
+
+
+def test_plan_spmd_add_packs_programs():
+    ck = _add_ck()
+    n = 1 << 28
+    plan = plan_launch(ck, {"N": n})
+    geo = ck.geometry
+    programs = -(-n // 256)
+    assert plan.hidden == (programs,)
+    assert plan.grid == (-(-programs // (geo.programs_per_wg * geo.unroll)), 1, 1)
+    assert plan.block == (geo.wg_size, 1, 1)
+    # the workgroup's lanes cover its programs' BLOCK elements exactly
+    assert (256 * geo.programs_per_wg) % geo.wg_size == 0
+
+
+def test_plan_zero_extent_and_tptg_rules():
+    ck = _add_ck()
+    assert plan_launch(ck, {"N": 0}) is None
+    assert plan_launch(ck, {"N": 10}, grid=(0, 1, 1)) is None
+    with pytest.raises(ValueError):
+        plan_launch(ck, {"N": 10}, tptg=(256, 1, 1))  # SPMD kernels take (1,1,1)
+    tck = K.tptg_independent_kernel.compile(np.zeros(1, np.float32), 10, BLOCK=64)
+    assert tck.launch_mode == "thread"
+    plan = plan_launch(tck, {"N": 1000}, tptg=(64, 1, 1))
+    assert plan.grid == (16, 1, 1) and plan.block == (64, 1, 1) and plan.hidden == (1000,)
+    with pytest.raises(ValueError):
+        plan_launch(tck, {"N": 1000}, tptg=(1, 1, 1))
+
+
+def test_plan_lifted_gemm_covers_the_reference_rectangle():
+    f16, f32 = np.zeros(1, np.float16), np.zeros(1, np.float32)
+    ck = K.matmul_mma_kernel.compile(f16, f16, f32, 300, 520, BM=32, BN=32, BK=8, K=200, NT=512)
+    assert ck.geometry.kind == "gemm"
+    plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(17, 10, 1))
+    assert plan.hidden == (300, 520) and plan.grid == (2 * 3, 1, 1) and plan.block == (256, 1, 1)
+    plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(3, 2, 1))  # partial grid: 64 x 96 rectangle
+    assert plan.hidden == (64, 96) and plan.grid == (1, 1, 1)
+
+
+# ---- kernel-argument packing through a recording extension ------------------------
+
+class _RecordingExt:
+    ABI_VERSION = 2
+
+    def __init__(self):
+        self.launches, self.h2d, self.d2h, self.allocs = [], [], [], []
+
+    def alloc_buffer(self, nbytes, storage):
+        self.allocs.append((nbytes, storage))
+        return ("buf", len(self.allocs))
+
+    def copy_from_host(self, buf, arr):
+        self.h2d.append((buf, arr.nbytes))
+
+    def copy_to_host(self, buf, arr):
+        self.d2h.append((buf, arr.nbytes))
+
+    def compile_to_code(self, src, name, options):
+        return b"\x7fELF-recorded"
+
+    def load(self, code, entry):
+        return ("kernel", entry)
+
+    def launch(self, kernel, argv, writable, grid, block, stream=None):
+        self.launches.append((kernel, list(argv), list(writable), grid, block))
+
+    def launch_async(self, kernel, argv, writable, grid, block, stream=None):
+        self.launch(kernel, argv, writable, grid, block, stream)
+        return ("pending", len(self.launches))
+
+    def synchronize(self, pending):
+        pass
+
+    def queue_synchronize(self, stream=None):
+        pass
+
+
+def test_numpy_add_argv_contract(monkeypatch, tmp_path):
+    monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
+    ext = _RecordingExt()
+    rt = HipRuntime(ext=ext)
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    n = 1031
+    a = np.ones(n, np.float32)
+    b = np.ones(n, np.float32)
+    c = np.zeros(n, np.float32)
+    K.add_kernel(a, b, c, n, BLOCK=256)
+    assert len(ext.launches) == 1
+    kern, argv, writable, grid, block = ext.launches[0]
+    assert kern == ("kernel", "add_kernel")
+    # IR argument order (a, b, c, N) then the hidden program count
+    assert argv[:3] == [("buf", 1), ("buf", 2), ("buf", 3)]
+    assert argv[3] == struct.pack("<I", n) and argv[4] == struct.pack("<I", 5)
+    assert writable == [False, False, True, False, False]
+    # numpy inputs are staged; only the written buffer is copied back (a synchronous launch)
+    assert [nb for _, nb in ext.h2d] == [4 * n] * 3
+    assert ext.d2h == [(("buf", 3), 4 * n)]
+
+
+def test_scalar_packing_errors(monkeypatch, tmp_path):
+    monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
+    rt = HipRuntime(ext=_RecordingExt())
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    x = np.zeros(8, np.float32)
+    with pytest.raises((OverflowError, ValueError, struct.error)):
+        K.add_kernel(x, x, x, 1 << 32, BLOCK=256)
+    with pytest.raises(TypeError):
+        K.add_kernel(x.astype(np.float64), x, x, 8, BLOCK=256)
+
+
+# ---- autotune ----------------------------------------------------------------------
+
+class _TimingRuntime:
+    """Benchmarks cost 1/BLOCK seconds; records what ran."""
+
+    def __init__(self):
+        self.benchmarked, self.ran = [], []
+
+    def benchmark(self, ck, runtime_args, meta, *, repeat, warmup=0, **_):
+        self.benchmarked.append(int(meta["BLOCK"]))
+        return {64: 3.0, 128: 2.0, 256: 1.0, 1024: 1.5}[int(meta["BLOCK"])]
+
+    def run(self, ck, runtime_args, meta, **_):
+        self.ran.append(int(meta["BLOCK"]))
+
+
+@eas.autotune(configs=[eas.Config(meta={"BLOCK": b}) for b in (64, 128, 256, 1024)], key=["N"], warmup=0, repeat=1)
+@eas.kernel
+def _tuned_add(a, b, c, N, BLOCK: eas.constexpr = 64):
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.arange(0, BLOCK)
+    mask = offs < N
+    mk.store(c, offs, mk.load(a, offs, mask) + mk.load(b, offs, mask), mask)
+
+
+def test_autotune_benchmarks_once_per_key_and_keeps_fastest(monkeypatch):
+    rt = _TimingRuntime()
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    x = np.zeros(2000, np.float32)
+    _tuned_add(x, x, x, 1027)
+    assert sorted(rt.benchmarked) == [64, 128, 256, 1024] and rt.ran == [256]
+    _tuned_add(x, x, x, 1027)
+    assert len(rt.benchmarked) == 4 and rt.ran == [256, 256]
+    _tuned_add(x, x, x, 2000)  # a new key value is tuned again
+    assert len(rt.benchmarked) == 8 and rt.ran[-1] == 256
