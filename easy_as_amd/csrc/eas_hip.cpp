@@ -10,7 +10,10 @@
 // that already holds another hiprtc/comgr pair (PyTorch wheels bundle an older
 // one with the same SONAMEs) would otherwise hand us that copy, and with it an
 // older LLVM; hiprtc itself has no HIP-runtime dependency, so a private copy
-// touches no GPU state.
+// touches no GPU state.  The namespace has its own libc, whose `environ` is the
+// main program's environment array as it was at dlmopen time; setenv in the
+// main program can reallocate (free) that array, so every call into hiprtc
+// first points the namespace's `environ` at the current array (under a lock).
 
 #include "eas_hip.h"
 
@@ -19,6 +22,7 @@
 
 #include <dlfcn.h>
 #include <link.h>
+#include <unistd.h>
 
 #include <cstdarg>
 #include <cstdio>
@@ -115,9 +119,20 @@ struct Rtc {
   hiprtcResult (*destroy)(hiprtcProgram*) = nullptr;
   const char* (*error_string)(hiprtcResult) = nullptr;
   hiprtcResult (*version)(int*, int*) = nullptr;
+  char*** ns_environ = nullptr;  // `environ` of the namespace's libc (null when not in a namespace)
   std::string path;
   std::string error;
   bool ok = false;
+};
+
+std::mutex g_rtc_mutex;
+
+// Held around every call into hiprtc: serialises them and refreshes the namespace's environment.
+struct RtcCall {
+  std::lock_guard<std::mutex> lock;
+  explicit RtcCall(const Rtc& r) : lock(g_rtc_mutex) {
+    if (r.ns_environ) *r.ns_environ = environ;
+  }
 };
 
 bool bind_rtc(Rtc& r, void* h) {
@@ -150,6 +165,15 @@ const Rtc& rtc() {
         continue;
       }
       if (bind_rtc(r, h)) {
+        Lmid_t lmid;
+        if (dlinfo(h, RTLD_DI_LMID, &lmid) == 0) {
+          if (void* ns_libc = dlmopen(lmid, "libc.so.6", RTLD_NOW | RTLD_NOLOAD))
+            r.ns_environ = reinterpret_cast<char***>(dlsym(ns_libc, "environ"));
+        }
+        if (!r.ns_environ) {  // cannot keep its environment current: do not use this copy
+          r.error += c + ": namespace libc `environ` not found; ";
+          continue;
+        }
         r.path = c;
         r.ok = true;
         return;
@@ -215,6 +239,7 @@ int eas_hip_compile_source(const char* src, const char* name, const char* const*
   if (log && loglen) log[0] = 0;
   const Rtc& rt = rtc();
   if (!rt.ok) return fail(EAS_HIP_ERR_COMPILE, "hiprtc not available: %s", rt.error.c_str());
+  RtcCall guard(rt);
   hiprtcProgram prog;
   hiprtcResult r = rt.create(&prog, src, name ? name : "eas_kernel.hip", 0, nullptr, nullptr);
   if (r != HIPRTC_SUCCESS) return fail(EAS_HIP_ERR_COMPILE, "hiprtcCreateProgram: %s", rt.error_string(r));
@@ -254,6 +279,7 @@ int eas_hip_compiler_version(int* major, int* minor, char* path, size_t pathlen)
   if (!major || !minor) return fail(EAS_HIP_ERR_INVALID, "major/minor must not be NULL");
   const Rtc& rt = rtc();
   if (!rt.ok) return fail(EAS_HIP_ERR_COMPILE, "hiprtc not available: %s", rt.error.c_str());
+  RtcCall guard(rt);
   hiprtcResult r = rt.version(major, minor);
   if (r != HIPRTC_SUCCESS) return fail(EAS_HIP_ERR_COMPILE, "hiprtcVersion: %s", rt.error_string(r));
   if (path && pathlen) {

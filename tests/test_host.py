@@ -103,6 +103,30 @@ def test_compiler_version_is_rocm_hiprtc(lib):
     assert major.value >= 7 and path.value.endswith(b"libhiprtc.so.7")
 
 
+def test_compile_after_environment_grows():
+    # hiprtc lives in a private link namespace with its own libc; growing the
+    # environment (setenv reallocates the array) must not leave it reading freed memory
+    import subprocess
+    import sys
+
+    script = (
+        "import os\n"
+        "os.environ['EAS_T_PRE'] = '1'\n"
+        "from easy_as_amd.runtime.hip_ext import load_hip_ext\n"
+        "m = load_hip_ext(require=True)\n"
+        "src = 'extern \"C\" __global__ void k(float* x) { x[threadIdx.x] = %s; }'\n"
+        "opts = ['--offload-arch=gfx950', '-O3']\n"
+        "m.compile_to_code(src % '1.0f', 'k.hip', opts)\n"
+        "for i in range(300): os.environ[f'EAS_T_GROW_{i}'] = 'x' * 64\n"
+        "m.compiler_version()\n"
+        "assert m.compile_to_code(src % '2.0f', 'k.hip', opts)[:4] == b'\\x7fELF'\n"
+        "print('ok')\n"
+    )
+    r = subprocess.run([sys.executable, "-c", script], cwd=ROOT, capture_output=True, text=True, timeout=300,
+                       env={**__import__("os").environ, "PYTHONPATH": str(ROOT)})
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), (r.returncode, r.stderr[-2000:])
+
+
 def test_no_device_paths_fail_cleanly(lib):
     if lib.eas_hip_is_available() != 0:
         pytest.skip("a GPU is visible; the no-device contract is checked only on CPU hosts")
