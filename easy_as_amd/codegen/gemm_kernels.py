@@ -24,7 +24,8 @@ matrix under 2 GiB):
   DMA issue (one every two MFMAs) and the next stage's ks0 fragment reads.
 
 Register body (any other case, including f32 inputs that MFMA consumes as f16):
-global -> registers -> LDS, BK = 64, double buffered; B is transposed in
+global -> registers -> LDS, BK = 64, double buffered; A loads use the widest
+vector (up to 16 bytes) that K's row alignment allows; B is transposed in
 registers (each thread loads an 8(k) x 8(n) block) so LDS holds B as [n][k];
 edge tiles and the K tail load element by element with zero fill straight into
 LDS.
@@ -61,6 +62,35 @@ template <> __device__ __forceinline__ eas_h8 eas_load8<float>(const float* p) {
   v[0] = (_Float16)lo[0]; v[1] = (_Float16)lo[1]; v[2] = (_Float16)lo[2]; v[3] = (_Float16)lo[3];
   v[4] = (_Float16)hi[0]; v[5] = (_Float16)hi[1]; v[6] = (_Float16)hi[2]; v[7] = (_Float16)hi[3];
   return v;
+}
+
+// elements per load for rows of `k` elements of T: the widest power of two up to 16 bytes dividing k
+template <typename T> constexpr int eas_row_vec(int k) {
+  int v = 16 / (int)sizeof(T);
+  while (v > 1 && k % v != 0) v /= 2;
+  return v;
+}
+// 8 consecutive elements from rows whose alignment allows AL-element vector loads
+template <typename T, int AL> static __device__ __forceinline__ eas_h8 eas_load8_al(const T* p) {
+  if constexpr (AL >= 8 && sizeof(T) == 2) {
+    return *(const eas_h8*)p;
+  } else if constexpr (AL == 1) {
+    eas_h8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (_Float16)p[e];
+    return v;
+  } else {
+    constexpr int W = AL > 8 ? 8 : AL;
+    typedef T vec_t __attribute__((ext_vector_type(W)));
+    eas_h8 v;
+#pragma unroll
+    for (int e = 0; e < 8; e += W) {
+      const vec_t x = *(const vec_t*)(p + e);
+#pragma unroll
+      for (int i = 0; i < W; ++i) v[e + i] = (_Float16)x[i];
+    }
+    return v;
+  }
 }
 
 // raw buffer resource: base, range in bytes (reads at or past it return 0), gfx9 word 3
@@ -242,16 +272,18 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
   _Float16* Bs0 = smem + 2 * BM * PITCH;  // [2][BN * PITCH]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  // 16-byte vector loads need aligned rows and base pointers; anything else takes the masked path
-  const bool mn_full = (m0 + BM <= M) && (n0 + BN <= N) && (ldb % 8 == 0) && (K % 8 == 0) &&
-                       ((((uint64_t)A) | ((uint64_t)B)) % 32 == 0);
+  // A rows (length K, compile time) load A_AL elements per vector; B rows need 16-byte vectors
+  // (ldb a multiple of 16 bytes, aligned base).  Anything else takes the masked element path.
+  constexpr int A_AL = eas_row_vec<AT>(K);
+  const bool mn_full = (m0 + BM <= M) && (n0 + BN <= N) && (ldb % (16 / (int)sizeof(BT)) == 0) &&
+                       ((uint64_t)B % 16 == 0) && ((uint64_t)A % (A_AL * sizeof(AT)) == 0);
 
   eas_h8 ra[A_IT], rb[B_IT][8];
   auto gload_fast = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + NTHREADS * i, row = c / KC, kc = c % KC;
-      ra[i] = eas_load8<AT>(A + (size_t)(m0 + row) * K + k0 + kc * 8);
+      ra[i] = eas_load8_al<AT, A_AL>(A + (size_t)(m0 + row) * K + k0 + kc * 8);
     }
 #pragma unroll
     for (int i = 0; i < B_IT; ++i) {

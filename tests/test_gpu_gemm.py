@@ -43,7 +43,9 @@ def _check(c, a, b, m, n, k):
                                       ((512, 512, 512), (32, 64, 16)),
                                       # HBM->LDS path: M/N edge tiles, K tail of 8, K below one stage
                                       ((257, 264, 72), (32, 32, 8)), ((130, 136, 8), (32, 32, 8)),
-                                      ((64, 520, 24), (32, 32, 8)), ((520, 256, 1000), (32, 32, 8))])
+                                      ((64, 520, 24), (32, 32, 8)), ((520, 256, 1000), (32, 32, 8)),
+                                      # register body: A rows 4-byte aligned (K % 8 = 2) and 2-byte (odd K)
+                                      ((300, 256, 50), (32, 32, 8)), ((260, 264, 33), (32, 32, 8))])
 def test_lifted_mma_matmul_matches_f64(gpu_runtime, mnk, tile):
     m, n, k = mnk
     bm, bn, bk = tile
