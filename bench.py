@@ -157,8 +157,13 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
     peak = F32_PEAK_TFLOPS if tiled else MFMA_F16_PEAK_TFLOPS
     tf = flops / (ev_ms * 1e-3) / 1e12
     bytes_min = (m * k + k * n) * ha.itemsize + m * n * (2 if out_dt == torch.float16 else 4)
+    # roofline: HBM-bound below the ridge point (peak flop/s / peak bytes/s), compute-bound above
+    hbm_bound = flops / bytes_min < peak * 1e12 / (HBM_PEAK_GBS * 1e9)
+    gbs = bytes_min / (ev_ms * 1e-3) / 1e9
     res = {
         "desc": desc, "kernel": ck.geometry.kind if ck.geometry is not None else "thread",
+        "bound": "hbm" if hbm_bound else ("valu" if tiled else "mfma"),
+        "frac_of_bound": round(gbs / HBM_PEAK_GBS if hbm_bound else tf / peak, 4),
         "TFLOP/s": round(tf, 1), "frac": round(tf / peak, 4), "peak_TFLOP/s": peak,
         "wall_TFLOP/s": round(flops / (wall_ms * 1e-3) / 1e12, 1), "ms_per_launch": round(ev_ms, 5),
         "min_hbm_GB/s": round(bytes_min / (ev_ms * 1e-3) / 1e9, 1),
@@ -365,8 +370,10 @@ def _matmul_main(args, rt, torch) -> int:
         "data": "synthetic (seeded; see config)",
         "config": {"workload": desc, "M": m, "N": n, "K": k, "parallelism": "single GPU"},
         "parity": res["parity"],
-        "roofline": {"bound": "valu" if tiled else "mfma", "achieved": res["TFLOP/s"], "peak": res["peak_TFLOP/s"],
-                     "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic},
+        "roofline": ({"bound": "hbm", "achieved": res["min_hbm_GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": res["frac_of_bound"], "traffic": traffic} if res["bound"] == "hbm" else
+                     {"bound": res["bound"], "achieved": res["TFLOP/s"], "peak": res["peak_TFLOP/s"],
+                      "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic}),
         "cpu_baseline": None if args.no_cpu_baseline else _matmul_cpu_baseline(),
         "extra": {},
     }

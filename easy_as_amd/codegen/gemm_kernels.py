@@ -261,6 +261,128 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
       }
 }
 
+// Skinny path (M <= 16, decode-like): one workgroup per 64 columns, the four waves split K.
+// Each wave streams its K range of B (and A) HBM -> LDS into a private 4-stage ring (no
+// barriers in the loop), multiplies with v_mfma_f32_16x16x32_f16 (B transposed by
+// ds_read_b64_tr_b16), and the waves add their 16 x 64 partial sums through LDS at the end.
+template <typename CT, int K>
+static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                                                           CT* __restrict__ C, int ldb, int M, int N, _Float16* smem) {
+  typedef float eas_f32x4_acc __attribute__((ext_vector_type(4)));
+  constexpr int NT = 64, KS = 32, NST = 4;
+  constexpr int KW = ((K + 4 * KS - 1) / (4 * KS)) * KS;  // k rows per wave
+  constexpr int BST = KS * NT, AST = 16 * KS, STH = BST + AST;  // halves per stage: B [32][64], A [16][32]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * NT;
+  const int kb = wave * KW, ke = min(K, kb + KW);
+  const int nsteps = ke > kb ? (ke - kb + KS - 1) / KS : 0;
+  _Float16* ws = smem + wave * NST * STH;
+  const uint32_t lds_ws = (uint32_t)(size_t)(EAS_LDS _Float16*)ws;
+  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
+  const eas_rsrc rb = eas_make_rsrc(B, (uint32_t)K * (uint32_t)ldb * 2u);
+  // B DMA q: rows 8q + lane/8 of the stage, chunk lane%8 stored at chunk ^ s(row),
+  // s(r) = 2((r/2)%2) + 4((r/8)%2) keeps each 16-lane transposed read conflict free
+  uint32_t b_off[4];
+  int b_row[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 8 * q + (lane >> 3);
+    const int lc = (lane & 7) ^ (2 * ((r >> 1) & 1) + 4 * ((r >> 3) & 1));
+    b_row[q] = r;
+    b_off[q] = ((uint32_t)r * (uint32_t)ldb + (uint32_t)(n0 + lc * 8)) * 2u;
+  }
+  // A DMA: row lane/4, chunk lane%4 stored at chunk ^ ((row/4)%4)
+  const int a_m = lane >> 2, a_lc = (lane & 3) ^ ((a_m >> 2) & 3);
+  const uint32_t a_off = ((uint32_t)a_m * (uint32_t)K + (uint32_t)(a_lc * 8)) * 2u;
+  auto dma_step = [&](int t) {
+    const int k0 = kb + t * KS;
+    const uint32_t dst = lds_ws + (uint32_t)((t % NST) * STH) * 2u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t off = b_off[q] + (uint32_t)k0 * (uint32_t)ldb * 2u;
+      if (k0 + b_row[q] >= ke) off = 0x80000000u;  // another wave's rows, or past K: zeros
+      eas_dma16(rb, off, dst + q * 1024);
+    }
+    uint32_t off = a_off + (uint32_t)k0 * 2u;
+    if (k0 + a_lc * 8 >= ke) off = 0x80000000u;
+    eas_dma16(ra, off, dst + BST * 2);
+  };
+  // 16x16x32 operands: A lane l holds A[l%16][8(l/16)..+7]; B lane l holds B[8(l/16)..+7][l%16]
+  const int fm = lane & 15;
+  const int fa = fm * KS + (((lane >> 4) ^ ((fm >> 2) & 3)) * 8);
+  int fb[4][2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int g = lane >> 4, kq = lane & 15;
+      const int row = 8 * g + 4 * h + (kq >> 2), col = 16 * j + 4 * (kq & 3);
+      const int pc = (col >> 3) ^ (2 * ((row >> 1) & 1) + 4 * ((row >> 3) & 1));
+      fb[j][h] = row * NT + pc * 8 + (col & 7);
+    }
+  eas_f32x4_acc acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = (eas_f32x4_acc){};
+#pragma unroll
+  for (int p = 0; p < NST - 1; ++p)
+    if (p < nsteps) dma_step(p);
+  for (int t = 0; t < nsteps; ++t) {
+    // this wave's step t landed; up to NST-2 newer steps (5 loads each) stay in flight
+    const int later = min(NST - 2, nsteps - 1 - t);
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(10));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(5));
+    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+    if (t + NST - 1 < nsteps) dma_step(t + NST - 1);  // refills the stage read at step t-1
+    const _Float16* st = ws + (t % NST) * STH;
+    const eas_h8 a = *(const eas_h8*)(st + BST + fa);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(st + fb[j][0]));
+      const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(st + fb[j][1]));
+      const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
+      const eas_h8 b = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+    }
+  }
+  __syncthreads();
+  // 16x16 D layout: lane l, register r holds (row 4(l/16) + r, col l%16)
+  float* red = (float*)smem;  // [4 waves][16][64]
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(wave * 16 + 4 * (lane >> 4) + r) * NT + 16 * j + (lane & 15)] = acc[j][r];
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int idx = tid + 256 * e, row = idx >> 6, col = idx & 63;
+    const float sum = (red[row * NT + col] + red[(16 + row) * NT + col]) +
+                      (red[(32 + row) * NT + col] + red[(48 + row) * NT + col]);
+    if (row < M && n0 + col < N) C[(size_t)row * ldb + n0 + col] = (CT)sum;
+  }
+}
+
+// Skinny path for inputs the DMA cannot take (f32 or unaligned): one thread per (column, 4 rows).
+template <typename AT, typename BT, typename CT, int K>
+static __device__ __forceinline__ void eas_gemm_skinny_simple(const AT* __restrict__ A, const BT* __restrict__ B,
+                                                              CT* __restrict__ C, int ldb, int M, int N) {
+  const int tid = threadIdx.x, col = blockIdx.x * 64 + (tid & 63), r0 = tid >> 6;
+  if (col >= N) return;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k = 0; k < K; ++k) {
+    const float b = (float)(_Float16)B[(size_t)k * ldb + col];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = r0 + 4 * i;
+      const float a = row < M ? (float)(_Float16)A[(size_t)row * K + k] : 0.0f;
+      acc[i] = __builtin_fmaf(a, b, acc[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (r0 + 4 * i < M) C[(size_t)(r0 + 4 * i) * ldb + col] = (CT)acc[i];
+}
+
 template <typename AT, typename BT, typename CT, int K>
 static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, const BT* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
@@ -409,7 +531,7 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
 
 extern "C" __global__ __launch_bounds__(256) void @NAME@(
     @PARAMS@) {
-  constexpr int BM = 256, BN = 256, K = @K@;
+  constexpr int BM = 256, BN = 256, K = @K@, SKINNY_M = @SKINNY_M@;
   constexpr bool F16_IN = @F16_IN@;
   typedef @AT@ AT;
   typedef @BT@ BT;
@@ -419,8 +541,21 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   CT* __restrict__ C = @C@;
   const int ldb = (int)@LDB@;
   const int M = (int)__eas_m_eff, N = (int)__eas_n_eff;
-  // one LDS array for both bodies: DMA ring 4 x 2 x 16 KB, register body 2 x 2 x 256 x 72 halves
+  // one LDS array for all bodies: DMA ring 4 x 2 x 16 KB, register body 2 x 2 x 256 x 72 halves,
+  // skinny path 4 waves x 4 stages x 5 KB
   __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 2 * 256 * 72];
+  const bool dma_ok = F16_IN && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0) &&
+                      ((uint64_t)M * K * 2 < (1ull << 31)) && ((uint64_t)K * ldb * 2 < (1ull << 31));
+  if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns
+    if constexpr (F16_IN) {
+      if (dma_ok) {
+        eas_gemm_skinny_dma<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
+        return;
+      }
+    }
+    eas_gemm_skinny_simple<AT, BT, CT, K>(A, B, C, ldb, M, N);
+    return;
+  }
   // XCD-contiguous, M-grouped tile order
   const int tilesM = (M + BM - 1) / BM, tilesN = (N + BN - 1) / BN, T = tilesM * tilesN;
   const int w = blockIdx.x;
@@ -431,8 +566,6 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   const int ty = first_m + (t % gsize) % gm, tx = (t % gsize) / gm;
   const int m0 = ty * BM, n0 = tx * BN;
   if constexpr (F16_IN) {
-    const bool dma_ok = (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0) &&
-                        ((uint64_t)M * K * 2 < (1ull << 31)) && ((uint64_t)K * ldb * 2 < (1ull << 31));
     if (dma_ok) {
       eas_gemm_dma<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
       return;
@@ -444,6 +577,8 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
 
 TILE = (256, 256)  # BM, BN
 THREADS = 256
+SKINNY_M = 16  # m_eff at or below this runs the skinny path: one workgroup per SKINNY_N columns
+SKINNY_N = 64
 
 
 def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
@@ -461,8 +596,10 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
             params.append(f"const {ctype(arg.dtype)} __eas_a{i}")
     params += ["const uint32_t __eas_m_eff", "const uint32_t __eas_n_eff"]
     f16_in = spec.a_dtype == DType.F16 and spec.b_dtype == DType.F16
+    assert SKINNY_N == 64, "the skinny path's tile width is fixed by its LDS layout"
     subs = {
         "@NAME@": ir.name,
+        "@SKINNY_M@": str(SKINNY_M),
         "@PARAMS@": ",\n    ".join(params),
         "@K@": str(spec.K),
         "@F16_IN@": "true" if f16_in else "false",
@@ -483,5 +620,6 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
     geo = Geometry("gemm", ir.name, block, THREADS, params={
         "m_sym": spec.m_sym, "n_sym": spec.n_sym, "K": spec.K, "TM": spec.TM, "TN": spec.TN,
         "row_axis": spec.row_axis, "BM": bm, "BN": bn, "threads": THREADS,
+        "skinny_m": SKINNY_M, "skinny_n": SKINNY_N,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

@@ -759,6 +759,10 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
     n_eff = min(N, g_cols * p["TN"])
     if m_eff == 0 or n_eff == 0:
         return None
-    bm, bn = p["BM"], p["BN"]
-    tiles = -(-m_eff // bm) * -(-n_eff // bn)
+    if m_eff <= p.get("skinny_m", 0):
+        # the kernel's skinny path: one workgroup per skinny_n columns, all rows
+        tiles = -(-n_eff // p["skinny_n"])
+    else:
+        bm, bn = p["BM"], p["BN"]
+        tiles = -(-m_eff // bm) * -(-n_eff // bn)
     return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), (m_eff, n_eff))

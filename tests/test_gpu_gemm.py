@@ -58,6 +58,39 @@ def test_lifted_mma_matmul_matches_f64(gpu_runtime, mnk, tile):
     _check(c, a, b, m, n, k)
 
 
+@pytest.mark.parametrize("mnk", [(1, 104, 72), (5, 640, 40), (16, 200, 1000), (12, 64, 8), (16, 136, 4096)])
+def test_skinny_path_matches_f64(gpu_runtime, mnk):
+    m, n, k = mnk
+    a, b = _inputs(m, n, k)
+    c = np.full(m * n, np.nan, np.float32)
+    _mma(K.matmul_mma_kernel, a, b, c, m, n, k)
+    _check(c, a, b, m, n, k)
+
+
+@pytest.mark.parametrize("mnk,dtype", [((7, 101, 64), np.float16), ((16, 96, 72), np.float32)])
+def test_skinny_fallback_unaligned_or_f32(gpu_runtime, mnk, dtype):
+    m, n, k = mnk  # N = 101: rows of B are not 16-byte aligned; f32 inputs are rounded to f16
+    a, b = _inputs(m, n, k, dtype)
+    c = np.full(m * n, np.nan, np.float32)
+    _mma(K.matmul_mma_kernel, a, b, c, m, n, k)
+    _check(c, a.astype(np.float16), b.astype(np.float16), m, n, k)
+
+
+def test_decode_shape_f16_out(gpu_runtime):
+    import torch
+
+    m, n, k = 16, 14336, 4096
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(m * k, dtype=np.float32).astype(np.float16)
+    b = (0.02 * rng.standard_normal(k * n, dtype=np.float32)).astype(np.float16)
+    tc = torch.full((m * n,), float("nan"), device="cuda", dtype=torch.float16)
+    _mma(K.matmul_mma_f16out_kernel, torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda(), tc, m, n, k)
+    torch.cuda.synchronize()
+    c = tc.float().cpu().numpy().reshape(m, n)
+    ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
+    assert np.isfinite(c).all() and ops.rel_err(c, ref) <= 2e-3
+
+
 def test_rows_past_k_are_never_read(gpu_runtime):
     # B is followed by NaN padding and A rows end where the next begins: a K-tail
     # stage that read past K would put NaN (B) or wrong values (A) into C.

@@ -198,6 +198,11 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
     assert plan.hidden == (300, 520) and plan.grid == (2 * 3, 1, 1) and plan.block == (256, 1, 1)
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(3, 2, 1))  # partial grid: 64 x 96 rectangle
     assert plan.hidden == (64, 96) and plan.grid == (1, 1, 1)
+    # M <= 16 (decode-like): one workgroup per 64 columns
+    plan = plan_launch(ck, {"M": 16, "N": 14336}, grid=(448, 1, 1))
+    assert plan.hidden == (16, 14336) and plan.grid == (224, 1, 1)
+    plan = plan_launch(ck, {"M": 17, "N": 14336}, grid=(448, 1, 1))
+    assert plan.hidden == (17, 14336) and plan.grid == (56, 1, 1)
 
 
 # ---- kernel-argument packing through a recording extension ------------------------
