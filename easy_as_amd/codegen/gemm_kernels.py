@@ -33,9 +33,12 @@ LDS.
 Tile order is XCD aware: workgroup w runs on XCD w % 8, so each XCD gets a
 contiguous range of tiles, grouped 4 tile-rows high for L2 reuse.
 
-The kernel computes C[m, n] for m < m_eff, n < n_eff (hidden arguments: the
-rectangle the reference launch covers).  Rows of A have length K (a compile-
-time constant); B and C rows have the scalar argument ``ldb`` as stride.
+The kernel computes C[m, n] for m in [m_lo, m_hi), n in [n_lo, n_hi) (hidden
+arguments: the rectangle the reference launch covers); it moves its base
+pointers to (m_lo, n_lo) on entry, so every body works on a sub-matrix whose
+origin is 0.  Rows of A have length K (a compile-time constant); B and C rows
+have the scalar argument ``ldb`` as stride.  B's buffer range is the extent the
+rectangle is proven to read, (K-1)*ldb + N, so tile-wide reads past it return 0.
 """
 
 from __future__ import annotations
@@ -122,7 +125,7 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
-  const eas_rsrc rb = eas_make_rsrc(B, (uint32_t)K * (uint32_t)ldb * 2u);
+  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
   // DMA instruction q = 4 wave + i writes 1 KB of a stage.  A: rows 16q + lane/4, chunk lane%4
   // stored at chunk ^ ((row/4)%4).  B: rows (k) 2q + lane/32, chunk lane%32 stored at chunk ^ 4(row%4).
   uint32_t a_off[4], b_off[4];
@@ -280,7 +283,7 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __res
   _Float16* ws = smem + wave * NST * STH;
   const uint32_t lds_ws = (uint32_t)(size_t)(EAS_LDS _Float16*)ws;
   const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
-  const eas_rsrc rb = eas_make_rsrc(B, (uint32_t)K * (uint32_t)ldb * 2u);
+  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
   // B DMA q: rows 8q + lane/8 of the stage, chunk lane%8 stored at chunk ^ s(row),
   // s(r) = 2((r/2)%2) + 4((r/8)%2) keeps each 16-lane transposed read conflict free
   uint32_t b_off[4];
@@ -536,16 +539,17 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   typedef @AT@ AT;
   typedef @BT@ BT;
   typedef @CT@ CT;
-  const AT* __restrict__ A = @A@;
-  const BT* __restrict__ B = @B@;
-  CT* __restrict__ C = @C@;
   const int ldb = (int)@LDB@;
-  const int M = (int)__eas_m_eff, N = (int)__eas_n_eff;
+  // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
+  const AT* __restrict__ A = @A@ + (size_t)__eas_m_lo * K;
+  const BT* __restrict__ B = @B@ + __eas_n_lo;
+  CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
+  const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
   // one LDS array for all bodies: DMA ring 4 x 2 x 16 KB, register body 2 x 2 x 256 x 72 halves,
   // skinny path 4 waves x 4 stages x 5 KB
   __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 2 * 256 * 72];
   const bool dma_ok = F16_IN && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0) &&
-                      ((uint64_t)M * K * 2 < (1ull << 31)) && ((uint64_t)K * ldb * 2 < (1ull << 31));
+                      ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
   if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns
     if constexpr (F16_IN) {
       if (dma_ok) {
@@ -575,9 +579,153 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
 }
 """
 
+_TEMPLATE_F32 = r"""
+typedef float eas_f32x16 __attribute__((ext_vector_type(16)));
+typedef int eas_rsrc __attribute__((ext_vector_type(4)));
+#define EAS_LDS __attribute__((address_space(3)))
+#define EAS_WAITVM(n) (((n) & 15) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+
+static __device__ __forceinline__ eas_rsrc eas_make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  eas_rsrc r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+static __device__ __forceinline__ void eas_dma16(eas_rsrc r, uint32_t voff, uint32_t lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+}
+
+extern "C" __global__ __launch_bounds__(256) void @NAME@(
+    @PARAMS@) {
+  constexpr int BM = 64, BN = 64, BK = 32, NSTAGE = 4, K = @K@, KT = (K + BK - 1) / BK;
+  constexpr int AST = BM * BK, BST = BK * BN, STF = AST + BST;  // floats per stage
+  const int ldb = (int)@LDB@;
+  // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
+  const float* __restrict__ A = @A@ + (size_t)__eas_m_lo * K;
+  const float* __restrict__ B = @B@ + __eas_n_lo;
+  float* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
+  const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
+  __shared__ __attribute__((aligned(1024))) float smem[NSTAGE * STF];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // XCD-contiguous, M-grouped tile order
+  const int tilesM = (M + BM - 1) / BM, tilesN = (N + BN - 1) / BN, T = tilesM * tilesN;
+  const int w = blockIdx.x;
+  const int t = (T % 8 == 0) ? (w % 8) * (T / 8) + w / 8 : w;
+  constexpr int GROUP_M = 8;
+  const int gsize = GROUP_M * tilesN, g = t / gsize, first_m = g * GROUP_M;
+  const int gm = min(tilesM - first_m, GROUP_M);
+  const int m0 = (first_m + (t % gsize) % gm) * BM, n0 = ((t % gsize) / gm) * BN;
+  const bool dma_ok = (K % 4 == 0) && (ldb % 4 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0) &&
+                      ((uint64_t)M * K * 4 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 4 < (1ull << 31));
+  if (!dma_ok) {
+    // rows not 16-byte aligned: each thread accumulates a 4 x 4 block with plain fmas
+    const int r0 = m0 + (tid >> 4) * 4, c0 = n0 + (tid & 15) * 4;
+    float acc[4][4] = {};
+    for (int k = 0; k < K; ++k) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = r0 + i < M ? A[(size_t)(r0 + i) * K + k] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = c0 + j < N ? B[(size_t)k * ldb + c0 + j] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (r0 + i < M && c0 + j < N) C[(size_t)(r0 + i) * ldb + c0 + j] = acc[i][j];
+    return;
+  }
+  // 4 waves of 32 x 32; v_mfma_f32_32x32x2_f32: A lane l holds A[l%32][k], B lane l holds B[k][l%32]
+  const int wm = wave >> 1, wn = wave & 1;
+  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 4u);
+  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 4u);
+  const uint32_t lds0 = (uint32_t)(size_t)(EAS_LDS float*)smem;
+  // DMA (1 KB per instruction, 2 A + 2 B per wave per stage):
+  //   A stage [64 rows][32 k]: rows 8q + lane/8, 16-byte chunk lane%8 stored at chunk ^ ((row/2)%8)
+  //   B stage [32 k][64 n]:    rows 4q + lane/16, chunk lane%16 stored at chunk ^ 8((row/16)%2)
+  uint32_t a_off[2], b_off[2];
+  int a_k[2], b_r[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = wave * 2 + i;
+    const int r = 8 * q + (lane >> 3), lc = (lane & 7) ^ ((r >> 1) & 7);
+    a_off[i] = ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)(lc * 4)) * 4u;
+    a_k[i] = lc * 4;
+    const int rr = 4 * q + (lane >> 4), lcb = (lane & 15) ^ (8 * ((rr >> 4) & 1));
+    b_off[i] = ((uint32_t)rr * (uint32_t)ldb + (uint32_t)(n0 + lcb * 4)) * 4u;
+    b_r[i] = rr;
+  }
+  auto dma = [&](int kt) {
+    const uint32_t st = lds0 + (uint32_t)((kt % NSTAGE) * STF) * 4u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t off = a_off[i] + (uint32_t)(kt * BK) * 4u;
+      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: zeros
+      eas_dma16(ra, off, st + (wave * 2 + i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t off = b_off[i] + (uint32_t)(kt * BK) * (uint32_t)ldb * 4u;
+      if (K % BK != 0 && kt * BK + b_r[i] >= K) off = 0x80000000u;
+      eas_dma16(rb, off, st + AST * 4 + (wave * 2 + i) * 1024);
+    }
+  };
+  // k order within a stage: MFMA step s (0..15) takes k = s + 16 c for lane half c = lane/32, so one
+  // ds_read_b128 gives a lane A values for four steps; B is one float of row s + 16 c per step
+  const int c = lane >> 5, ai = wm * 32 + (lane & 31), bj = wn * 32 + (lane & 31);
+  int fa[4], fb[16];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) fa[u] = ai * BK + (((4 * c + u) ^ ((ai >> 1) & 7)) * 4);
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const int row = s + 16 * c;
+    fb[s] = AST + row * BN + (((bj >> 2) ^ (8 * ((row >> 4) & 1))) * 4) + (bj & 3);
+  }
+  eas_f32x16 acc = {};
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p)
+    if (p < KT) dma(p);
+  for (int kt = 0; kt < KT; ++kt) {
+    // this wave's loads of stage kt landed (newer stages, 4 loads each, may stay in flight);
+    // the barrier makes every wave's part visible and frees stage kt-1 for the next DMA
+    const int later = min(NSTAGE - 2, KT - 1 - kt);
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));
+    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+    __syncthreads();
+    if (kt + NSTAGE - 1 < KT) dma(kt + NSTAGE - 1);
+    const float* st = smem + (kt % NSTAGE) * STF;
+    eas_f32x4 a[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) a[u] = *(const eas_f32x4*)(st + fa[u]);
+    float b[16];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) b[s] = st[fb[s]];
+#pragma unroll
+    for (int s = 0; s < 16; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s >> 2][s & 3], b[s], acc, 0, 0, 0);
+  }
+  // lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = m0 + wm * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
+    const int col = n0 + wn * 32 + (lane & 31);
+    if (row < M && col < N) C[(size_t)row * ldb + col] = acc[r];
+  }
+}
+"""
+
 TILE = (256, 256)  # BM, BN
+TILE_F32 = (64, 64)
 THREADS = 256
-SKINNY_M = 16  # m_eff at or below this runs the skinny path: one workgroup per SKINNY_N columns
+SKINNY_M = 16  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
 
 
@@ -594,9 +742,12 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
             params.append(f"{const}{ctype(arg.dtype)}* __restrict__ __eas_a{i}")
         else:
             params.append(f"const {ctype(arg.dtype)} __eas_a{i}")
-    params += ["const uint32_t __eas_m_eff", "const uint32_t __eas_n_eff"]
+    params += ["const uint32_t __eas_m_lo", "const uint32_t __eas_m_hi", "const uint32_t __eas_n_lo",
+               "const uint32_t __eas_n_hi"]
     f16_in = spec.a_dtype == DType.F16 and spec.b_dtype == DType.F16
     assert SKINNY_N == 64, "the skinny path's tile width is fixed by its LDS layout"
+    if spec.f32:
+        bm, bn = TILE_F32
     subs = {
         "@NAME@": ir.name,
         "@SKINNY_M@": str(SKINNY_M),
@@ -611,7 +762,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "@C@": pname[spec.c],
         "@LDB@": pname[spec.n_sym],
     }
-    src = _TEMPLATE
+    src = _TEMPLATE_F32 if spec.f32 else _TEMPLATE
     for k, v in subs.items():
         src = src.replace(k, v)
     header = (f"// Lifted from eas kernel `{ir.name}`: proven dense GEMM C[M,N] = A[M,{spec.K}] @ B[{spec.K},N]\n"
@@ -620,6 +771,8 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
     geo = Geometry("gemm", ir.name, block, THREADS, params={
         "m_sym": spec.m_sym, "n_sym": spec.n_sym, "K": spec.K, "TM": spec.TM, "TN": spec.TN,
         "row_axis": spec.row_axis, "BM": bm, "BN": bn, "threads": THREADS,
-        "skinny_m": SKINNY_M, "skinny_n": SKINNY_N,
+        "skinny_m": 0 if spec.f32 else SKINNY_M, "skinny_n": SKINNY_N, "row_base": spec.row_base,
+        "col_base": spec.col_base,
+        "col_masked": spec.col_masked,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

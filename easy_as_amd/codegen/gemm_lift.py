@@ -126,7 +126,7 @@ class GemmSpec:
     a: str
     b: str
     c: str
-    m_sym: str
+    m_sym: str | None      # row bound (None: rows bounded by the launched grid only)
     n_sym: str
     K: int
     TM: int
@@ -136,6 +136,10 @@ class GemmSpec:
     b_dtype: DType
     c_dtype: DType
     c_f16: bool            # output rounded to f16
+    f32: bool = False      # fp32 products and sums (the `mk.dot` tiled pattern); else f16 MFMA operands
+    row_base: str | None = None   # tile rows start at TM * (program_id + row_base) when set
+    col_base: str | None = None
+    col_masked: bool = True       # outputs/operands bounded by col < N (else by the launched grid)
 
 
 # ---------------------------------------------------------------------------
@@ -159,6 +163,10 @@ class _SymExec:
         self.frag_stores: list[tuple[int, int, np.ndarray, np.ndarray]] = []  # (tg id, frag id, base, stride)
         self.loaded: set[str] = set()
         self.stored: set[str] = set()
+        # f32 values that are sums of products of threadgroup slots (`dot` chains): value id -> terms,
+        # each term (A rec, A writer thread, B rec, B writer thread), arrays of shape (threads, k)
+        self.sums: dict[int, list[tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]]] = {}
+        self.dot_stores: list[tuple[str, Poly, Cond, list]] = []
 
     def run(self) -> None:
         for inst in self.ir.insts:
@@ -206,7 +214,9 @@ class _SymExec:
                 self.ints[out.id] = Poly.const(v, n)
             elif out.dtype == DType.BOOL:
                 self.bools[out.id] = Cond(np.full(n, bool(v)), [])
-            return  # float consts only matter if used, which is unsupported below
+            elif out.dtype == DType.F32 and float(v) == 0.0:
+                self.sums[out.id] = []
+            return  # other float consts only matter if used, which is unsupported below
         if op == "program_id":
             self.ints[out.id] = Poly({(f"%p{int(a[0])}",): np.ones(n, np.int64)})
             return
@@ -227,6 +237,31 @@ class _SymExec:
         if op in ("add", "mul") and out.dtype == DType.U32:
             x, y = self.ip(a[0]), self.ip(a[1])
             self.ints[out.id] = x.add(y) if op == "add" else x.mul(y)
+            return
+        if op == "add" and out.dtype == DType.F32:
+            if a[0].id not in self.sums or a[1].id not in self.sums:
+                raise Unsupported("f32 add of values that are not dot sums")
+            self.sums[out.id] = self.sums[a[0].id] + self.sums[a[1].id]
+            return
+        if op == "dot":
+            a_buf, a_base, a_st, b_buf, b_base, b_st, kref = a
+            if a_buf.id not in self.tg or b_buf.id not in self.tg:
+                raise Unsupported("dot operands must come from threadgroup memory")
+            if self.tg[a_buf.id][2] != DType.F32 or self.tg[b_buf.id][2] != DType.F32:
+                raise Unsupported("only f32 threadgroup tiles are lifted for dot")
+            kd = _concrete_of(self.ip(kref), n)
+            if np.any(kd != kd[0]) or kd[0] <= 0:
+                raise Unsupported("dot length differs across threads")
+            kk = np.arange(int(kd[0]), dtype=np.int64)
+            a_slots = _concrete_of(self.ip(a_base), n)[:, None] + _concrete_of(self.ip(a_st), n)[:, None] * kk[None, :]
+            b_slots = _concrete_of(self.ip(b_base), n)[:, None] + _concrete_of(self.ip(b_st), n)[:, None] * kk[None, :]
+            ar, at, _ = self.tg[a_buf.id]
+            br, bt, _ = self.tg[b_buf.id]
+            if a_slots.min() < 0 or b_slots.min() < 0 or a_slots.max() >= ar.size or b_slots.max() >= br.size:
+                raise Unsupported("dot reads outside its threadgroup tile")
+            if np.any(ar[a_slots] < 0) or np.any(br[b_slots] < 0):
+                raise Unsupported("dot reads an unwritten threadgroup slot")
+            self.sums[out.id] = [(ar[a_slots].copy(), at[a_slots].copy(), br[b_slots].copy(), bt[b_slots].copy())]
             return
         if op in ("floordiv", "mod"):
             x, y = _concrete_of(self.ip(a[0]), n), _concrete_of(self.ip(a[1]), n)
@@ -305,6 +340,11 @@ class _SymExec:
         if op == "store":
             buf, off, val, mask = a
             cond = self.bc(mask)
+            if val.id in self.sums and buf.id in self.global_bufs:
+                name = self.global_bufs[buf.id]
+                self.stored.add(name)
+                self.dot_stores.append((name, self.ip(off), cond, self.sums[val.id]))
+                return
             if val.id not in self.floats:
                 raise Unsupported("stored value is not a tracked float")
             rid = self.floats[val.id]
@@ -478,16 +518,24 @@ def _same(p: dict[Mono, np.ndarray], q: dict[Mono, np.ndarray]) -> bool:
     return True
 
 
-def _as_tile(p: dict[Mono, np.ndarray], what: str) -> tuple[str, int, np.ndarray]:
-    """``p = T * %p<axis> + r`` with r concrete; returns (axis symbol, T, r)."""
+def _as_tile(p: dict[Mono, np.ndarray], what: str) -> tuple[str, int, np.ndarray, str | None]:
+    """``p = T * (%p<axis> [+ base]) + r`` with r concrete and base one scalar argument;
+    returns (axis symbol, T, r, base symbol or None)."""
     syms = [m for m in p if m != ()]
-    if len(syms) != 1 or len(syms[0]) != 1 or not syms[0][0].startswith("%p"):
-        raise Unsupported(f"{what} index is not tile*program_id + offset")
-    T = p[syms[0]]
+    pids = [m for m in syms if len(m) == 1 and m[0].startswith("%p")]
+    bases = [m for m in syms if len(m) == 1 and not m[0].startswith("%p")]
+    if len(pids) != 1 or len(bases) > 1 or len(pids) + len(bases) != len(syms):
+        raise Unsupported(f"{what} index is not tile*(program_id + base) + offset")
+    T = p[pids[0]]
     if np.any(T != T.flat[0]) or T.flat[0] <= 0:
         raise Unsupported(f"{what} tile size differs")
+    base = None
+    if bases:
+        if not np.array_equal(p[bases[0]], T):
+            raise Unsupported(f"{what} base offset is not a whole number of tiles")
+        base = bases[0][0]
     r = p.get((), np.zeros(T.shape, np.int64))
-    return syms[0][0], int(T.flat[0]), r
+    return pids[0][0], int(T.flat[0]), r, base
 
 
 def _atoms_match(recs: list[Rec], rid: np.ndarray, thr: np.ndarray, expect: dict[Mono, np.ndarray], bound_sym: str | None,
@@ -654,8 +702,8 @@ def analyze(ir: IRModule, block: int) -> GemmSpec:
     ldb_sym = list(ldb)[0][0]
     if n_sym is not None and n_sym != ldb_sym:
         raise Unsupported("B's column bound differs from its row stride")
-    r_axis, TM, r_off = _as_tile(row_of, "row")
-    c_axis, TN, c_off = _as_tile(col_of, "col")
+    r_axis, TM, r_off, r_base = _as_tile(row_of, "row")
+    c_axis, TN, c_off, c_base = _as_tile(col_of, "col")
     if r_axis == c_axis:
         raise Unsupported("rows and cols indexed by the same program id")
 
@@ -716,7 +764,175 @@ def analyze(ir: IRModule, block: int) -> GemmSpec:
     if c_dt == DType.F16 and not c_f16:
         raise Unsupported("f16 output without an explicit conversion")
     return GemmSpec(a=a_buf, b=b_buf, c=c_name, m_sym=m_sym, n_sym=ldb_sym, K=int(K), TM=TM, TN=TN,
-                    row_axis=int(r_axis[2:]), a_dtype=a_dt, b_dtype=b_dt, c_dtype=c_dt, c_f16=bool(c_f16))
+                    row_axis=int(r_axis[2:]), a_dtype=a_dt, b_dtype=b_dt, c_dtype=c_dt, c_f16=bool(c_f16),
+                    row_base=r_base, col_base=c_base)
+
+
+def analyze_dot(ir: IRModule, block: int) -> GemmSpec:
+    """Prove that a thread-mode kernel built from ``mk.dot`` over threadgroup tiles
+    (``examples/matmul_tiled.py:27-131``) is a dense fp32 GEMM.
+
+    Every stored output must be, for its thread, the sum over k in [0, K) (each k
+    once) of A[row*K + k] * B[k*ldb + col] with f32 threadgroup tiles filled from
+    global loads masked only by ``row < M`` / ``col < N`` (k beyond K masked to
+    zero), stored to C[row*ldb + col] under ``row < M`` / ``col < N``, and the
+    outputs of one threadgroup must cover a TM x TN rectangle exactly once.
+    """
+    ops = {i.op for i in ir.insts}
+    if "dot" not in ops or ops & {"mma", "mma_zero", "mma_store"}:
+        raise Unsupported("not a dot-tile kernel")
+    ex = _SymExec(ir, block)
+    ex.run()
+    recs = ex.recs
+    if ex.stores or not ex.dot_stores:
+        raise Unsupported("outputs are not dot sums")
+    if len(ex.stored) != 1 or ex.stored & ex.loaded:
+        raise Unsupported("expected one output buffer that is not read")
+    c_name = next(iter(ex.stored))
+    a_buf = b_buf = ldb_sym = m_sym = None
+    col_masked: bool | None = None
+    row_masked_out: list[bool] = []
+    K = None
+    rows_all: list[np.ndarray] = []
+    cols_all: list[np.ndarray] = []
+    tile = None
+    for name, off, cond, terms in ex.dot_stores:
+        t = np.nonzero(cond.base)[0]
+        if t.size == 0 or not terms:
+            raise Unsupported("empty output or empty sum")
+        AR = np.concatenate([x[0] for x in terms], axis=1)[t]
+        AT = np.concatenate([x[1] for x in terms], axis=1)[t]
+        BR = np.concatenate([x[2] for x in terms], axis=1)[t]
+        BT = np.concatenate([x[3] for x in terms], axis=1)[t]
+        for rid in (AR, BR):
+            if {recs[int(r)].kind for r in np.unique(rid)} != {"gload"}:
+                raise Unsupported("tile slot not filled from global memory")
+        an = {recs[int(r)].buf for r in np.unique(AR)}
+        bn = {recs[int(r)].buf for r in np.unique(BR)}
+        if len(an) != 1 or len(bn) != 1:
+            raise Unsupported("an operand mixes buffers")
+        an, bn = an.pop(), bn.pop()
+        a_buf, b_buf = a_buf or an, b_buf or bn
+        if (an, bn) != (a_buf, b_buf) or a_buf == b_buf or c_name in (a_buf, b_buf):
+            raise Unsupported("operand buffers differ between outputs")
+        # concrete liveness of each product (a masked load is 0, so the product is 0)
+        a_live = np.zeros(AR.shape, bool)
+        b_live = np.zeros(BR.shape, bool)
+        for r in np.unique(AR):
+            sel = AR == r
+            a_live[sel] = recs[int(r)].cond.base[AT[sel]]
+        for r in np.unique(BR):
+            sel = BR == r
+            b_live[sel] = recs[int(r)].cond.base[BT[sel]]
+        live = a_live & b_live
+        a_off = _gather_poly(recs, AR, AT, "off")
+        b_off = _gather_poly(recs, BR, BT, "off")
+        # B: k * ldb + col with ldb one scalar argument: the scalar whose coefficient runs
+        # through [0, K) over each thread's live products (a tile-base scalar's does not)
+        def k_cover(sym: str) -> tuple[dict, np.ndarray, int]:
+            b_k, b_col_ = _split(b_off, {(sym,): 1}, AR.shape)
+            kB_ = _concrete_part(b_k, AR.shape, "B's k")
+            kk: int | None = K
+            for i in range(t.size):
+                ks = np.sort(kB_[i][live[i]])
+                if kk is None:
+                    kk = int(ks.size)
+                if ks.size != kk or not np.array_equal(ks, np.arange(kk)):
+                    raise Unsupported("the dot chain does not cover k in [0, K) exactly once")
+            return b_col_, kB_, int(kk or 0)
+
+        cands = sorted({m[0] for m in b_off if len(m) == 1 and not m[0].startswith("%p")})
+        if ldb_sym is not None:
+            cands = [ldb_sym] if ldb_sym in cands else []
+        found = None
+        for sym in cands:
+            try:
+                found = (sym, *k_cover(sym))
+                break
+            except Unsupported:
+                continue
+        if found is None:
+            raise Unsupported("B's row stride is not a scalar argument walking k over [0, K)")
+        ldb_sym, b_col, kB, K = found
+        if K == 0:
+            raise Unsupported("empty reduction")
+        # A: row * K + k (row length K, a compile-time constant)
+        a_rest = _poly_sub(a_off, {(): kB}, AR.shape)
+        row = {}
+        for m, cf in a_rest.items():
+            if np.any(cf[live] % K):
+                raise Unsupported("A's row length is not the reduction length K")
+            row[m] = cf // K
+        # row / col uniform along k (over the live products)
+        def first_live(d: dict) -> dict:
+            out = {}
+            j0 = np.argmax(live, axis=1)
+            for m, cf in d.items():
+                v = cf[np.arange(t.size), j0]
+                if np.any((cf != v[:, None]) & live):
+                    raise Unsupported("operand row/col varies along k")
+                out[m] = v
+            return out
+        row1 = first_live(row)
+        col1 = first_live(b_col)
+        m_sym = _atoms_match(recs, AR, AT, {m: np.repeat(c[:, None], AR.shape[1], 1) for m, c in row1.items()},
+                             m_sym, live)
+        n_found = _atoms_match(recs, BR, BT, {m: np.repeat(c[:, None], BR.shape[1], 1) for m, c in col1.items()},
+                               None, live)
+        if n_found is not None and n_found != ldb_sym:
+            raise Unsupported("B's column bound differs from its row stride")
+        # output offset row * ldb + col, masks row < M / col < N
+        offp = {m: c[t] for m, c in off.t.items()}
+        o_row, o_col = _split(offp, {(ldb_sym,): 1}, t.shape)
+        if not (_same(o_row, row1) and _same(o_col, col1)):
+            raise Unsupported("output offset is not row*ldb + col of its products")
+        out_row = out_col = False
+        for atom in cond.atoms:
+            at_ = {m: c[t] for m, c in atom.t.items()}
+            neg = [m for m, c in at_.items() if len(m) == 1 and not m[0].startswith("%p") and np.all(c == -1)]
+            if len(neg) != 1:
+                raise Unsupported("output mask is not `index < scalar`")
+            rest = {m: c for m, c in at_.items() if m != neg[0]}
+            sym = neg[0][0]
+            if _same(rest, row1) and (m_sym is None or m_sym == sym):
+                m_sym, out_row = sym, True
+            elif _same(rest, col1) and sym == ldb_sym:
+                out_col = True
+            else:
+                raise Unsupported("output mask is not row < M / col < N")
+        # a bound is either applied to the operand and the output, or nowhere (a full-tile kernel)
+        masks = (n_found is not None, out_col)
+        if masks[0] != masks[1] or (col_masked is not None and col_masked != masks[0]):
+            raise Unsupported("column bound applied inconsistently")
+        col_masked = masks[0]
+        r_axis, TM, r_off, r_base = _as_tile(row1, "row")
+        c_axis, TN, c_off, c_base = _as_tile(col1, "col")
+        if r_axis == c_axis:
+            raise Unsupported("rows and cols indexed by the same program id")
+        if tile is None:
+            tile = (r_axis, TM, c_axis, TN, r_base, c_base)
+        if tile != (r_axis, TM, c_axis, TN, r_base, c_base):
+            raise Unsupported("outputs use different tilings")
+        row_masked_out.append(out_row)
+        rows_all.append(r_off)
+        cols_all.append(c_off)
+    assert tile is not None and K is not None
+    r_axis, TM, c_axis, TN, r_base, c_base = tile
+    pos = np.concatenate(rows_all) * TN + np.concatenate(cols_all)
+    if pos.size != TM * TN or not np.array_equal(np.sort(pos), np.arange(TM * TN)):
+        raise Unsupported("the outputs do not cover a TM x TN tile exactly once")
+    # the row bound, when there is one, guards the A loads and every output store
+    if m_sym is not None and not all(row_masked_out):
+        raise Unsupported("row bound applied inconsistently")
+    args = {x.name: x for x in ir.args}
+    if (m_sym is not None and m_sym not in args) or ldb_sym not in args:
+        raise Unsupported("bounds are not kernel arguments")
+    dts = (args[a_buf].dtype, args[b_buf].dtype, args[c_name].dtype)
+    if dts != (DType.F32, DType.F32, DType.F32):
+        raise Unsupported("the fp32 GEMM lift takes f32 A, B and C")
+    return GemmSpec(a=a_buf, b=b_buf, c=c_name, m_sym=m_sym, n_sym=ldb_sym, K=int(K), TM=TM, TN=TN,
+                    row_axis=int(r_axis[2:]), a_dtype=DType.F32, b_dtype=DType.F32, c_dtype=DType.F32,
+                    c_f16=False, f32=True, row_base=r_base, col_base=c_base, col_masked=bool(col_masked))
 
 
 # ---------------------------------------------------------------------------
@@ -730,10 +946,14 @@ def try_lift(ir: IRModule, block: int) -> Any:
 
     if os.environ.get("EAS_HIP_DISABLE_GEMM_LIFT", "") not in ("", "0"):
         return None
-    if "mma" not in {i.op for i in ir.insts}:
-        return None
+    ops = {i.op for i in ir.insts}
     try:
-        spec = analyze(ir, block)
+        if "mma" in ops:
+            spec = analyze(ir, block)
+        elif "dot" in ops:
+            spec = analyze_dot(ir, block)
+        else:
+            return None
     except Unsupported:
         return None
     from .gemm_kernels import emit_gemm
@@ -741,28 +961,58 @@ def try_lift(ir: IRModule, block: int) -> Any:
     return emit_gemm(ir, block, spec)
 
 
+def _numel(v: Any) -> int | None:
+    """Element count of a buffer argument (numpy array, torch tensor, eas.Tensor)."""
+    numel = getattr(v, "numel", None)
+    if callable(numel):
+        return int(numel())
+    shape = getattr(v, "shape", None)
+    if shape is not None:
+        n = 1
+        for d in shape:
+            n *= int(d)
+        return n
+    return None
+
+
 def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x: int | None) -> Any:
-    """Launch plan of a lifted GEMM for a reference grid ``groups``."""
+    """Launch plan of a lifted GEMM for a reference grid ``groups``.
+
+    The launch covers rows [m_lo, m_hi) and columns [n_lo, n_hi): the origin is
+    TM * row_base (TN * col_base) when the kernel offsets its program ids by a
+    scalar, the extent is the launched grid, clamped to M (N) when the kernel
+    bounds rows (columns).  Every buffer must hold what that rectangle touches;
+    a launch that would read or write past one raises instead of running.
+    """
     from ..runtime.hip import LaunchPlan
 
     if live_x is not None:
         raise ValueError("a lifted GEMM kernel needs a 2-D grid (pass _grid=...)")
     p = geo.params
-    M = int(runtime_args[p["m_sym"]])
-    N = int(runtime_args[p["n_sym"]])
     K = int(p["K"])
-    if max(M * K, K * N, M * N) >= 1 << 32:
-        raise ValueError("lifted GEMM: matrix too large for u32 indexing")
+    ldb = int(runtime_args[p["n_sym"]])
     g_rows = groups[p["row_axis"]]
     g_cols = groups[1 - p["row_axis"]]
-    m_eff = min(M, g_rows * p["TM"])
-    n_eff = min(N, g_cols * p["TN"])
-    if m_eff == 0 or n_eff == 0:
+    m_lo = p["TM"] * int(runtime_args[p["row_base"]]) if p.get("row_base") else 0
+    n_lo = p["TN"] * int(runtime_args[p["col_base"]]) if p.get("col_base") else 0
+    m_hi = m_lo + g_rows * p["TM"]
+    n_hi = n_lo + g_cols * p["TN"]
+    if p.get("m_sym"):
+        m_hi = min(m_hi, int(runtime_args[p["m_sym"]]))
+    if p.get("col_masked", True):
+        n_hi = min(n_hi, ldb)
+    if m_hi <= m_lo or n_hi <= n_lo:
         return None
-    if m_eff <= p.get("skinny_m", 0):
+    if max(m_hi * K, K * max(ldb, n_hi), m_hi * max(ldb, n_hi)) >= 1 << 32:
+        raise ValueError("lifted GEMM: matrix too large for u32 indexing")
+    need = {p["a"]: m_hi * K, p["b"]: (K - 1) * ldb + n_hi, p["c"]: (m_hi - 1) * ldb + n_hi}
+    for name, n_need in need.items():
+        have = _numel(runtime_args.get(name)) if name in runtime_args else None
+        if have is not None and have < n_need:
+            raise ValueError(f"buffer {name!r} holds {have} elements; this launch touches {n_need}")
+    if m_hi - m_lo <= p.get("skinny_m", 0):
         # the kernel's skinny path: one workgroup per skinny_n columns, all rows
-        tiles = -(-n_eff // p["skinny_n"])
+        tiles = -(-(n_hi - n_lo) // p["skinny_n"])
     else:
-        bm, bn = p["BM"], p["BN"]
-        tiles = -(-m_eff // bm) * -(-n_eff // bn)
-    return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), (m_eff, n_eff))
+        tiles = -(-(m_hi - m_lo) // p["BM"]) * -(-(n_hi - n_lo) // p["BN"])
+    return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), (m_lo, m_hi, n_lo, n_hi))

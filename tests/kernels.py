@@ -288,6 +288,116 @@ def matmul_tiled_kernel(a, b, c, M, N, PID_M_BASE, PID_N_BASE, BM: eas.constexpr
 
 
 @eas.kernel
+def matmul_tiled_full_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexpr, BK: eas.constexpr,
+                             K: eas.constexpr, NT: eas.constexpr):
+    """Interior-tile fp32 tiled matmul without bounds checks (examples/matmul_tiled.py:132-230):
+    valid only for grids of whole tiles and K divisible by BK."""
+    pid_n = mk.program_id(0)
+    pid_m = mk.program_id(1)
+    tid = mk.tid(0, NT)
+    tn = 4
+    ng = BN // tn
+    if NT != BM * ng or (BM * BK) % NT or (BK * BN) % NT:
+        raise ValueError("full kernel needs NT = BM*BN/4 dividing both tile loads")
+    lda = BK + 1
+    ldb = BN + 1
+    rm = tid // ng
+    cg = tid % ng
+    tile_m = pid_m * BM
+    tile_n = pid_n * BN
+    row = tile_m + rm
+    col0 = tile_n + cg * tn
+    As = mk.alloc_tg(BM * lda)
+    Bs = mk.alloc_tg(BK * ldb)
+    acc0 = acc1 = acc2 = acc3 = 0.0
+    for k0 in range(0, K, BK):
+        for i in range(0, BM * BK, NT):
+            a_idx = tid + i
+            a_r = a_idx // BK
+            a_c = a_idx % BK
+            mk.store(As, a_r * lda + a_c, mk.load(a, (tile_m + a_r) * K + k0 + a_c, True), True)
+        for i in range(0, BK * BN, NT):
+            b_idx = tid + i
+            b_r = b_idx // BN
+            b_c = b_idx % BN
+            mk.store(Bs, b_r * ldb + b_c, mk.load(b, (k0 + b_r) * N + tile_n + b_c, True), True)
+        mk.barrier()
+        a_base = rm * lda
+        b_base = cg * tn
+        acc0 = acc0 + mk.dot(As, a_base, 1, Bs, b_base + 0, ldb, BK)
+        acc1 = acc1 + mk.dot(As, a_base, 1, Bs, b_base + 1, ldb, BK)
+        acc2 = acc2 + mk.dot(As, a_base, 1, Bs, b_base + 2, ldb, BK)
+        acc3 = acc3 + mk.dot(As, a_base, 1, Bs, b_base + 3, ldb, BK)
+        mk.barrier()
+    base = row * N + col0
+    mk.store(c, base + 0, acc0, True)
+    mk.store(c, base + 1, acc1, True)
+    mk.store(c, base + 2, acc2, True)
+    mk.store(c, base + 3, acc3, True)
+
+
+@eas.kernel
+def matmul_tiled_variant_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexpr, BK: eas.constexpr,
+                                K: eas.constexpr, NT: eas.constexpr, VARIANT: eas.constexpr):
+    """matmul_tiled_kernel (without tile bases) with one deliberate change selected by VARIANT
+    (0 = none).  Variants 1-7 are not GEMMs and must not be lifted; 8-9 are equivalent rewrites."""
+    pid_n = mk.program_id(0)
+    pid_m = mk.program_id(1)
+    tid = mk.tid(0, NT)
+    tn = 4
+    ng = BN // tn
+    lda = BK + 1
+    ldb = BN + 1
+    rm = tid // ng
+    cg = tid % ng
+    tile_m = pid_m * BM
+    tile_n = pid_n * BN
+    row = tile_m + rm
+    col0 = tile_n + cg * tn
+    As = mk.alloc_tg(BM * lda)
+    Bs = mk.alloc_tg(BK * ldb)
+    acc = [0.0, 0.0, 0.0, 0.0]
+    row_ok = row < M
+    k_start = BK if VARIANT == 1 else 0          # 1: skips the first k block
+    for k0 in range(k_start, K, BK):
+        for i in range(0, BM * BK, NT):
+            a_idx = tid + i
+            in_tile = a_idx < (BM * BK)
+            a_r = a_idx // BK
+            a_c = a_idx % BK
+            a_row = tile_m + a_r
+            a_mask = in_tile & (a_row < M) & ((k0 + a_c) < K)
+            if VARIANT == 6:                       # 6: A masked by the column bound
+                a_mask = in_tile & (a_row < N) & ((k0 + a_c) < K)
+            src = b if VARIANT == 4 else a         # 4: A read from B
+            mk.store(As, a_r * lda + a_c, mk.load(src, a_row * K + k0 + a_c, a_mask), in_tile)
+        for i in range(0, BK * BN, NT):
+            b_idx = tid + i
+            in_tile = b_idx < (BK * BN)
+            b_r = b_idx // BN
+            b_c = b_idx % BN
+            b_mask = in_tile & ((k0 + b_r) < K) & ((tile_n + b_c) < N)
+            mk.store(Bs, b_r * ldb + b_c, mk.load(b, (k0 + b_r) * N + tile_n + b_c, b_mask), in_tile)
+        mk.barrier()
+        a_base = rm * lda
+        b_base = cg * tn
+        kd = BK - 1 if VARIANT == 5 else BK        # 5: each dot drops its last k
+        bst = ldb + 1 if VARIANT == 2 else ldb     # 2: B walked with the wrong stride
+        for j in range(4):
+            d = mk.dot(As, a_base, 1, Bs, b_base + j, bst, kd)
+            acc[j] = d + acc[j] if VARIANT == 8 else acc[j] + d   # 8: operands of the add swapped
+        mk.barrier()
+    for j in range(4):
+        jj = 3 - j if VARIANT == 3 else j          # 3: outputs stored to mirrored columns
+        mask = row_ok & (col0 + j < N)
+        if VARIANT == 7:                           # 7: a store mask on the wrong index
+            mask = (col0 + j < M) & (col0 + j < N)
+        if VARIANT == 9:                           # 9: equivalent mask written the other way round
+            mask = (col0 + j < N) & row_ok
+        mk.store(c, row * N + col0 + jj, acc[j], mask)
+
+
+@eas.kernel
 def matmul_mma_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexpr, BK: eas.constexpr,
                       K: eas.constexpr, NT: eas.constexpr):
     """Simdgroup 8x8x8 MMA matmul, f16 operands in threadgroup memory, f32

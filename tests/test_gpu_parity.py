@@ -232,18 +232,87 @@ def test_naive_matmul_bit_exact_vs_oracle(gpu_runtime):
 
 
 @pytest.mark.parametrize("mnk", [(33, 65, 48), (64, 64, 32), (17, 130, 31)])
-def test_tiled_matmul_cases(gpu_runtime, mnk):
+def test_tiled_matmul_literal_bit_exact(gpu_runtime, monkeypatch, mnk):
+    # the literal lowering (lift disabled) keeps the reference's fma order: bit-exact vs the oracle
+    monkeypatch.setenv("EAS_HIP_DISABLE_GEMM_LIFT", "1")
+    kern = eas.kernel(K.matmul_tiled_kernel.fn)
     m, n, k = mnk
     bm, bn, bk, nt = 16, 64, 16, 256
     a2 = seeded_normal(0, m * k).reshape(m, k) / np.float32(math.sqrt(k))
     b2 = seeded_normal(1, k * n).reshape(k, n)
     c = np.zeros(m * n, np.float32)
-    K.matmul_tiled_kernel(a2.reshape(-1), b2.reshape(-1), c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
-                          _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
+    kern(a2.reshape(-1), b2.reshape(-1), c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
+         _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
+    assert kern.compile(a2.reshape(-1), b2.reshape(-1), c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k,
+                        NT=nt).geometry.kind == "thread"
     ref = interp.run_kernel(K.matmul_tiled_kernel, a2.reshape(-1), b2.reshape(-1), np.zeros(m * n, np.float32), m, n,
                             0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt, _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1))["c"]
     assert _bits_equal(c, ref)
     assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
+
+
+def _tiled_inputs(m, n, k, seed=0):
+    a2 = seeded_normal(seed, m * k).reshape(m, k) / np.float32(math.sqrt(k))
+    b2 = seeded_normal(seed + 1, k * n).reshape(k, n) / np.float32(math.sqrt(k))
+    return a2, b2
+
+
+@pytest.mark.parametrize("mnk,tile", [((33, 65, 48), (16, 64, 16, 256)), ((64, 64, 32), (16, 64, 16, 256)),
+                                      ((17, 130, 31), (16, 64, 16, 256)), ((300, 260, 1000), (32, 32, 32, 256)),
+                                      ((1024, 1024, 1024), (32, 32, 32, 256)), ((130, 70, 30), (16, 16, 16, 64))])
+def test_tiled_matmul_lifted_fp32_tolerance(gpu_runtime, mnk, tile):
+    # lifted to the fp32 MFMA GEMM (K = 31 and 30: rows not 16-byte aligned, the kernel's fma path)
+    m, n, k = mnk
+    bm, bn, bk, nt = tile
+    a2, b2 = _tiled_inputs(m, n, k)
+    c = np.full(m * n, np.nan, np.float32)
+    assert K.matmul_tiled_kernel.compile(a2.reshape(-1), b2.reshape(-1), c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k,
+                                         NT=nt).geometry.kind == "gemm"
+    K.matmul_tiled_kernel(a2.reshape(-1), b2.reshape(-1), c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
+                          _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
+    assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
+
+
+def test_tiled_matmul_split_launch_like_the_reference(gpu_runtime):
+    # examples/matmul_tiled.py's split mode: the full-tile kernel on the interior, the masked
+    # kernel with tile bases on the right strip, the bottom strip and the corner
+    m, n, k = 100, 200, 64
+    bm, bn, bk, nt = 32, 32, 32, 256
+    a2, b2 = _tiled_inputs(m, n, k, seed=4)
+    c = np.full(m * n, np.nan, np.float32)
+    gx, gy = n // bn, m // bm
+    meta = dict(BM=bm, BN=bn, BK=bk, K=k, NT=nt, _tptg=(nt, 1, 1))
+    A, B = a2.reshape(-1), b2.reshape(-1)
+    K.matmul_tiled_full_kernel(A, B, c, m, n, _grid=(gx, gy, 1), **meta)
+    K.matmul_tiled_kernel(A, B, c, m, n, 0, gx, _grid=(K.cdiv(n, bn) - gx, gy, 1), **meta)
+    K.matmul_tiled_kernel(A, B, c, m, n, gy, 0, _grid=(gx, K.cdiv(m, bm) - gy, 1), **meta)
+    K.matmul_tiled_kernel(A, B, c, m, n, gy, gx, _grid=(K.cdiv(n, bn) - gx, K.cdiv(m, bm) - gy, 1), **meta)
+    assert np.isfinite(c).all()
+    assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
+
+
+def test_tiled_rows_past_k_are_never_read(gpu_runtime):
+    m, n, k = 64, 128, 40
+    a2, b2 = _tiled_inputs(m, n, k, seed=8)
+    b_pad = np.concatenate([b2.reshape(-1), np.full(64 * n, np.nan, np.float32)])
+    c = np.zeros(m * n, np.float32)
+    K.matmul_tiled_kernel(a2.reshape(-1), b_pad, c, m, n, 0, 0, BM=32, BN=32, BK=32, K=k, NT=256,
+                          _grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), _tptg=(256, 1, 1))
+    assert np.isfinite(c).all()
+    assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
+
+
+def test_tiled_partial_grid_touches_only_its_rectangle(gpu_runtime):
+    m, n, k = 96, 160, 64
+    a2, b2 = _tiled_inputs(m, n, k, seed=6)
+    c = np.full(m * n, 7.0, np.float32)
+    K.matmul_tiled_kernel(a2.reshape(-1), b2.reshape(-1), c, m, n, 1, 2, BM=32, BN=32, BK=32, K=k, NT=256,
+                          _grid=(2, 1, 1), _tptg=(256, 1, 1))
+    got = c.reshape(m, n)
+    ref = ops.matmul_ref(a2, b2)
+    assert ops.rel_err(got[32:64, 64:128], ref[32:64, 64:128]) <= 1e-5 * math.sqrt(k)
+    got[32:64, 64:128] = 7.0
+    assert np.all(got == 7.0)
 
 
 @pytest.mark.parametrize("mnk", [(64, 64, 64), (40, 72, 24), (33, 17, 16)])

@@ -195,14 +195,14 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, 300, 520, BM=32, BN=32, BK=8, K=200, NT=512)
     assert ck.geometry.kind == "gemm"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(17, 10, 1))
-    assert plan.hidden == (300, 520) and plan.grid == (2 * 3, 1, 1) and plan.block == (256, 1, 1)
+    assert plan.hidden == (0, 300, 0, 520) and plan.grid == (2 * 3, 1, 1) and plan.block == (256, 1, 1)
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(3, 2, 1))  # partial grid: 64 x 96 rectangle
-    assert plan.hidden == (64, 96) and plan.grid == (1, 1, 1)
+    assert plan.hidden == (0, 64, 0, 96) and plan.grid == (1, 1, 1)
     # M <= 16 (decode-like): one workgroup per 64 columns
     plan = plan_launch(ck, {"M": 16, "N": 14336}, grid=(448, 1, 1))
-    assert plan.hidden == (16, 14336) and plan.grid == (224, 1, 1)
+    assert plan.hidden == (0, 16, 0, 14336) and plan.grid == (224, 1, 1)
     plan = plan_launch(ck, {"M": 17, "N": 14336}, grid=(448, 1, 1))
-    assert plan.hidden == (17, 14336) and plan.grid == (56, 1, 1)
+    assert plan.hidden == (0, 17, 0, 14336) and plan.grid == (56, 1, 1)
 
 
 # ---- kernel-argument packing through a recording extension ------------------------
