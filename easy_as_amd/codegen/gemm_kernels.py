@@ -5,8 +5,8 @@ a 128 x 128 block held as 4 x 4 ``v_mfma_f32_32x32x16_f16`` accumulators
 (256 AGPRs).  Two bodies share one LDS array; a uniform branch picks one per
 launch:
 
-DMA body (f16 A and B; K and ldb multiples of 8, 16-byte aligned bases, each
-matrix under 2 GiB):
+DMA body (f16 A and B; K and ldb even and 4-byte aligned bases, so every row
+is 4-byte aligned; each matrix under 2 GiB):
 
 * A and B go HBM -> LDS with ``buffer_load_dwordx4 ... lds`` (no staging
   registers), BK = 32 per stage, a 4-stage ring (128 KB), so loads are issued
@@ -16,9 +16,11 @@ matrix under 2 GiB):
 * A fragments are ``ds_read_b128`` (8 consecutive k per lane); B fragments are
   two ``ds_read_b64_tr_b16`` per MFMA operand, which transpose a 4(k) x 16(n)
   block across each 16-lane group so every lane receives k-contiguous B;
-* buffer range checks give zeros for rows past M and for B rows past K; the
-  lanes of the K tail stage that would read past K in A use an offset outside
-  the range;
+* buffer range checks (per dword) give zeros for rows past M and for B rows
+  past K; the lanes of the K tail stage that would read past K in A use an
+  offset outside the range, and when K is not a multiple of 8 the halves of
+  the last chunk of each row that lie past K are zeroed in LDS once the tail
+  stage has landed;
 * the iteration is scheduled by hand (``sched_barrier``): ks0 MFMAs overlap the
   ks1 fragment reads; after the mid-iteration barrier the ks1 MFMAs overlap the
   DMA issue (one every two MFMAs) and the next stage's ks0 fragment reads.
@@ -155,6 +157,19 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
       eas_dma16(rb, off, lds_b + dst);
     }
   };
+  // Rows of A need only 4-byte alignment: a 16-byte DMA chunk may start anywhere, and at the end
+  // of a row whose length K is not a multiple of 8 the last chunk runs into the next row.  Once
+  // the tail stage has landed, those halves (k >= K) are zeroed in LDS, so a non-finite value in
+  // the next row never meets B's zero rows.  One row per thread (BM = 256).
+  auto fix_tail = [&]() {
+    if constexpr (K % 8 != 0) {
+      constexpr int KR = K % BK, CP = KR / 8, E0 = KR % 8;
+      const int r = tid;
+      _Float16* row = As + ((KT - 1) % NSTAGE) * STAGE_H + r * BK + ((CP ^ ((r >> 2) & 3)) * 8);
+#pragma unroll
+      for (int e = E0; e < 8; ++e) row[e] = (_Float16)0.0f;
+    }
+  };
   // fragment offsets (halves within a stage)
   int fa_off[2][4], fb_off[2][4][2];
 #pragma unroll
@@ -210,6 +225,10 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
       for (int d = 0; d < 8; ++d) dma_one(p, d);
   wait_stage(KT - 1 < NSTAGE - 2 ? KT - 1 : NSTAGE - 2);
   __syncthreads();
+  if (K % 8 != 0 && KT == 1) {
+    fix_tail();
+    __syncthreads();
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) { read_b(0, 0, i); read_a(0, 0, i); }
   for (int kt = 0; kt < KT; ++kt) {
@@ -233,6 +252,10 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
       // stage kt+1 landed (all waves), and every wave is done with stage kt-1, whose buffer the next DMA refills
       wait_stage(KT - 2 - kt < NSTAGE - 3 ? KT - 2 - kt : NSTAGE - 3);
       __syncthreads();
+      if (K % 8 != 0 && kt == KT - 2) {  // the next stage is the tail
+        fix_tail();
+        __syncthreads();
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     // phase B: ks1 MFMAs (set 1); DMA of stage kt+3 and the ks0 fragments of stage kt+1 (set 0)
@@ -548,11 +571,14 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   // one LDS array for all bodies: DMA ring 4 x 2 x 16 KB, register body 2 x 2 x 256 x 72 halves,
   // skinny path 4 waves x 4 stages x 5 KB
   __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 2 * 256 * 72];
-  const bool dma_ok = F16_IN && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0) &&
+  // DMA loads take any 4-byte aligned rows (16-byte chunks may straddle alignment and the buffer range,
+  // which is checked per dword); the skinny path also wants whole 16-byte chunks per row of A
+  const bool dma_ok = F16_IN && (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
                       ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
+  const bool skinny_dma_ok = dma_ok && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0);
   if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns
     if constexpr (F16_IN) {
-      if (dma_ok) {
+      if (skinny_dma_ok) {
         eas_gemm_skinny_dma<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
         return;
       }

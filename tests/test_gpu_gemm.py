@@ -91,6 +91,24 @@ def test_decode_shape_f16_out(gpu_runtime):
     assert np.isfinite(c).all() and ops.rel_err(c, ref) <= 2e-3
 
 
+@pytest.mark.parametrize("k", [36, 4100])
+def test_row_tail_chunk_does_not_leak_the_next_row(gpu_runtime, k):
+    # K % 8 == 4: rows of A are 8-byte aligned and the last 16-byte chunk of row r holds the first
+    # halves of row r + 1.  An inf there must only affect row r + 1 of C.
+    m, n = 64, 128
+    a, b = _inputs(m, n, k, seed=9)
+    a = a.reshape(m, k)
+    a[5, 0] = np.inf
+    c = np.full(m * n, np.nan, np.float32)
+    _mma(K.matmul_mma_kernel, a.reshape(-1), b, c, m, n, k)
+    c = c.reshape(m, n)
+    ok = np.ones(m, bool)
+    ok[5] = False
+    assert np.isfinite(c[ok]).all() and not np.isfinite(c[5]).all()
+    ref = ops.matmul_ref(a[ok].astype(np.float32), b.reshape(k, n))
+    assert ops.rel_err(c[ok], ref) <= 1e-5 * math.sqrt(k)
+
+
 def test_rows_past_k_are_never_read(gpu_runtime):
     # B is followed by NaN padding and A rows end where the next begins: a K-tail
     # stage that read past K would put NaN (B) or wrong values (A) into C.
