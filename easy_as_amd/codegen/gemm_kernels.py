@@ -58,6 +58,8 @@ typedef int eas_rsrc __attribute__((ext_vector_type(4)));
 #define EAS_LDS __attribute__((address_space(3)))
 // s_waitcnt with only vmcnt limited (gfx9 encoding: vmcnt[3:0], [15:14]; expcnt and lgkmcnt at max)
 #define EAS_WAITVM(n) (((n) & 15) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt at max
+#define EAS_WAITLGKM0 (15 | (3 << 14) | (0x7 << 4))
 
 template <typename T> static __device__ __forceinline__ eas_h8 eas_load8(const T* p);
 template <> __device__ __forceinline__ eas_h8 eas_load8<_Float16>(const _Float16* p) { return *(const eas_h8*)p; }
@@ -285,6 +287,184 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
         const int col = n0 + wn * 128 + j * 32 + (lane & 31);
         if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
       }
+}
+
+// Ping-pong DMA body: 8 waves (two per SIMD; waves w and w+4 share one) in two groups.  Group g
+// owns rows [128g, 128g+128) of the 256x256 tile, wave p of the group columns [64p, 64p+64)
+// (4 x 2 accumulators of 32x32, 128 registers).  Each wave alternates a load phase (all fragments
+// of one BK=32 stage, plus its quarter of the DMA three stages ahead) and an MFMA phase (16 MFMAs),
+// separated by workgroup barriers; group 1 enters the loop one barrier later, so while one wave of
+// a SIMD runs MFMAs the other one loads.  Stage ring, LDS layout, swizzles and range checks are
+// the 4-wave DMA body's.  When K is not a multiple of 8, the A fragments of the tail stage are
+// masked to zero past K in registers (the last 16-byte chunk of a row reaches into the next row).
+template <typename CT, int K>
+static __device__ __forceinline__ void eas_gemm_pp(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                                                   CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
+                                                   _Float16* smem) {
+  constexpr int BM = 256, BN = 256, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
+  constexpr int STAGE_H = BM * BK;
+  _Float16* As = smem;
+  _Float16* Bs = smem + NSTAGE * STAGE_H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = wave >> 2, p = wave & 3;
+  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
+  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
+  // DMA instruction q = 2 wave + i writes 1 KB of a stage.  A: rows 16q + lane/4, chunk lane%4
+  // stored at chunk ^ ((row/4)%4).  B: rows (k) 2q + lane/32, chunk lane%32 stored at chunk ^ 4(row%4).
+  uint32_t a_off[2], b_off[2];
+  int a_k[2], b_k[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = wave * 2 + i;
+    const int r_a = 16 * q + (lane >> 2);
+    const int c_a = (lane & 3) ^ ((r_a >> 2) & 3);
+    a_off[i] = ((uint32_t)(m0 + r_a) * (uint32_t)K + (uint32_t)(c_a * 8)) * 2u;
+    a_k[i] = c_a * 8;
+    const int r_b = 2 * q + (lane >> 5);
+    const int c_b = (lane & 31) ^ (4 * (r_b & 3));
+    b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
+    b_k[i] = r_b;
+  }
+  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS _Float16*)As, lds_b = (uint32_t)(size_t)(EAS_LDS _Float16*)Bs;
+  auto dma_one = [&](int kt, int d) {  // d: 0, 1 A; 2, 3 B
+    const int s = kt % NSTAGE, i = d & 1;
+    const uint32_t dst = (uint32_t)((s * STAGE_H + (wave * 2 + i) * 512) * 2);
+    if (d < 2) {
+      uint32_t off = a_off[i] + (uint32_t)(kt * BK * 2);
+      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: past the range -> zeros
+      eas_dma16(ra, off, lds_a + dst);
+    } else {
+      uint32_t off = b_off[i] + (uint32_t)kt * (uint32_t)(BK * 2) * (uint32_t)ldb;
+      if (K % BK != 0 && kt * BK + b_k[i] >= K) off = 0x80000000u;  // B rows past K
+      eas_dma16(rb, off, lds_b + dst);
+    }
+  };
+  int fa_off[2][4], fb_off[2][2][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = g * 128 + i * 32 + (lane & 31);
+      const int c = (2 * ks + (lane >> 5)) ^ ((r >> 2) & 3);
+      fa_off[ks][i] = r * BK + c * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // ds_read_b64_tr_b16: in each 16-lane group, source lane kq addresses row kq/4, columns 4(kq%4)..+3;
+        // result lane i receives column i for the four rows
+        const int gq = lane >> 4, kq = lane & 15;
+        const int row = 16 * ks + 8 * (gq >> 1) + 4 * h + (kq >> 2);
+        const int col = p * 64 + j * 32 + 16 * (gq & 1) + 4 * (kq & 3);
+        const int chunk = (col >> 3) ^ (4 * (row & 3));
+        fb_off[ks][j][h] = row * BN + chunk * 8 + (col & 7);
+      }
+  }
+  eas_h8 fa[2][4], fb[2][2];
+  auto read_a = [&](int s, int ks, int i) { fa[ks][i] = *(const eas_h8*)(As + s * STAGE_H + fa_off[ks][i]); };
+  auto read_b = [&](int s, int ks, int j) {
+    const _Float16* bs = Bs + s * STAGE_H;
+    const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
+    const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
+    const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
+    fb[ks][j] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+  };
+  eas_f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
+  // this wave's loads of the awaited stage are done; `later` newer stages (4 loads each) may stay in flight
+  auto wait_stage = [&](int later) {
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));
+    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+  };
+
+  // Barrier schedule (b = workgroup barrier index): stage kt is read by group 0 between b(2kt+1)
+  // and b(2kt+2) and by group 1 between b(2kt+2) and b(2kt+3).  Every wave waits for its own DMA
+  // of stage kt+1 before b(2kt+2): group 0 at the end of its MFMA phase, group 1 at the end of its
+  // load phase.  Stage kt+3 refills the buffer of stage kt-1, whose last reader (group 1) passed
+  // b(2kt) before any wave issues that DMA.  Both groups execute the same number of barriers.
+#pragma unroll
+  for (int s = 0; s < NSTAGE - 1; ++s)
+    if (s < KT)
+#pragma unroll
+      for (int d = 0; d < 4; ++d) dma_one(s, d);
+  wait_stage(KT - 1 < NSTAGE - 2 ? KT - 1 : NSTAGE - 2);
+  __syncthreads();
+  if (g == 1) __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int s = kt % NSTAGE;
+    const bool issue = kt + NSTAGE - 1 < KT;
+    const int later = KT - 2 - kt < NSTAGE - 2 ? KT - 2 - kt : NSTAGE - 2;
+    // load phase: every fragment of stage kt, and this wave's quarter of stage kt+3
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (issue) dma_one(kt + NSTAGE - 1, u);
+      read_a(s, u >> 1, 2 * (u & 1));
+      read_a(s, u >> 1, 2 * (u & 1) + 1);
+      read_b(s, u >> 1, u & 1);
+    }
+    if (g == 1 && kt + 1 < KT) wait_stage(later);
+    if constexpr (K % 8 != 0) {
+      if (kt == KT - 1) {  // tail stage: halves at k >= K hold the next row of A
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const bool past = kt * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) fa[ks][i][e] = past ? (_Float16)0.0f : fa[ks][i][e];
+          }
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(EAS_WAITLGKM0);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    // MFMA phase
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+    if (g == 0 && kt + 1 < KT) wait_stage(later);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+  }
+  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier
+  const bool full = (m0 + BM <= M) && (n0 + BN <= N);
+  // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + g * 128 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
+        const int col = n0 + p * 64 + j * 32 + (lane & 31);
+        if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
+      }
+}
+
+// Guard body of the 8-wave entry for inputs the DMA cannot take (the launch plan sends those to
+// the 4-wave entry; this path only keeps a mistaken plan correct): one f32 dot product per element.
+template <typename AT, typename BT, typename CT, int K>
+static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict__ A, const BT* __restrict__ B,
+                                                            CT* __restrict__ C, int ldb, int M, int N, int m0, int n0) {
+  for (int e = threadIdx.x; e < 256 * 256; e += blockDim.x) {
+    const int row = m0 + (e >> 8), col = n0 + (e & 255);
+    if (row >= M || col >= N) continue;
+    float acc = 0.0f;
+    for (int k = 0; k < K; ++k)
+      acc = __builtin_fmaf((float)(_Float16)A[(size_t)row * K + k], (float)(_Float16)B[(size_t)k * ldb + col], acc);
+    C[(size_t)row * ldb + col] = (CT)acc;
+  }
 }
 
 // Skinny path (M <= 16, decode-like): one workgroup per 64 columns, the four waves split K.
@@ -555,9 +735,22 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
       }
 }
 
+// Origin of this workgroup's 256 x 256 tile: XCD-contiguous (workgroup w runs on XCD w % 8, so
+// each XCD gets a contiguous range of tiles), grouped 4 tile-rows high for L2 reuse.
+static __device__ __forceinline__ void eas_tile_origin(int M, int N, int& m0, int& n0) {
+  constexpr int BM = 256, BN = 256, GROUP_M = 4;
+  const int tilesM = (M + BM - 1) / BM, tilesN = (N + BN - 1) / BN, T = tilesM * tilesN;
+  const int w = blockIdx.x;
+  const int t = (T % 8 == 0) ? (w % 8) * (T / 8) + w / 8 : w;
+  const int gsize = GROUP_M * tilesN, g = t / gsize, first_m = g * GROUP_M;
+  const int gm = min(tilesM - first_m, GROUP_M);
+  m0 = (first_m + (t % gsize) % gm) * BM;
+  n0 = ((t % gsize) / gm) * BN;
+}
+
 extern "C" __global__ __launch_bounds__(256) void @NAME@(
     @PARAMS@) {
-  constexpr int BM = 256, BN = 256, K = @K@, SKINNY_M = @SKINNY_M@;
+  constexpr int K = @K@, SKINNY_M = @SKINNY_M@;
   constexpr bool F16_IN = @F16_IN@;
   typedef @AT@ AT;
   typedef @BT@ BT;
@@ -586,15 +779,8 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
     eas_gemm_skinny_simple<AT, BT, CT, K>(A, B, C, ldb, M, N);
     return;
   }
-  // XCD-contiguous, M-grouped tile order
-  const int tilesM = (M + BM - 1) / BM, tilesN = (N + BN - 1) / BN, T = tilesM * tilesN;
-  const int w = blockIdx.x;
-  const int t = (T % 8 == 0) ? (w % 8) * (T / 8) + w / 8 : w;
-  constexpr int GROUP_M = 4;
-  const int gsize = GROUP_M * tilesN, g = t / gsize, first_m = g * GROUP_M;
-  const int gm = min(tilesM - first_m, GROUP_M);
-  const int ty = first_m + (t % gsize) % gm, tx = (t % gsize) / gm;
-  const int m0 = ty * BM, n0 = tx * BN;
+  int m0, n0;
+  eas_tile_origin(M, N, m0, n0);
   if constexpr (F16_IN) {
     if (dma_ok) {
       eas_gemm_dma<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
@@ -602,6 +788,33 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
     }
   }
   eas_gemm_regs<AT, BT, CT, K>(A, B, C, ldb, M, N, m0, n0, smem);
+}
+"""
+
+# The 8-wave entry (f16 A and B): the launch plan picks it for launches above the skinny
+# height whose operands the DMA can take; the same tile grid as the 4-wave entry.
+_TEMPLATE_PP_ENTRY = r"""
+extern "C" __global__ __launch_bounds__(512) void @NAME@__pp(
+    @PARAMS@) {
+  constexpr int K = @K@;
+  typedef @AT@ AT;
+  typedef @BT@ BT;
+  typedef @CT@ CT;
+  const int ldb = (int)@LDB@;
+  // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
+  const AT* __restrict__ A = @A@ + (size_t)__eas_m_lo * K;
+  const BT* __restrict__ B = @B@ + __eas_n_lo;
+  CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
+  const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 4 * 256 * 32];  // DMA ring 4 x 2 x 16 KB
+  const bool dma_ok = (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
+                      ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
+  int m0, n0;
+  eas_tile_origin(M, N, m0, n0);
+  if (dma_ok)
+    eas_gemm_pp<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
+  else
+    eas_gemm_elementwise<AT, BT, CT, K>(A, B, C, ldb, M, N, m0, n0);
 }
 """
 
@@ -751,6 +964,7 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
 TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
+PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
 SKINNY_M = 16  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
 
@@ -789,6 +1003,9 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "@LDB@": pname[spec.n_sym],
     }
     src = _TEMPLATE_F32 if spec.f32 else _TEMPLATE
+    pingpong = f16_in and not spec.f32
+    if pingpong:
+        src += _TEMPLATE_PP_ENTRY
     for k, v in subs.items():
         src = src.replace(k, v)
     header = (f"// Lifted from eas kernel `{ir.name}`: proven dense GEMM C[M,N] = A[M,{spec.K}] @ B[{spec.K},N]\n"
@@ -800,5 +1017,6 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "skinny_m": 0 if spec.f32 else SKINNY_M, "skinny_n": SKINNY_N, "row_base": spec.row_base,
         "col_base": spec.col_base,
         "col_masked": spec.col_masked,
+        "pp_entry": f"{ir.name}__pp" if pingpong else None, "pp_threads": PP_THREADS,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

@@ -32,6 +32,8 @@ M*N below 2^32 (the u32 index range the reference computes in).
 
 from __future__ import annotations
 
+import os
+
 from dataclasses import dataclass
 from typing import Any
 
@@ -1010,9 +1012,31 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
         have = _numel(runtime_args.get(name)) if name in runtime_args else None
         if have is not None and have < n_need:
             raise ValueError(f"buffer {name!r} holds {have} elements; this launch touches {n_need}")
+    hidden = (m_lo, m_hi, n_lo, n_hi)
     if m_hi - m_lo <= p.get("skinny_m", 0):
         # the kernel's skinny path: one workgroup per skinny_n columns, all rows
-        tiles = -(-(n_hi - n_lo) // p["skinny_n"])
-    else:
-        tiles = -(-(m_hi - m_lo) // p["BM"]) * -(-(n_hi - n_lo) // p["BN"])
-    return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), (m_lo, m_hi, n_lo, n_hi))
+        return LaunchPlan((-(-(n_hi - n_lo) // p["skinny_n"]), 1, 1), (p["threads"], 1, 1), hidden)
+    tiles = -(-(m_hi - m_lo) // p["BM"]) * -(-(n_hi - n_lo) // p["BN"])
+    if p.get("pp_entry") and _pingpong_fits(p, runtime_args, K, ldb, m_hi - m_lo, n_lo, n_hi - n_lo):
+        return LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
+    return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
+
+
+def _pingpong_fits(p: dict, runtime_args: Any, K: int, ldb: int, m: int, n_lo: int, n: int) -> bool:
+    """Whether the 8-wave entry's DMA takes this launch: every row of A and B (after the
+    move to the rectangle's origin) 4-byte aligned, each operand's extent under 2 GiB.
+    Device addresses are known here for torch tensors; numpy inputs are staged into fresh
+    allocations, and the entry re-checks the addresses it gets (a misaligned operand
+    takes its slow element-wise guard rather than a wrong result).
+    ``EAS_HIP_GEMM_PINGPONG=0`` keeps every launch on the 4-wave entry."""
+    if os.environ.get("EAS_HIP_GEMM_PINGPONG", "1").strip() == "0":
+        return False
+    if K % 2 or ldb % 2 or n_lo % 2:
+        return False
+    if m * K * 2 >= 1 << 31 or ((K - 1) * ldb + n) * 2 >= 1 << 31:
+        return False
+    for name in (p["a"], p["b"]):
+        ptr = getattr(runtime_args.get(name), "data_ptr", None)
+        if callable(ptr) and int(ptr()) % 4:
+            return False
+    return True

@@ -95,14 +95,17 @@ def compile_code(mod: Any, src: str, entry: str, options: tuple[str, ...] = COMP
 
 
 class LaunchPlan:
-    """A concrete HIP dispatch: workgroup grid, block and hidden u32 arguments."""
+    """A concrete HIP dispatch: workgroup grid, block, hidden u32 arguments and the
+    entry point to launch (``None``: the kernel's own)."""
 
-    __slots__ = ("grid", "block", "hidden")
+    __slots__ = ("grid", "block", "hidden", "entry")
 
-    def __init__(self, grid: tuple[int, int, int], block: tuple[int, int, int], hidden: tuple[int, ...]) -> None:
+    def __init__(self, grid: tuple[int, int, int], block: tuple[int, int, int], hidden: tuple[int, ...],
+                 entry: str | None = None) -> None:
         self.grid = grid
         self.block = block
         self.hidden = hidden
+        self.entry = entry
 
 
 def plan_launch(
@@ -223,15 +226,17 @@ class HipRuntime:
                 self._max_in_flight = 256
         return self._max_in_flight
 
-    def kernel_handle(self, ck: Any) -> Any:
-        """Loaded kernel for ``ck`` (compiled once per source; disk-cached)."""
-        entry = ck.geometry.entry if ck.geometry is not None else ck.ir.name
+    def kernel_handle(self, ck: Any, entry: str | None = None) -> Any:
+        """Loaded kernel ``entry`` (default: the kernel's own) of ``ck``'s source, which is
+        compiled once (disk-cached) for all of its entry points."""
+        main = ck.geometry.entry if ck.geometry is not None else ck.ir.name
+        entry = entry or main
         key = (ck.src, entry)
         k = self._kernels.get(key)
         if k is None:
             mod = self._mod()
             if callable(getattr(mod, "compile_to_code", None)) and callable(getattr(mod, "load", None)):
-                k = mod.load(compile_code(mod, ck.src, entry), entry)
+                k = mod.load(compile_code(mod, ck.src, main), entry)
             else:
                 k = mod.compile(ck.src, entry)
             self._kernels[key] = k
@@ -332,7 +337,7 @@ class HipRuntime:
         argv += [struct.pack("<I", h) for h in plan.hidden]
         writable += [False] * len(plan.hidden)
         mod = self._mod()
-        kernel = self.kernel_handle(ck)
+        kernel = self.kernel_handle(ck, plan.entry)
         if sync or copy_back:
             mod.launch(kernel, argv, writable, plan.grid, plan.block, stream=stream)
             for buf, arr in copy_back:
@@ -381,6 +386,6 @@ class HipRuntime:
                              "torch GPU tensors for device-resident timing")
         argv += [struct.pack("<I", h) for h in plan.hidden]
         writable += [False] * len(plan.hidden)
-        ms = self._mod().launch_timed(self.kernel_handle(ck), argv, writable, plan.grid, plan.block,
+        ms = self._mod().launch_timed(self.kernel_handle(ck, plan.entry), argv, writable, plan.grid, plan.block,
                                       repeat=int(repeat), warmup=int(warmup), stream=stream)
         return float(ms) * 1e-3

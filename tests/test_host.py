@@ -195,14 +195,50 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, 300, 520, BM=32, BN=32, BK=8, K=200, NT=512)
     assert ck.geometry.kind == "gemm"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(17, 10, 1))
-    assert plan.hidden == (0, 300, 0, 520) and plan.grid == (2 * 3, 1, 1) and plan.block == (256, 1, 1)
+    assert plan.hidden == (0, 300, 0, 520) and plan.grid == (2 * 3, 1, 1)
+    # f16 operands the DMA takes run on the 8-wave entry, on the same tile grid
+    assert plan.block == (512, 1, 1) and plan.entry == "matmul_mma_kernel__pp"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(3, 2, 1))  # partial grid: 64 x 96 rectangle
     assert plan.hidden == (0, 64, 0, 96) and plan.grid == (1, 1, 1)
-    # M <= 16 (decode-like): one workgroup per 64 columns
+    # M <= 16 (decode-like): one workgroup per 64 columns, on the 4-wave entry
     plan = plan_launch(ck, {"M": 16, "N": 14336}, grid=(448, 1, 1))
     assert plan.hidden == (0, 16, 0, 14336) and plan.grid == (224, 1, 1)
+    assert plan.block == (256, 1, 1) and plan.entry is None
     plan = plan_launch(ck, {"M": 17, "N": 14336}, grid=(448, 1, 1))
-    assert plan.hidden == (0, 17, 0, 14336) and plan.grid == (56, 1, 1)
+    assert plan.hidden == (0, 17, 0, 14336) and plan.grid == (56, 1, 1) and plan.entry == "matmul_mma_kernel__pp"
+
+
+class _FakeTorchTensor:
+    def __init__(self, addr, numel):
+        self._addr, self._numel = addr, numel
+
+    def data_ptr(self):
+        return self._addr
+
+    def numel(self):
+        return self._numel
+
+
+def test_plan_pingpong_entry_only_for_operands_the_dma_takes(monkeypatch):
+    f16, f32 = np.zeros(1, np.float16), np.zeros(1, np.float32)
+    ck = K.matmul_mma_kernel.compile(f16, f16, f32, 512, 512, BM=32, BN=32, BK=8, K=64, NT=512)
+    args = {"M": 512, "N": 512}
+    assert plan_launch(ck, args, grid=(16, 16, 1)).entry == "matmul_mma_kernel__pp"
+    # odd row stride of B: rows are not 4-byte aligned
+    assert plan_launch(ck, {"M": 512, "N": 511}, grid=(16, 16, 1)).entry is None
+    # a torch operand at a 2-byte offset
+    odd = {**args, "a": _FakeTorchTensor(0x1000002, 512 * 64), "b": _FakeTorchTensor(0x2000000, 64 * 512)}
+    assert plan_launch(ck, odd, grid=(16, 16, 1)).entry is None
+    even = {**args, "a": _FakeTorchTensor(0x1000004, 512 * 64), "b": _FakeTorchTensor(0x2000000, 64 * 512)}
+    assert plan_launch(ck, even, grid=(16, 16, 1)).entry == "matmul_mma_kernel__pp"
+    # odd K (rows of A 2-byte aligned) and f32 inputs have no 8-wave entry
+    ck_odd = K.matmul_mma_kernel.compile(f16, f16, f32, 512, 512, BM=32, BN=32, BK=8, K=63, NT=512)
+    assert plan_launch(ck_odd, args, grid=(16, 16, 1)).entry is None
+    ck32 = K.matmul_mma_kernel.compile(f32, f32, f32, 512, 512, BM=32, BN=32, BK=8, K=64, NT=512)
+    assert ck32.geometry.params["pp_entry"] is None and "__pp" not in ck32.src
+    assert plan_launch(ck32, args, grid=(16, 16, 1)).block == (256, 1, 1)
+    monkeypatch.setenv("EAS_HIP_GEMM_PINGPONG", "0")
+    assert plan_launch(ck, args, grid=(16, 16, 1)).entry is None
 
 
 # ---- kernel-argument packing through a recording extension ------------------------
