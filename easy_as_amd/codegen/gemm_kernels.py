@@ -1,11 +1,19 @@
 """gfx950 MFMA GEMM emitted for kernels that ``gemm_lift`` proved to be dense GEMMs.
 
-One workgroup of 4 waves (2 x 2) computes a 256 x 256 tile of C; each wave owns
-a 128 x 128 block held as 4 x 4 ``v_mfma_f32_32x32x16_f16`` accumulators
-(256 AGPRs).  Two bodies share one LDS array; a uniform branch picks one per
-launch:
+Launches of more than 16 rows tile C into 256 x 256 workgroup tiles (the fp32
+template at the end of this module uses 64 x 64).  The f16 source has two
+entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
 
-DMA body (f16 A and B; K and ldb even and 4-byte aligned bases, so every row
+* ``<name>__pp`` (512 threads): the 8-wave ping-pong DMA body for f16 A and B
+  whose rows the DMA takes.  Waves w and w+4 share a SIMD; the two groups of
+  four waves alternate load phases and MFMA phases one barrier apart, each
+  wave holding 128 x 64 of the tile (4 x 2 ``v_mfma_f32_32x32x16_f16``
+  accumulators).
+* ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
+  AGPRs): the skinny path (launches of at most 16 rows), the 4-wave DMA body,
+  and the register body; a uniform branch picks one per launch.
+
+DMA bodies (f16 A and B; K and ldb even and 4-byte aligned bases, so every row
 is 4-byte aligned; each matrix under 2 GiB):
 
 * A and B go HBM -> LDS with ``buffer_load_dwordx4 ... lds`` (no staging
@@ -19,11 +27,12 @@ is 4-byte aligned; each matrix under 2 GiB):
 * buffer range checks (per dword) give zeros for rows past M and for B rows
   past K; the lanes of the K tail stage that would read past K in A use an
   offset outside the range, and when K is not a multiple of 8 the halves of
-  the last chunk of each row that lie past K are zeroed in LDS once the tail
-  stage has landed;
-* the iteration is scheduled by hand (``sched_barrier``): ks0 MFMAs overlap the
-  ks1 fragment reads; after the mid-iteration barrier the ks1 MFMAs overlap the
-  DMA issue (one every two MFMAs) and the next stage's ks0 fragment reads.
+  the last chunk of each row that lie past K are zeroed (the 4-wave body in
+  LDS once the tail stage has landed, the 8-wave body in its A fragments);
+* the 4-wave iteration is scheduled by hand (``sched_barrier``): ks0 MFMAs
+  overlap the ks1 fragment reads; after the mid-iteration barrier the ks1
+  MFMAs overlap the DMA issue (one every two MFMAs) and the next stage's ks0
+  fragment reads.
 
 Register body (any other case, including f32 inputs that MFMA consumes as f16):
 global -> registers -> LDS, BK = 64, double buffered; A loads use the widest
