@@ -58,10 +58,7 @@ from ..ir import DType, IRModule
 from .gemm_lift import GemmSpec
 from .hip import PRELUDE, Geometry, Lowered, ctype
 
-_TEMPLATE = r"""
-typedef _Float16 eas_h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 eas_h4 __attribute__((ext_vector_type(4)));
-typedef __fp16 eas_h4t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+_DMA_HELPERS = r"""
 typedef float eas_f32x16 __attribute__((ext_vector_type(16)));
 typedef int eas_rsrc __attribute__((ext_vector_type(4)));
 #define EAS_LDS __attribute__((address_space(3)))
@@ -69,6 +66,29 @@ typedef int eas_rsrc __attribute__((ext_vector_type(4)));
 #define EAS_WAITVM(n) (((n) & 15) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
 // s_waitcnt lgkmcnt(0) with vmcnt and expcnt at max
 #define EAS_WAITLGKM0 (15 | (3 << 14) | (0x7 << 4))
+
+// raw buffer resource: base, range in bytes (reads at or past it return 0), gfx9 word 3
+static __device__ __forceinline__ eas_rsrc eas_make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  eas_rsrc r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+// 16 bytes per lane, HBM -> LDS; lane i writes LDS bytes [lds + 16 i, lds + 16 i + 16).
+// Issued as asm so the compiler does not add vmcnt(0) before every LDS read; the
+// pipelines count their own loads with EAS_WAITVM.
+static __device__ __forceinline__ void eas_dma16(eas_rsrc r, uint32_t voff, uint32_t lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+}
+"""
+
+_TEMPLATE = r"""
+typedef _Float16 eas_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 eas_h4 __attribute__((ext_vector_type(4)));
+typedef __fp16 eas_h4t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
 template <typename T> static __device__ __forceinline__ eas_h8 eas_load8(const T* p);
 template <> __device__ __forceinline__ eas_h8 eas_load8<_Float16>(const _Float16* p) { return *(const eas_h8*)p; }
@@ -107,23 +127,6 @@ template <typename T, int AL> static __device__ __forceinline__ eas_h8 eas_load8
     }
     return v;
   }
-}
-
-// raw buffer resource: base, range in bytes (reads at or past it return 0), gfx9 word 3
-static __device__ __forceinline__ eas_rsrc eas_make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  eas_rsrc r;
-  r[0] = (int)(uint32_t)a;
-  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);
-  r[2] = (int)bytes;
-  r[3] = 0x00020000;
-  return r;
-}
-// 16 bytes per lane, HBM -> LDS; lane i writes LDS bytes [lds + 16 i, lds + 16 i + 16).
-// Issued as asm so the compiler does not add vmcnt(0) before every LDS read; the
-// pipeline counts its own loads with EAS_WAITVM.
-static __device__ __forceinline__ void eas_dma16(eas_rsrc r, uint32_t voff, uint32_t lds) {
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 
 template <typename CT, int K>
@@ -828,24 +831,6 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__pp(
 """
 
 _TEMPLATE_F32 = r"""
-typedef float eas_f32x16 __attribute__((ext_vector_type(16)));
-typedef int eas_rsrc __attribute__((ext_vector_type(4)));
-#define EAS_LDS __attribute__((address_space(3)))
-#define EAS_WAITVM(n) (((n) & 15) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
-
-static __device__ __forceinline__ eas_rsrc eas_make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)base;
-  eas_rsrc r;
-  r[0] = (int)(uint32_t)a;
-  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);
-  r[2] = (int)bytes;
-  r[3] = 0x00020000;
-  return r;
-}
-static __device__ __forceinline__ void eas_dma16(eas_rsrc r, uint32_t voff, uint32_t lds) {
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
-}
-
 extern "C" __global__ __launch_bounds__(256) void @NAME@(
     @PARAMS@) {
   constexpr int BM = 64, BN = 64, BK = 32, NSTAGE = 4, K = @K@, KT = (K + BK - 1) / BK;
@@ -1011,8 +996,8 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "@C@": pname[spec.c],
         "@LDB@": pname[spec.n_sym],
     }
-    src = _TEMPLATE_F32 if spec.f32 else _TEMPLATE
-    pingpong = f16_in and not spec.f32
+    src = _DMA_HELPERS + (_TEMPLATE_F32 if spec.f32 else _TEMPLATE)
+    pingpong = f16_in and not spec.f32 and spec.K % 2 == 0  # odd K: rows of A are not 4-byte aligned
     if pingpong:
         src += _TEMPLATE_PP_ENTRY
     for k, v in subs.items():

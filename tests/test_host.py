@@ -233,6 +233,7 @@ def test_plan_pingpong_entry_only_for_operands_the_dma_takes(monkeypatch):
     assert plan_launch(ck, even, grid=(16, 16, 1)).entry == "matmul_mma_kernel__pp"
     # odd K (rows of A 2-byte aligned) and f32 inputs have no 8-wave entry
     ck_odd = K.matmul_mma_kernel.compile(f16, f16, f32, 512, 512, BM=32, BN=32, BK=8, K=63, NT=512)
+    assert ck_odd.geometry.params["pp_entry"] is None and "__pp" not in ck_odd.src
     assert plan_launch(ck_odd, args, grid=(16, 16, 1)).entry is None
     ck32 = K.matmul_mma_kernel.compile(f32, f32, f32, 512, 512, BM=32, BN=32, BK=8, K=64, NT=512)
     assert ck32.geometry.params["pp_entry"] is None and "__pp" not in ck32.src
