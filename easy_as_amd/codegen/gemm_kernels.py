@@ -464,19 +464,148 @@ static __device__ __forceinline__ void eas_gemm_pp(const _Float16* __restrict__ 
       }
 }
 
-// Guard body of the 8-wave entry for inputs the DMA cannot take (the launch plan sends those to
-// the 4-wave entry; this path only keeps a mistaken plan correct): one f32 dot product per element.
-template <typename AT, typename BT, typename CT, int K>
+// Guard body of the 8-wave and 128-tile entries for inputs the DMA cannot take (the launch plan
+// sends those to the 4-wave entry; this path only keeps a mistaken plan correct): one f32 dot
+// product per element of the T x T tile.
+template <typename AT, typename BT, typename CT, int K, int T = 256>
 static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict__ A, const BT* __restrict__ B,
                                                             CT* __restrict__ C, int ldb, int M, int N, int m0, int n0) {
-  for (int e = threadIdx.x; e < 256 * 256; e += blockDim.x) {
-    const int row = m0 + (e >> 8), col = n0 + (e & 255);
+  for (int e = threadIdx.x; e < T * T; e += blockDim.x) {
+    const int row = m0 + e / T, col = n0 + e % T;
     if (row >= M || col >= N) continue;
     float acc = 0.0f;
     for (int k = 0; k < K; ++k)
       acc = __builtin_fmaf((float)(_Float16)A[(size_t)row * K + k], (float)(_Float16)B[(size_t)k * ldb + col], acc);
     C[(size_t)row * ldb + col] = (CT)acc;
   }
+}
+
+// 128 x 128 tile body for launches whose 256 x 256 grid would leave CUs idle: 4 waves of 64 x 64
+// (2 x 2 accumulators of 32x32), the same DMA ring, swizzles and range checks as the 256 bodies
+// with 16 KB stages (64 KB of LDS, so two workgroups share a CU and overlap each other's waits).
+// Per stage: wait for this wave's DMA, barrier, issue this wave's quarter of the DMA three stages
+// ahead, read the stage's fragments, 8 MFMAs.
+template <typename CT, int K>
+static __device__ __forceinline__ void eas_gemm_t128(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+                                                     CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
+                                                     _Float16* smem) {
+  constexpr int BM = 128, BN = 128, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
+  constexpr int STAGE_H = BM * BK;  // halves per operand per stage (8 KB)
+  _Float16* As = smem;
+  _Float16* Bs = smem + NSTAGE * STAGE_H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
+  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
+  // DMA instruction q = 2 wave + i writes 1 KB of a stage.  A: rows 16q + lane/4, chunk lane%4
+  // stored at chunk ^ ((row/4)%4).  B: rows (k) 4q + lane/16, chunk lane%16 stored at chunk ^ 4(row%4).
+  uint32_t a_off[2], b_off[2];
+  int a_k[2], b_k[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int q = wave * 2 + i;
+    const int r_a = 16 * q + (lane >> 2);
+    const int c_a = (lane & 3) ^ ((r_a >> 2) & 3);
+    a_off[i] = ((uint32_t)(m0 + r_a) * (uint32_t)K + (uint32_t)(c_a * 8)) * 2u;
+    a_k[i] = c_a * 8;
+    const int r_b = 4 * q + (lane >> 4);
+    const int c_b = (lane & 15) ^ (4 * (r_b & 3));
+    b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
+    b_k[i] = r_b;
+  }
+  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS _Float16*)As, lds_b = (uint32_t)(size_t)(EAS_LDS _Float16*)Bs;
+  auto dma_stage = [&](int kt) {
+    const int s = kt % NSTAGE;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t dst = (uint32_t)((s * STAGE_H + (wave * 2 + i) * 512) * 2);
+      uint32_t off = a_off[i] + (uint32_t)(kt * BK * 2);
+      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: past the range -> zeros
+      eas_dma16(ra, off, lds_a + dst);
+      uint32_t offb = b_off[i] + (uint32_t)kt * (uint32_t)(BK * 2) * (uint32_t)ldb;
+      if (K % BK != 0 && kt * BK + b_k[i] >= K) offb = 0x80000000u;  // B rows past K
+      eas_dma16(rb, offb, lds_b + dst);
+    }
+  };
+  int fa_off[2][2], fb_off[2][2][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = wm * 64 + i * 32 + (lane & 31);
+      const int c = (2 * ks + (lane >> 5)) ^ ((r >> 2) & 3);
+      fa_off[ks][i] = r * BK + c * 8;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        // ds_read_b64_tr_b16: in each 16-lane group, source lane kq addresses row kq/4, columns 4(kq%4)..+3
+        const int gq = lane >> 4, kq = lane & 15;
+        const int row = 16 * ks + 8 * (gq >> 1) + 4 * h + (kq >> 2);
+        const int col = wn * 64 + i * 32 + 16 * (gq & 1) + 4 * (kq & 3);
+        const int chunk = (col >> 3) ^ (4 * (row & 3));
+        fb_off[ks][i][h] = row * BN + chunk * 8 + (col & 7);
+      }
+    }
+  eas_f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
+  auto wait_stage = [&](int later) {  // `later` newer stages (4 loads each) may stay in flight
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));
+    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+  };
+#pragma unroll
+  for (int s = 0; s < NSTAGE - 1; ++s)
+    if (s < KT) dma_stage(s);
+  for (int kt = 0; kt < KT; ++kt) {
+    // this wave's loads of stage kt landed; the barrier makes every wave's visible and frees
+    // stage kt-1, which the DMA of stage kt+3 refills
+    wait_stage(KT - 1 - kt < NSTAGE - 2 ? KT - 1 - kt : NSTAGE - 2);
+    __syncthreads();
+    if (kt + NSTAGE - 1 < KT) dma_stage(kt + NSTAGE - 1);
+    const _Float16* as = As + (kt % NSTAGE) * STAGE_H;
+    const _Float16* bs = Bs + (kt % NSTAGE) * STAGE_H;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      eas_h8 fa[2], fb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        fa[i] = *(const eas_h8*)(as + fa_off[ks][i]);
+        const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][0]));
+        const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][1]));
+        const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
+        fb[i] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+      }
+      if constexpr (K % 8 != 0) {
+        if (kt == KT - 1) {  // tail stage: halves at k >= K hold the next row of A
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const bool past = kt * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) fa[i][e] = past ? (_Float16)0.0f : fa[i][e];
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  const bool full = (m0 + BM <= M) && (n0 + BN <= N);
+  // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
+        const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+        if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
+      }
 }
 
 // Skinny path (M <= 16, decode-like): one workgroup per 64 columns, the four waves split K.
@@ -747,10 +876,11 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
       }
 }
 
-// Origin of this workgroup's 256 x 256 tile: XCD-contiguous (workgroup w runs on XCD w % 8, so
+// Origin of this workgroup's BM x BN tile: XCD-contiguous (workgroup w runs on XCD w % 8, so
 // each XCD gets a contiguous range of tiles), grouped 4 tile-rows high for L2 reuse.
+template <int BM = 256, int BN = 256>
 static __device__ __forceinline__ void eas_tile_origin(int M, int N, int& m0, int& n0) {
-  constexpr int BM = 256, BN = 256, GROUP_M = 4;
+  constexpr int GROUP_M = 4;
   const int tilesM = (M + BM - 1) / BM, tilesN = (N + BN - 1) / BN, T = tilesM * tilesN;
   const int w = blockIdx.x;
   const int t = (T % 8 == 0) ? (w % 8) * (T / 8) + w / 8 : w;
@@ -803,8 +933,9 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
 }
 """
 
-# The 8-wave entry (f16 A and B): the launch plan picks it for launches above the skinny
-# height whose operands the DMA can take; the same tile grid as the 4-wave entry.
+# The 8-wave entry and the 128 x 128 tile entry (f16 A and B): the launch plan picks one for
+# launches above the skinny height whose operands the DMA can take (the 128-tile one when the
+# 256 x 256 grid would leave CUs idle).
 _TEMPLATE_PP_ENTRY = r"""
 extern "C" __global__ __launch_bounds__(512) void @NAME@__pp(
     @PARAMS@) {
@@ -827,6 +958,29 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__pp(
     eas_gemm_pp<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
   else
     eas_gemm_elementwise<AT, BT, CT, K>(A, B, C, ldb, M, N, m0, n0);
+}
+
+extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
+    @PARAMS@) {
+  constexpr int K = @K@;
+  typedef @AT@ AT;
+  typedef @BT@ BT;
+  typedef @CT@ CT;
+  const int ldb = (int)@LDB@;
+  // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
+  const AT* __restrict__ A = @A@ + (size_t)__eas_m_lo * K;
+  const BT* __restrict__ B = @B@ + __eas_n_lo;
+  CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
+  const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
+  __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 4 * 128 * 32];  // DMA ring 4 x 2 x 8 KB
+  const bool dma_ok = (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
+                      ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
+  int m0, n0;
+  eas_tile_origin<128, 128>(M, N, m0, n0);
+  if (dma_ok)
+    eas_gemm_t128<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
+  else
+    eas_gemm_elementwise<AT, BT, CT, K, 128>(A, B, C, ldb, M, N, m0, n0);
 }
 """
 
@@ -1012,5 +1166,6 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "col_base": spec.col_base,
         "col_masked": spec.col_masked,
         "pp_entry": f"{ir.name}__pp" if pingpong else None, "pp_threads": PP_THREADS,
+        "t128_entry": f"{ir.name}__t128" if pingpong else None,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

@@ -977,7 +977,8 @@ def _numel(v: Any) -> int | None:
     return None
 
 
-def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x: int | None) -> Any:
+def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x: int | None,
+              compute_units: int = 256) -> Any:
     """Launch plan of a lifted GEMM for a reference grid ``groups``.
 
     The launch covers rows [m_lo, m_hi) and columns [n_lo, n_hi): the origin is
@@ -1016,21 +1017,36 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
     if m_hi - m_lo <= p.get("skinny_m", 0):
         # the kernel's skinny path: one workgroup per skinny_n columns, all rows
         return LaunchPlan((-(-(n_hi - n_lo) // p["skinny_n"]), 1, 1), (p["threads"], 1, 1), hidden)
-    tiles = -(-(m_hi - m_lo) // p["BM"]) * -(-(n_hi - n_lo) // p["BN"])
-    if p.get("pp_entry") and _pingpong_fits(p, runtime_args, K, ldb, m_hi - m_lo, n_lo, n_hi - n_lo):
+    m, n = m_hi - m_lo, n_hi - n_lo
+    tiles = -(-m // p["BM"]) * -(-n // p["BN"])
+    choice = _gemm_entry_choice()
+    if p.get("pp_entry") and choice != "4wave" and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
+        # 128 x 128 tiles when 256 x 256 ones would fill at most half of the CUs
+        if choice == "tile128" or (choice == "auto" and 2 * tiles <= compute_units):
+            return LaunchPlan((-(-m // 128) * -(-n // 128), 1, 1), (p["threads"], 1, 1), hidden,
+                              entry=p["t128_entry"])
         return LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
     return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
 
 
-def _pingpong_fits(p: dict, runtime_args: Any, K: int, ldb: int, m: int, n_lo: int, n: int) -> bool:
-    """Whether the 8-wave entry's DMA takes this launch: every row of A and B (after the
-    move to the rectangle's origin) 4-byte aligned, each operand's extent under 2 GiB.
-    Device addresses are known here for torch tensors; numpy inputs are staged into fresh
-    allocations, and the entry re-checks the addresses it gets (a misaligned operand
-    takes its slow element-wise guard rather than a wrong result).
-    ``EAS_HIP_GEMM_PINGPONG=0`` keeps every launch on the 4-wave entry."""
-    if os.environ.get("EAS_HIP_GEMM_PINGPONG", "1").strip() == "0":
-        return False
+_ENTRY_CHOICES = ("auto", "8wave", "tile128", "4wave")
+
+
+def _gemm_entry_choice() -> str:
+    """``EAS_HIP_GEMM_ENTRY``: ``auto`` (default), or one entry for every f16 launch
+    the DMA takes: ``8wave``, ``tile128`` or ``4wave``."""
+    v = os.environ.get("EAS_HIP_GEMM_ENTRY", "auto").strip().lower() or "auto"
+    if v not in _ENTRY_CHOICES:
+        raise ValueError(f"EAS_HIP_GEMM_ENTRY must be one of {_ENTRY_CHOICES}, got {v!r}")
+    return v
+
+
+def _dma_fits(p: dict, runtime_args: Any, K: int, ldb: int, m: int, n_lo: int, n: int) -> bool:
+    """Whether the DMA entries take this launch: every row of A and B (after the move to
+    the rectangle's origin) 4-byte aligned, each operand's extent under 2 GiB.  Device
+    addresses are known here for torch tensors; numpy inputs are staged into fresh
+    allocations, and the entries re-check the addresses they get (a misaligned operand
+    takes their slow element-wise guard rather than a wrong result)."""
     if K % 2 or ldb % 2 or n_lo % 2:
         return False
     if m * K * 2 >= 1 << 31 or ((K - 1) * ldb + n) * 2 >= 1 << 31:

@@ -163,7 +163,7 @@ def plan_launch(
     if geo.kind == "gemm":
         from ..codegen.gemm_lift import plan_gemm
 
-        return plan_gemm(geo, groups, runtime_args, live_x)
+        return plan_gemm(geo, groups, runtime_args, live_x, compute_units)
     raise ValueError(f"unknown kernel geometry: {geo.kind!r}")
 
 

@@ -194,9 +194,10 @@ def test_full_size_4096_sampled_rows(gpu_runtime, k):
     assert ops.rel_err(c[rows], ref) <= 1e-5 * math.sqrt(k)
 
 
-@pytest.mark.parametrize("mnk", [(300, 520, 200), (257, 264, 72), (520, 256, 1000), (64, 128, 36), (17, 300, 8)])
-def test_eight_and_four_wave_entries_agree(gpu_runtime, monkeypatch, mnk):
-    """The 8-wave (ping-pong) entry and the 4-wave entry on the same launch: both within
+@pytest.mark.parametrize("mnk", [(300, 520, 200), (257, 264, 72), (520, 256, 1000), (64, 128, 36), (17, 300, 8),
+                                 (130, 260, 4100)])
+def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
+    """The 8-wave (ping-pong), 128-tile and 4-wave entries on the same launch: each within
     tolerance of float64 (edge tiles, K tails of 8 and of 4, one stage, 17 rows)."""
     from easy_as_amd.runtime.hip import plan_launch
 
@@ -205,26 +206,29 @@ def test_eight_and_four_wave_entries_agree(gpu_runtime, monkeypatch, mnk):
     ck = K.matmul_mma_kernel.compile(a, b, np.zeros(1, np.float32), m, n, BM=32, BN=32, BK=8, K=k, NT=512)
     args = {"a": a, "b": b, "c": np.zeros(m * n, np.float32), "M": m, "N": n}
     outs = {}
-    for flag, entry in (("1", "matmul_mma_kernel__pp"), ("0", None)):
-        monkeypatch.setenv("EAS_HIP_GEMM_PINGPONG", flag)
+    for choice, entry in (("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128"), ("4wave", None)):
+        monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
         assert plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args)).entry == entry
         c = np.full(m * n, np.nan, np.float32)
         _mma(K.matmul_mma_kernel, a, b, c, m, n, k)
         _check(c, a, b, m, n, k)
-        outs[flag] = c
+        outs[choice] = c.reshape(m, n).astype(np.float64)
     # the same MFMA sequence per output element: equal up to f32 rounding
-    assert ops.rel_err(outs["1"].reshape(m, n), outs["0"].reshape(m, n).astype(np.float64)) <= 1e-6
+    assert ops.rel_err(outs["8wave"], outs["4wave"]) <= 1e-6
+    assert ops.rel_err(outs["tile128"], outs["4wave"]) <= 1e-6
 
 
-def test_eight_wave_entry_guard_for_an_operand_it_cannot_see(gpu_runtime):
+@pytest.mark.parametrize("choice,entry", [("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128")])
+def test_dma_entry_guard_for_an_operand_it_cannot_see(gpu_runtime, monkeypatch, choice, entry):
     """An eas.Tensor viewing torch memory at a 2-byte offset: the plan cannot see the address,
-    picks the 8-wave entry, and the entry's own check sends the launch to its element-wise
-    guard.  The same view as a torch tensor is planned onto the 4-wave entry."""
+    picks a DMA entry, and the entry's own check sends the launch to its element-wise guard.
+    The same view as a torch tensor is planned onto the 4-wave entry."""
     import torch
 
     import eas
     from easy_as_amd.runtime.hip import plan_launch
 
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
     m, n, k = 96, 160, 64
     a, b = _inputs(m, n, k, seed=5)
     store = torch.zeros(m * k + 1, dtype=torch.float16, device="cuda")
@@ -236,7 +240,7 @@ def test_eight_wave_entry_guard_for_an_operand_it_cannot_see(gpu_runtime):
     grid = (K.cdiv(m, 32), K.cdiv(n, 32), 1)
     assert plan_launch(ck, {"a": ta, "b": tb, "M": m, "N": n}, grid=grid).entry is None
     ea = eas.tensor(ta, device="hip")
-    assert plan_launch(ck, {"a": ea, "b": tb, "M": m, "N": n}, grid=grid).entry == "matmul_mma_kernel__pp"
+    assert plan_launch(ck, {"a": ea, "b": tb, "M": m, "N": n}, grid=grid).entry == entry
     for a_arg in (ta, ea):
         tc = torch.full((m * n,), float("nan"), device="cuda", dtype=torch.float32)
         _mma(K.matmul_mma_kernel, a_arg, tb, tc, m, n, k)

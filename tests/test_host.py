@@ -195,9 +195,9 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, 300, 520, BM=32, BN=32, BK=8, K=200, NT=512)
     assert ck.geometry.kind == "gemm"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(17, 10, 1))
-    assert plan.hidden == (0, 300, 0, 520) and plan.grid == (2 * 3, 1, 1)
-    # f16 operands the DMA takes run on the 8-wave entry, on the same tile grid
-    assert plan.block == (512, 1, 1) and plan.entry == "matmul_mma_kernel__pp"
+    # 6 tiles of 256 x 256 would leave CUs idle: 3 x 5 tiles of 128 x 128 on the 128-tile entry
+    assert plan.hidden == (0, 300, 0, 520) and plan.grid == (3 * 5, 1, 1)
+    assert plan.block == (256, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(3, 2, 1))  # partial grid: 64 x 96 rectangle
     assert plan.hidden == (0, 64, 0, 96) and plan.grid == (1, 1, 1)
     # M <= 16 (decode-like): one workgroup per 64 columns, on the 4-wave entry
@@ -205,7 +205,20 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
     assert plan.hidden == (0, 16, 0, 14336) and plan.grid == (224, 1, 1)
     assert plan.block == (256, 1, 1) and plan.entry is None
     plan = plan_launch(ck, {"M": 17, "N": 14336}, grid=(448, 1, 1))
-    assert plan.hidden == (0, 17, 0, 14336) and plan.grid == (56, 1, 1) and plan.entry == "matmul_mma_kernel__pp"
+    assert plan.hidden == (0, 17, 0, 14336) and plan.grid == (112, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
+
+
+@pytest.mark.parametrize("mn,entry,grid", [((4096, 4096), "__pp", 256), ((3072, 3072), "__pp", 144),
+                                           ((2560, 2560), "__t128", 400), ((2048, 2048), "__t128", 256),
+                                           ((8192, 8192), "__pp", 1024)])
+def test_plan_tile_size_follows_the_cu_count(mn, entry, grid):
+    # 256 x 256 tiles unless they would fill at most half of the 256 CUs
+    m, n = mn
+    f16, f32 = np.zeros(1, np.float16), np.zeros(1, np.float32)
+    ck = K.matmul_mma_kernel.compile(f16, f16, f32, m, n, BM=32, BN=32, BK=8, K=64, NT=512)
+    plan = plan_launch(ck, {"M": m, "N": n}, grid=(n // 32, m // 32, 1))
+    assert plan.entry == "matmul_mma_kernel" + entry and plan.grid == (grid, 1, 1)
+    assert plan.block == ((512 if entry == "__pp" else 256), 1, 1)
 
 
 class _FakeTorchTensor:
@@ -219,10 +232,11 @@ class _FakeTorchTensor:
         return self._numel
 
 
-def test_plan_pingpong_entry_only_for_operands_the_dma_takes(monkeypatch):
+def test_plan_dma_entries_only_for_operands_the_dma_takes(monkeypatch):
     f16, f32 = np.zeros(1, np.float16), np.zeros(1, np.float32)
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, 512, 512, BM=32, BN=32, BK=8, K=64, NT=512)
     args = {"M": 512, "N": 512}
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "8wave")
     assert plan_launch(ck, args, grid=(16, 16, 1)).entry == "matmul_mma_kernel__pp"
     # odd row stride of B: rows are not 4-byte aligned
     assert plan_launch(ck, {"M": 512, "N": 511}, grid=(16, 16, 1)).entry is None
@@ -233,13 +247,21 @@ def test_plan_pingpong_entry_only_for_operands_the_dma_takes(monkeypatch):
     assert plan_launch(ck, even, grid=(16, 16, 1)).entry == "matmul_mma_kernel__pp"
     # odd K (rows of A 2-byte aligned) and f32 inputs have no 8-wave entry
     ck_odd = K.matmul_mma_kernel.compile(f16, f16, f32, 512, 512, BM=32, BN=32, BK=8, K=63, NT=512)
-    assert ck_odd.geometry.params["pp_entry"] is None and "__pp" not in ck_odd.src
+    assert ck_odd.geometry.params["pp_entry"] is None and "__pp" not in ck_odd.src and "__t128" not in ck_odd.src
     assert plan_launch(ck_odd, args, grid=(16, 16, 1)).entry is None
     ck32 = K.matmul_mma_kernel.compile(f32, f32, f32, 512, 512, BM=32, BN=32, BK=8, K=64, NT=512)
     assert ck32.geometry.params["pp_entry"] is None and "__pp" not in ck32.src
     assert plan_launch(ck32, args, grid=(16, 16, 1)).block == (256, 1, 1)
-    monkeypatch.setenv("EAS_HIP_GEMM_PINGPONG", "0")
+    # the entry switch: one entry for every launch the DMA takes, or the automatic choice
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "tile128")
+    assert plan_launch(ck, args, grid=(16, 16, 1)).entry == "matmul_mma_kernel__t128"
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "4wave")
     assert plan_launch(ck, args, grid=(16, 16, 1)).entry is None
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "auto")
+    assert plan_launch(ck, args, grid=(16, 16, 1)).entry == "matmul_mma_kernel__t128"
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "fastest")
+    with pytest.raises(ValueError):
+        plan_launch(ck, args, grid=(16, 16, 1))
 
 
 # ---- kernel-argument packing through a recording extension ------------------------
