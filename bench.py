@@ -77,8 +77,12 @@ def _inputs(n: int, seeds: tuple[int, ...]) -> list[np.ndarray]:
     return [np.random.default_rng(s).standard_normal(n, dtype=np.float32) for s in seeds]
 
 
+EVENT_TRIALS = 5
+
+
 def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch, **launch) -> tuple[float, float]:
-    """(wall ms/step bracketed by device syncs, HIP-event ms/launch on the launch stream)."""
+    """(wall ms/step bracketed by device syncs, HIP-event ms/launch on the launch stream: the
+    median of EVENT_TRIALS trials of ``steps`` back-to-back launches)."""
     for _ in range(warmup):
         rt.run(ck, rargs, meta, sync=False, **launch)
     rt.synchronize()
@@ -89,8 +93,8 @@ def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch, **launch) 
     rt.synchronize()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    ev_ms = rt.benchmark(ck, rargs, meta, repeat=steps, warmup=0, **launch) * 1e3
-    return wall_ms, ev_ms
+    trials = sorted(rt.benchmark(ck, rargs, meta, repeat=steps, warmup=0, **launch) for _ in range(EVENT_TRIALS))
+    return wall_ms, trials[EVENT_TRIALS // 2] * 1e3
 
 
 def _matmul_inputs(name: str) -> tuple[np.ndarray, np.ndarray]:
