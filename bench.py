@@ -69,6 +69,11 @@ MATMULS = {
 }
 
 
+# rocprofv3 counter summaries (profiles/<name>.pmc.json) that give a matmul line its HBM traffic
+MATMUL_PROFILES = {"mma": "mma_f16_4096", "decode": "decode_f16_16x14336x4096", "prefill": "prefill_f16_8192",
+                   "tiled1024": "tiled_f32_1024"}
+
+
 def _log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -355,7 +360,7 @@ def _matmul_main(args, rt, torch) -> int:
     res = _matmul(args.workload, rt, torch, args.steps, args.warmup)
     _, m, n, k, _, _, desc = MATMULS[args.workload]
     traffic = None
-    pmc = ROOT / "profiles" / f"{args.workload}_f16.pmc.json"
+    pmc = ROOT / "profiles" / f"{MATMUL_PROFILES.get(args.workload, args.workload)}.pmc.json"
     if pmc.exists():
         traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
     tiled = args.workload.startswith("tiled")
