@@ -102,17 +102,36 @@ def classify_arg(v: Any) -> RuntimeArgSig:
     return RuntimeArgSig("scalar", _scalar_dtype(v), None)
 
 
+_NP_BUFFER_KEYS = {np.dtype(np.float32): ("buffer", DType.F32, "cpu"), np.dtype(np.float16): ("buffer", DType.F16, "cpu")}
+_SCALAR_KEYS = {int: ("scalar", DType.U32, None), float: ("scalar", DType.F32, None), bool: ("scalar", DType.BOOL, None)}
+
+
+def _arg_key(v: Any) -> tuple[str, DType, str | None]:
+    """``(kind, dtype, device)`` of ``classify_arg``, with the per-launch common cases
+    (NumPy f32/f16 arrays, torch tensors, Python scalars) answered without building a
+    ``RuntimeArgSig``."""
+    t = type(v)
+    if t is np.ndarray:
+        key = _NP_BUFFER_KEYS.get(v.dtype)
+        if key is not None:
+            return key
+    elif t in _SCALAR_KEYS:
+        return _SCALAR_KEYS[t]
+    else:
+        torch = _torch()
+        if torch is not None and isinstance(v, torch.Tensor):
+            return ("buffer", _torch_buffer_dtype(v), v.device.type)
+    s = classify_arg(v)
+    return (s.kind, s.dtype, s.device)
+
+
 def runtime_arg_signature(runtime_args: Mapping[str, Any]) -> tuple[tuple[str, Any], ...]:
     """Cache key part for runtime args: ``(name, (kind, dtype, device))`` sorted by name.
 
     Scalar *values* are deliberately not part of it: they are kernel arguments,
     not trace-time constants (reference ``compiler.py:41-54``).
     """
-    out = []
-    for name, value in runtime_args.items():
-        s = classify_arg(value)
-        out.append((name, (s.kind, s.dtype, s.device)))
-    return tuple(sorted(out))
+    return tuple(sorted((name, _arg_key(value)) for name, value in runtime_args.items()))
 
 
 # ---------------------------------------------------------------------------

@@ -49,6 +49,12 @@ class Kernel:
         self.meta_params = {
             name for name, p in self.sig.parameters.items() if annotations.get(name, p.annotation) is constexpr
         }
+        # plain signatures (every parameter positional-or-keyword) bind without inspect
+        params = list(self.sig.parameters.values())
+        self._plain = all(p.kind is inspect.Parameter.POSITIONAL_OR_KEYWORD for p in params)
+        self._names = tuple(p.name for p in params)
+        self._name_set = frozenset(self._names)
+        self._defaults = {p.name: p.default for p in params if p.default is not inspect.Parameter.empty}
         self._cache: dict[tuple[Any, Any], CompiledKernel] = {}
         self._autotune_spec: AutotuneSpec | None = None
         self._tuned_cache: dict[tuple[Any, ...], Config] = {}
@@ -106,10 +112,34 @@ class Kernel:
 
     # -- binding / specialisation --------------------------------------------------
     def _bind_and_split(self, /, *args: Any, **kwargs: Any) -> tuple[dict[str, Any], dict[str, Any]]:
-        bound = self.sig.bind(*args, **kwargs)
-        bound.apply_defaults()
-        meta = {k: bound.arguments.pop(k) for k in list(bound.arguments) if k in self.meta_params}
-        return meta, dict(bound.arguments)
+        bound = self._bind_plain(args, kwargs) if self._plain else None
+        if bound is None:  # not a plain signature, or a binding error that inspect reports
+            b = self.sig.bind(*args, **kwargs)
+            b.apply_defaults()
+            bound = b.arguments
+        meta = {k: v for k, v in bound.items() if k in self.meta_params}
+        return meta, {k: v for k, v in bound.items() if k not in self.meta_params}
+
+    def _bind_plain(self, args: tuple[Any, ...], kwargs: dict[str, Any]) -> dict[str, Any] | None:
+        """``Signature.bind`` + ``apply_defaults`` for positional-or-keyword parameters, in
+        parameter order; None when the call does not bind (inspect then raises its TypeError)."""
+        names = self._names
+        if len(args) > len(names) or any(k not in self._name_set for k in kwargs):
+            return None
+        given = dict(zip(names, args))
+        for k, v in kwargs.items():
+            if k in given:
+                return None
+            given[k] = v
+        bound = {}
+        for name in names:
+            if name in given:
+                bound[name] = given[name]
+            elif name in self._defaults:
+                bound[name] = self._defaults[name]
+            else:
+                return None
+        return bound
 
     def _compile_from_split(self, meta: dict[str, Any], runtime_args: dict[str, Any]) -> CompiledKernel:
         key = (tuple(sorted(meta.items())), runtime_arg_signature(runtime_args))

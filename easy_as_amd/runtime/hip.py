@@ -17,7 +17,6 @@ from __future__ import annotations
 import hashlib
 import os
 import struct
-import weakref
 from collections import deque
 from pathlib import Path
 from typing import Any, Mapping
@@ -180,7 +179,6 @@ class HipRuntime:
         self._kernels: dict[tuple[str, str], Any] = {}
         self._pending: deque[Any] = deque()
         self._max_in_flight: int | None = None
-        self._ptr_cache: dict[int, tuple[weakref.ref, Any]] = {}
         self._torch: Any = None
         self._torch_probed = False
         self._arch_checked = ext is not None
@@ -243,19 +241,6 @@ class HipRuntime:
         return k
 
     # -- arguments ---------------------------------------------------------------
-    def _torch_pointer(self, t: Any) -> Any:
-        key = id(t)
-        hit = self._ptr_cache.get(key)
-        if hit is not None and hit[0]() is t:
-            return hit[1]
-        buf = self._mod().wrap_pointer(int(t.data_ptr()), int(t.numel() * t.element_size()), t)
-        try:
-            weakref.finalize(t, self._ptr_cache.pop, key, None)
-            self._ptr_cache[key] = (weakref.ref(t), buf)
-        except TypeError:
-            pass
-        return buf
-
     def build_argv(self, ir: IRModule, runtime_args: Mapping[str, Any], writes: frozenset[str]) -> tuple[list, list, list, Any]:
         """Argument list for ``_hip.launch`` plus host copy-backs and the stream to use."""
         mod = self._mod()
@@ -264,7 +249,7 @@ class HipRuntime:
         writable: list[bool] = []
         copy_back: list[tuple[Any, np.ndarray]] = []
         staged: dict[int, Any] = {}
-        stream = None
+        cuda_device = None
         for arg in ir.args:
             v = runtime_args[arg.name]
             if arg.kind == "scalar":
@@ -274,19 +259,20 @@ class HipRuntime:
             want = np.float16 if arg.dtype == DType.F16 else np.float32
             w = arg.name in writes
             if torch is not None and isinstance(v, torch.Tensor):
-                t = v.detach()
-                if t.dtype != (torch.float16 if arg.dtype == DType.F16 else torch.float32):
-                    raise TypeError(f"{arg.name!r} must be {np.dtype(want).name}, got {t.dtype}")
-                if t.device.type == "cuda":
-                    if not t.is_contiguous():
+                if v.dtype != (torch.float16 if arg.dtype == DType.F16 else torch.float32):
+                    raise TypeError(f"{arg.name!r} must be {np.dtype(want).name}, got {v.dtype}")
+                dev = v.device
+                if dev.type == "cuda":
+                    if not v.is_contiguous():
                         raise ValueError(f"{arg.name!r} must be contiguous")
-                    argv.append(self._torch_pointer(t))
+                    # a non-owning view of the tensor's memory that keeps the tensor alive
+                    argv.append(mod.wrap_pointer(v.data_ptr(), v.numel() * v.element_size(), v))
                     writable.append(w)
-                    stream = torch.cuda.current_stream(t.device).cuda_stream
+                    cuda_device = dev
                     continue
-                if t.device.type != "cpu":
-                    raise TypeError(f"unsupported torch device for {arg.name!r}: {t.device}")
-                v = t.contiguous().numpy()
+                if dev.type != "cpu":
+                    raise TypeError(f"unsupported torch device for {arg.name!r}: {dev}")
+                v = v.detach().contiguous().numpy()
             if _is_eas_tensor(v):
                 if v.device == "hip":
                     if np.dtype(v.dtype) != np.dtype(want):
@@ -312,6 +298,8 @@ class HipRuntime:
                 writable.append(w)
                 continue
             raise TypeError(f"expected numpy.ndarray, eas.Tensor or torch.Tensor for {arg.name!r}, got {type(v)!r}")
+        # launches with torch GPU tensors go on torch's current stream, ordered with torch's own work
+        stream = None if cuda_device is None else torch.cuda.current_stream(cuda_device).cuda_stream
         return argv, writable, copy_back, stream
 
     # -- launching ------------------------------------------------------------------

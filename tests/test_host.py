@@ -370,3 +370,35 @@ def test_autotune_benchmarks_once_per_key_and_keeps_fastest(monkeypatch):
     assert len(rt.benchmarked) == 4 and rt.ran == [256, 256]
     _tuned_add(x, x, x, 2000)  # a new key value is tuned again
     assert len(rt.benchmarked) == 8 and rt.ran[-1] == 256
+
+
+# ---- argument binding ---------------------------------------------------------------
+
+def test_fast_binding_matches_inspect():
+    import inspect
+
+    def fn(a, b, c, N, BLOCK: eas.constexpr = 256, scale=1.5):
+        pass
+
+    k = eas_kernel.Kernel(fn)
+    assert k._plain
+    x = np.zeros(4, np.float32)
+    calls = [((x, x, x, 4), {}), ((x, x), {"c": x, "N": 7}), ((x, x, x, 4, 128), {"scale": 2.0}),
+             ((), {"a": x, "b": x, "c": x, "N": 1, "BLOCK": 64})]
+    for args, kw in calls:
+        b = inspect.signature(fn).bind(*args, **kw)
+        b.apply_defaults()
+        want_meta = {n: v for n, v in b.arguments.items() if n == "BLOCK"}
+        want_rt = {n: v for n, v in b.arguments.items() if n != "BLOCK"}
+        meta, rt = k._bind_and_split(*args, **kw)
+        assert meta == want_meta and list(rt) == list(want_rt) and all(rt[n] is want_rt[n] for n in rt)
+    # binding errors are inspect's TypeErrors
+    for args, kw in [((x, x, x, 4, 1, 2, 3), {}), ((x, x), {}), ((x, x, x, 4), {"a": x}), ((x, x, x, 4), {"M": 1})]:
+        with pytest.raises(TypeError):
+            k._bind_and_split(*args, **kw)
+
+    def kwonly(a, *, N):
+        pass
+
+    assert not eas_kernel.Kernel(kwonly)._plain
+    assert eas_kernel.Kernel(kwonly)._bind_and_split(x, N=3) == ({}, {"a": x, "N": 3})

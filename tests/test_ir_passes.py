@@ -211,6 +211,21 @@ def test_compile_cache_ignores_scalar_values():
     assert ck3 is not ck1
 
 
+def test_specialisation_key_fast_path_matches_classify_arg():
+    import torch
+
+    from eas.compiler import _arg_key, classify_arg
+
+    values = [f32(4), np.zeros(3, np.float16), 7, 2.5, True, np.float32(1.0), np.int64(3), np.float16(2.0),
+              torch.zeros(3), torch.zeros(3, dtype=torch.float16), eas.tensor(f32(4))]
+    for v in values:
+        s = classify_arg(v)
+        assert _arg_key(v) == (s.kind, s.dtype, s.device), type(v)
+    for bad in (np.zeros(3, np.float64), torch.zeros(3, dtype=torch.int32), "x"):
+        with pytest.raises(TypeError):
+            _arg_key(bad)
+
+
 def test_constexpr_removed_runtime_scalar_kept(monkeypatch):
     a = f32(8)
     src = K.add_kernel.to_hip(a, a, a, 8, BLOCK=256)
