@@ -156,6 +156,9 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
     rows = np.sort(np.random.default_rng(7).choice(m, min(m, 32), replace=False))
     ref = ops.matmul_ref(ha.reshape(m, k)[rows], hb.reshape(k, n))
     err = ops.rel_err(got[rows].astype(np.float64), ref)
+    # elementwise: |C - R| / (|R| + max|R| * 1e-3), the worst element of the sampled rows
+    diff = np.abs(got[rows].astype(np.float64) - ref)
+    elem_err = float(np.max(diff / (np.abs(ref) + 1e-3 * float(np.max(np.abs(ref)) or 1.0))))
     if tiled:
         tol, tol_s = 1e-5 * np.sqrt(k), "1e-5*sqrt(K)"
     elif out_dt == torch.float16:
@@ -178,6 +181,7 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
         "wall_TFLOP/s": round(flops / (wall_ms * 1e-3) / 1e12, 1), "ms_per_launch": round(ev_ms, 5),
         "min_hbm_GB/s": round(bytes_min / (ev_ms * 1e-3) / 1e9, 1),
         "parity": f"max rel err {err:.2e} on 32 sampled rows vs float64 (tol {tol_s})" + ("" if ok else " FAIL"),
+        "elementwise_err": float(f"{elem_err:.3e}"), "max_abs_err": float(f"{float(diff.max()):.3e}"),
         "parity_ok": ok, "compile_s": round(compile_s, 1),
     }
     _log(f"{name}: {res['TFLOP/s']} TFLOP/s ({100 * res['frac']:.1f}% of {peak}), {ev_ms:.4f} ms/launch, "
@@ -380,6 +384,7 @@ def _matmul_main(args, rt, torch) -> int:
         "data": "synthetic (seeded; see config)",
         "config": {"workload": desc, "M": m, "N": n, "K": k, "parallelism": "single GPU"},
         "parity": res["parity"],
+        "parity_elementwise_err": res["elementwise_err"], "parity_max_abs_err": res["max_abs_err"],
         "roofline": ({"bound": "hbm", "achieved": res["min_hbm_GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": res["frac_of_bound"], "traffic": traffic} if res["bound"] == "hbm" else
                      {"bound": res["bound"], "achieved": res["TFLOP/s"], "peak": res["peak_TFLOP/s"],
