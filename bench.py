@@ -321,7 +321,12 @@ def main() -> int:
         del ins, out
         torch.cuda.empty_cache()
         for name in ("mma", "mma_k4100", "decode", "prefill", "tiled1024", "tiled2048"):
-            extra[name] = _matmul(name, rt, torch, max(5, min(args.steps, 20)), max(2, min(args.warmup, 5)))
+            # a failing extra is reported in the line; it does not take the primary measurement with it
+            try:
+                extra[name] = _matmul(name, rt, torch, max(5, min(args.steps, 20)), max(2, min(args.warmup, 5)))
+            except Exception as e:  # noqa: BLE001
+                _log(f"{name}: {type(e).__name__}: {e}")
+                extra[name] = {"error": f"{type(e).__name__}: {e}"}
 
     bytes_per_launch = per_elem * N_ELEM
     traffic = None
