@@ -1109,6 +1109,141 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
 }
 """
 
+# The fp32 128 x 128 tile entry: four waves of 64 x 64 (2 x 2 accumulators of
+# v_mfma_f32_32x32x2_f32), a 3-stage ring of 32 KB stages.  A quarter of the
+# 64-tile kernel's DMA bytes per flop and four independent MFMA chains per wave;
+# the launch plan picks it when 128 x 128 tiles still give every CU one.
+_TEMPLATE_F32_T128 = r"""
+extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
+    @PARAMS@) {
+  constexpr int BM = 128, BN = 128, BK = 32, NSTAGE = 3, K = @K@, KT = (K + BK - 1) / BK;
+  constexpr int AST = BM * BK, BST = BK * BN, STF = AST + BST;  // floats per stage (32 KB)
+  const int ldb = (int)@LDB@;
+  // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
+  const float* __restrict__ A = @A@ + (size_t)__eas_m_lo * K;
+  const float* __restrict__ B = @B@ + __eas_n_lo;
+  float* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
+  const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
+  __shared__ __attribute__((aligned(1024))) float smem[NSTAGE * STF];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // XCD-contiguous, M-grouped tile order
+  const int tilesM = (M + BM - 1) / BM, tilesN = (N + BN - 1) / BN, T = tilesM * tilesN;
+  const int w = blockIdx.x;
+  const int t = (T % 8 == 0) ? (w % 8) * (T / 8) + w / 8 : w;
+  constexpr int GROUP_M = 4;
+  const int gsize = GROUP_M * tilesN, g = t / gsize, first_m = g * GROUP_M;
+  const int gm = min(tilesM - first_m, GROUP_M);
+  const int m0 = (first_m + (t % gsize) % gm) * BM, n0 = ((t % gsize) / gm) * BN;
+  const bool dma_ok = (K % 4 == 0) && (ldb % 4 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0) &&
+                      ((uint64_t)M * K * 4 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 4 < (1ull << 31));
+  if (!dma_ok) {
+    // guard for operands the launch plan could not see: one f32 dot product per element
+    for (int e = tid; e < BM * BN; e += 256) {
+      const int row = m0 + e / BN, col = n0 + e % BN;
+      if (row >= M || col >= N) continue;
+      float acc = 0.0f;
+      for (int k = 0; k < K; ++k) acc = __builtin_fmaf(A[(size_t)row * K + k], B[(size_t)k * ldb + col], acc);
+      C[(size_t)row * ldb + col] = acc;
+    }
+    return;
+  }
+  const int wm = wave >> 1, wn = wave & 1;
+  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 4u);
+  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 4u);
+  const uint32_t lds0 = (uint32_t)(size_t)(EAS_LDS float*)smem;
+  // DMA (1 KB per instruction, 4 A + 4 B per wave per stage, q = 4 wave + i):
+  //   A stage [128 rows][32 k]: rows 8q + lane/8, chunk lane%8 stored at chunk ^ ((row/2)%8)
+  //   B stage [32 k][128 n]:    rows 2q + lane/32, chunk lane%32 stored at chunk ^ 8((row/16)%2)
+  uint32_t a_off[4], b_off[4];
+  int a_k[4], b_r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = wave * 4 + i;
+    const int r = 8 * q + (lane >> 3), lc = (lane & 7) ^ ((r >> 1) & 7);
+    a_off[i] = ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)(lc * 4)) * 4u;
+    a_k[i] = lc * 4;
+    const int rr = 2 * q + (lane >> 5), lcb = (lane & 31) ^ (8 * ((rr >> 4) & 1));
+    b_off[i] = ((uint32_t)rr * (uint32_t)ldb + (uint32_t)(n0 + lcb * 4)) * 4u;
+    b_r[i] = rr;
+  }
+  auto dma = [&](int kt) {
+    const uint32_t st = lds0 + (uint32_t)((kt % NSTAGE) * STF) * 4u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t off = a_off[i] + (uint32_t)(kt * BK) * 4u;
+      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: zeros
+      eas_dma16(ra, off, st + (wave * 4 + i) * 1024);
+      uint32_t offb = b_off[i] + (uint32_t)(kt * BK) * (uint32_t)ldb * 4u;
+      if (K % BK != 0 && kt * BK + b_r[i] >= K) offb = 0x80000000u;
+      eas_dma16(rb, offb, st + AST * 4 + (wave * 4 + i) * 1024);
+    }
+  };
+  // MFMA step s (0..15) of a stage takes k = s + 16 c for lane half c = lane/32
+  const int c = lane >> 5;
+  int fa[2][4], fb[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ai = wm * 64 + i * 32 + (lane & 31);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fa[i][u] = ai * BK + (((4 * c + u) ^ ((ai >> 1) & 7)) * 4);
+    const int bj = wn * 64 + i * 32 + (lane & 31);
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int row = s + 16 * c;
+      fb[i][s] = AST + row * BN + (((bj >> 2) ^ (8 * ((row >> 4) & 1))) * 4) + (bj & 3);
+    }
+  }
+  eas_f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p)
+    if (p < KT) dma(p);
+  for (int kt = 0; kt < KT; ++kt) {
+    // this wave's loads of stage kt landed (a newer stage, 8 loads, may stay in flight); the barrier
+    // makes every wave's part visible and frees stage kt-1 for the next DMA
+    if (kt + 1 < KT) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
+    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+    __syncthreads();
+    if (kt + NSTAGE - 1 < KT) dma(kt + NSTAGE - 1);
+    const float* st = smem + (kt % NSTAGE) * STF;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {  // the stage's 16 steps in two halves of 8
+      eas_f32x4 a[2][2];
+      float b[2][8];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) a[i][u] = *(const eas_f32x4*)(st + fa[i][2 * h + u]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) b[i][s] = st[fb[i][8 * h + s]];
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s >> 2][s & 3], b[j][s], acc[i][j], 0, 0, 0);
+    }
+  }
+  // lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
+        const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+        if (row < M && col < N) C[(size_t)row * ldb + col] = acc[i][j][r];
+      }
+}
+"""
+
 TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
@@ -1150,7 +1285,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "@C@": pname[spec.c],
         "@LDB@": pname[spec.n_sym],
     }
-    src = _DMA_HELPERS + (_TEMPLATE_F32 if spec.f32 else _TEMPLATE)
+    src = _DMA_HELPERS + (_TEMPLATE_F32 + _TEMPLATE_F32_T128 if spec.f32 else _TEMPLATE)
     pingpong = f16_in and not spec.f32 and spec.K % 2 == 0  # odd K: rows of A are not 4-byte aligned
     if pingpong:
         src += _TEMPLATE_PP_ENTRY
@@ -1166,6 +1301,6 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "col_base": spec.col_base,
         "col_masked": spec.col_masked,
         "pp_entry": f"{ir.name}__pp" if pingpong else None, "pp_threads": PP_THREADS,
-        "t128_entry": f"{ir.name}__t128" if pingpong else None,
+        "t128_entry": f"{ir.name}__t128" if (pingpong or spec.f32) else None, "f32": spec.f32,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

@@ -1019,12 +1019,18 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
         return LaunchPlan((-(-(n_hi - n_lo) // p["skinny_n"]), 1, 1), (p["threads"], 1, 1), hidden)
     m, n = m_hi - m_lo, n_hi - n_lo
     tiles = -(-m // p["BM"]) * -(-n // p["BN"])
+    tiles128 = -(-m // 128) * -(-n // 128)
     choice = _gemm_entry_choice()
+    if p.get("f32"):
+        # fp32: 128 x 128 tiles (a quarter of the DMA bytes per flop) while they still give every CU one
+        if p.get("t128_entry") and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n, elem=4) and (
+                choice == "tile128" or (choice == "auto" and tiles128 >= compute_units)):
+            return LaunchPlan((tiles128, 1, 1), (p["threads"], 1, 1), hidden, entry=p["t128_entry"])
+        return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
     if p.get("pp_entry") and choice != "4wave" and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
         # 128 x 128 tiles when 256 x 256 ones would fill at most half of the CUs
         if choice == "tile128" or (choice == "auto" and 2 * tiles <= compute_units):
-            return LaunchPlan((-(-m // 128) * -(-n // 128), 1, 1), (p["threads"], 1, 1), hidden,
-                              entry=p["t128_entry"])
+            return LaunchPlan((tiles128, 1, 1), (p["threads"], 1, 1), hidden, entry=p["t128_entry"])
         return LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
     return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
 
@@ -1041,18 +1047,20 @@ def _gemm_entry_choice() -> str:
     return v
 
 
-def _dma_fits(p: dict, runtime_args: Any, K: int, ldb: int, m: int, n_lo: int, n: int) -> bool:
-    """Whether the DMA entries take this launch: every row of A and B (after the move to
-    the rectangle's origin) 4-byte aligned, each operand's extent under 2 GiB.  Device
-    addresses are known here for torch tensors; numpy inputs are staged into fresh
-    allocations, and the entries re-check the addresses they get (a misaligned operand
-    takes their slow element-wise guard rather than a wrong result)."""
-    if K % 2 or ldb % 2 or n_lo % 2:
+def _dma_fits(p: dict, runtime_args: Any, K: int, ldb: int, m: int, n_lo: int, n: int, elem: int = 2) -> bool:
+    """Whether the DMA entries take this launch.  f16 (``elem`` 2): every row of A and B
+    (after the move to the rectangle's origin) 4-byte aligned; fp32 (``elem`` 4): 16-byte
+    aligned; each operand's extent under 2 GiB.  Device addresses are known here for
+    torch tensors; numpy inputs are staged into fresh allocations, and the entries
+    re-check the addresses they get (a misaligned operand takes their slow element-wise
+    guard rather than a wrong result)."""
+    step = 2 if elem == 2 else 4  # elements per aligned unit: 4 bytes of f16, 16 bytes of f32
+    if K % step or ldb % step or n_lo % step:
         return False
-    if m * K * 2 >= 1 << 31 or ((K - 1) * ldb + n) * 2 >= 1 << 31:
+    if m * K * elem >= 1 << 31 or ((K - 1) * ldb + n) * elem >= 1 << 31:
         return False
     for name in (p["a"], p["b"]):
         ptr = getattr(runtime_args.get(name), "data_ptr", None)
-        if callable(ptr) and int(ptr()) % 4:
+        if callable(ptr) and int(ptr()) % (2 * step if elem == 2 else 16):
             return False
     return True

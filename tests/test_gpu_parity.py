@@ -273,9 +273,11 @@ def test_tiled_matmul_lifted_fp32_tolerance(gpu_runtime, mnk, tile):
     assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
 
 
-def test_tiled_matmul_split_launch_like_the_reference(gpu_runtime):
+@pytest.mark.parametrize("choice", ["auto", "tile128"])
+def test_tiled_matmul_split_launch_like_the_reference(gpu_runtime, monkeypatch, choice):
     # examples/matmul_tiled.py's split mode: the full-tile kernel on the interior, the masked
     # kernel with tile bases on the right strip, the bottom strip and the corner
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
     m, n, k = 100, 200, 64
     bm, bn, bk, nt = 32, 32, 32, 256
     a2, b2 = _tiled_inputs(m, n, k, seed=4)
@@ -289,6 +291,33 @@ def test_tiled_matmul_split_launch_like_the_reference(gpu_runtime):
     K.matmul_tiled_kernel(A, B, c, m, n, gy, gx, _grid=(K.cdiv(n, bn) - gx, K.cdiv(m, bm) - gy, 1), **meta)
     assert np.isfinite(c).all()
     assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
+
+
+@pytest.mark.parametrize("mnk", [(300, 260, 1000), (130, 300, 40), (257, 132, 36), (2048, 2048, 256)])
+def test_tiled_fp32_entries_agree(gpu_runtime, monkeypatch, mnk):
+    """The fp32 GEMM's 128 x 128-tile entry and its 64 x 64 default on the same launch (edge
+    tiles, K tails of 8 and 4 elements; 2048² picks the 128 tiles by itself)."""
+    from easy_as_amd.runtime.hip import plan_launch
+
+    m, n, k = mnk
+    a2, b2 = _tiled_inputs(m, n, k, seed=11)
+    A, B = a2.reshape(-1), b2.reshape(-1)
+    meta = dict(BM=32, BN=32, BK=32, K=k, NT=256)
+    grid = (K.cdiv(n, 32), K.cdiv(m, 32), 1)
+    ck = K.matmul_tiled_kernel.compile(A, B, np.zeros(1, np.float32), m, n, 0, 0, **meta)
+    args = {"a": A, "b": B, "c": np.zeros(m * n, np.float32), "M": m, "N": n, "PID_M_BASE": 0, "PID_N_BASE": 0}
+    auto = plan_launch(ck, args, grid=grid).entry
+    assert auto == ("matmul_tiled_kernel__t128" if m == 2048 else None)
+    ref = ops.matmul_ref(a2, b2)
+    outs = {}
+    for choice, entry in (("tile128", "matmul_tiled_kernel__t128"), ("auto", auto), ("4wave", None)):
+        monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
+        assert plan_launch(ck, args, grid=grid).entry == entry
+        c = np.full(m * n, np.nan, np.float32)
+        K.matmul_tiled_kernel(A, B, c, m, n, 0, 0, _grid=grid, _tptg=(256, 1, 1), **meta)
+        assert np.isfinite(c).all()
+        assert ops.rel_err(c.reshape(m, n), ref) <= 1e-5 * math.sqrt(k)
+        outs[choice] = c
 
 
 def test_tiled_rows_past_k_are_never_read(gpu_runtime):
