@@ -71,7 +71,7 @@ MATMULS = {
 
 # rocprofv3 counter summaries (profiles/<name>.pmc.json) that give a matmul line its HBM traffic
 MATMUL_PROFILES = {"mma": "mma_f16_4096", "decode": "decode_f16_16x14336x4096", "prefill": "prefill_f16_8192",
-                   "tiled1024": "tiled_f32_1024"}
+                   "tiled1024": "tiled_f32_1024", "tiled2048": "tiled_f32_2048"}
 
 
 def _log(msg: str) -> None:
