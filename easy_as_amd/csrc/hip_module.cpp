@@ -72,12 +72,32 @@ void buffer_destructor(PyObject* cap) {
   delete b;
 }
 
+// Completion events of async launches are reused: an event whose wait succeeded goes back to
+// this pool (touched only with the GIL held), so a launch does not create and destroy one.
+std::vector<void*> g_event_pool;
+constexpr size_t kEventPoolMax = 64;
+
+int acquire_event(void** ev) {
+  if (!g_event_pool.empty()) {
+    *ev = g_event_pool.back();
+    g_event_pool.pop_back();
+    return EAS_HIP_OK;
+  }
+  return eas_hip_event_create(ev);
+}
+
+void recycle_event(void* ev, bool ok) {
+  if (ok && g_event_pool.size() < kEventPoolMax) g_event_pool.push_back(ev);
+  else eas_hip_event_destroy(ev);
+}
+
 void release_pending(Pending* p) {
   if (p->event) {
+    int rc;
     Py_BEGIN_ALLOW_THREADS
-    eas_hip_event_synchronize(p->event);
+    rc = eas_hip_event_synchronize(p->event);
     Py_END_ALLOW_THREADS
-    eas_hip_event_destroy(p->event);
+    recycle_event(p->event, rc == EAS_HIP_OK);
     p->event = nullptr;
   }
   for (PyObject* o : p->keepalive) Py_XDECREF(o);
@@ -559,7 +579,7 @@ PyObject* launch_impl(PyObject* args, PyObject* kwargs, bool async) {
   }
   Py_INCREF(a.kernel);
   pending->keepalive.push_back(a.kernel);
-  rc = eas_hip_event_create(&pending->event);
+  rc = acquire_event(&pending->event);
   if (!rc) rc = eas_hip_event_record(pending->event, stream);
   if (rc) {
     release_pending(pending);
@@ -620,6 +640,8 @@ PyObject* py_synchronize(PyObject*, PyObject* args) {
     Py_BEGIN_ALLOW_THREADS
     rc = eas_hip_event_synchronize(p->event);
     Py_END_ALLOW_THREADS
+    recycle_event(p->event, rc == EAS_HIP_OK);
+    p->event = nullptr;
   }
   release_pending(p);
   if (rc) return raise_status(rc);
