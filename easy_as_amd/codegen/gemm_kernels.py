@@ -1,7 +1,7 @@
 """gfx950 MFMA GEMM emitted for kernels that ``gemm_lift`` proved to be dense GEMMs.
 
-Launches of more than 16 rows tile C into 256 x 256 workgroup tiles (the fp32
-template at the end of this module uses 64 x 64).  The f16 source has two
+Launches of more than 64 rows tile C into 256 x 256 workgroup tiles (or 128 x
+128, below; the fp32 templates at the end of this module use 64 x 64 and 128 x 128).  The f16 source has two
 entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
 
 * ``<name>__pp`` (512 threads): the 8-wave ping-pong DMA body for f16 A and B
@@ -10,7 +10,7 @@ entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
   wave holding 128 x 64 of the tile (4 x 2 ``v_mfma_f32_32x32x16_f16``
   accumulators).
 * ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
-  AGPRs): the skinny path (launches of at most 16 rows), the 4-wave DMA body,
+  AGPRs): the skinny path (launches of at most 64 rows), the 4-wave DMA body,
   and the register body; a uniform branch picks one per launch.
 
 DMA bodies (f16 A and B; K and ldb even and 4-byte aligned bases, so every row
@@ -608,17 +608,19 @@ static __device__ __forceinline__ void eas_gemm_t128(const _Float16* __restrict_
       }
 }
 
-// Skinny path (M <= 16, decode-like): one workgroup per 64 columns, the four waves split K.
+// Skinny path (M <= 64, decode-like): one workgroup per 64 columns, the four waves split K.
 // Each wave streams its K range of B (and A) HBM -> LDS into a private 4-stage ring (no
-// barriers in the loop), multiplies with v_mfma_f32_16x16x32_f16 (B transposed by
-// ds_read_b64_tr_b16), and the waves add their 16 x 64 partial sums through LDS at the end.
-template <typename CT, int K>
+// barriers in the loop), multiplies MT row tiles of 16 (MT = ceil(M / 16), 1, 2 or 4) by four
+// column tiles with v_mfma_f32_16x16x32_f16 (B transposed by ds_read_b64_tr_b16), and the waves
+// add their 16 MT x 64 partial sums through LDS at the end.
+template <typename CT, int K, int MT>
 static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
                                                            CT* __restrict__ C, int ldb, int M, int N, _Float16* smem) {
   typedef float eas_f32x4_acc __attribute__((ext_vector_type(4)));
-  constexpr int NT = 64, KS = 32, NST = 4;
+  constexpr int NT = 64, KS = 32, NST = 4, MR = 16 * MT;
   constexpr int KW = ((K + 4 * KS - 1) / (4 * KS)) * KS;  // k rows per wave
-  constexpr int BST = KS * NT, AST = 16 * KS, STH = BST + AST;  // halves per stage: B [32][64], A [16][32]
+  constexpr int BST = KS * NT, AST = MR * KS, STH = BST + AST;  // halves per stage: B [32][64], A [MR][32]
+  constexpr int LOADS = 4 + MT;                                   // DMA instructions per stage
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * NT;
@@ -639,7 +641,7 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __res
     b_row[q] = r;
     b_off[q] = ((uint32_t)r * (uint32_t)ldb + (uint32_t)(n0 + lc * 8)) * 2u;
   }
-  // A DMA: row lane/4, chunk lane%4 stored at chunk ^ ((row/4)%4)
+  // A DMA t (one per row tile): row 16t + lane/4, chunk lane%4 stored at chunk ^ ((row/4)%4)
   const int a_m = lane >> 2, a_lc = (lane & 3) ^ ((a_m >> 2) & 3);
   const uint32_t a_off = ((uint32_t)a_m * (uint32_t)K + (uint32_t)(a_lc * 8)) * 2u;
   auto dma_step = [&](int t) {
@@ -651,9 +653,12 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __res
       if (k0 + b_row[q] >= ke) off = 0x80000000u;  // another wave's rows, or past K: zeros
       eas_dma16(rb, off, dst + q * 1024);
     }
-    uint32_t off = a_off + (uint32_t)k0 * 2u;
-    if (k0 + a_lc * 8 >= ke) off = 0x80000000u;
-    eas_dma16(ra, off, dst + BST * 2);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      uint32_t off = a_off + ((uint32_t)(16 * mt) * (uint32_t)K + (uint32_t)k0) * 2u;
+      if (k0 + a_lc * 8 >= ke) off = 0x80000000u;
+      eas_dma16(ra, off, dst + BST * 2 + mt * 1024);
+    }
   };
   // 16x16x32 operands: A lane l holds A[l%16][8(l/16)..+7]; B lane l holds B[8(l/16)..+7][l%16]
   const int fm = lane & 15;
@@ -668,65 +673,76 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __res
       const int pc = (col >> 3) ^ (2 * ((row >> 1) & 1) + 4 * ((row >> 3) & 1));
       fb[j][h] = row * NT + pc * 8 + (col & 7);
     }
-  eas_f32x4_acc acc[4];
+  eas_f32x4_acc acc[MT][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = (eas_f32x4_acc){};
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[mt][j] = (eas_f32x4_acc){};
 #pragma unroll
   for (int p = 0; p < NST - 1; ++p)
     if (p < nsteps) dma_step(p);
   for (int t = 0; t < nsteps; ++t) {
-    // this wave's step t landed; up to NST-2 newer steps (5 loads each) stay in flight
+    // this wave's step t landed; up to NST-2 newer steps (LOADS loads each) stay in flight
     const int later = min(NST - 2, nsteps - 1 - t);
-    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(10));
-    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(5));
+    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(2 * LOADS));
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(LOADS));
     else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
     if (t + NST - 1 < nsteps) dma_step(t + NST - 1);  // refills the stage read at step t-1
     const _Float16* st = ws + (t % NST) * STH;
-    const eas_h8 a = *(const eas_h8*)(st + BST + fa);
+    eas_h8 a[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) a[mt] = *(const eas_h8*)(st + BST + mt * 16 * KS + fa);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(st + fb[j][0]));
       const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(st + fb[j][1]));
       const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
       const eas_h8 b = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt], b, acc[mt][j], 0, 0, 0);
     }
   }
   __syncthreads();
   // 16x16 D layout: lane l, register r holds (row 4(l/16) + r, col l%16)
-  float* red = (float*)smem;  // [4 waves][16][64]
+  float* red = (float*)smem;  // [4 waves][MR][64]
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[(wave * 16 + 4 * (lane >> 4) + r) * NT + 16 * j + (lane & 15)] = acc[j][r];
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[(wave * MR + 16 * mt + 4 * (lane >> 4) + r) * NT + 16 * j + (lane & 15)] = acc[mt][j][r];
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int e = 0; e < MR / 4; ++e) {
     const int idx = tid + 256 * e, row = idx >> 6, col = idx & 63;
-    const float sum = (red[row * NT + col] + red[(16 + row) * NT + col]) +
-                      (red[(32 + row) * NT + col] + red[(48 + row) * NT + col]);
+    const float sum = (red[row * NT + col] + red[(MR + row) * NT + col]) +
+                      (red[(2 * MR + row) * NT + col] + red[(3 * MR + row) * NT + col]);
     if (row < M && n0 + col < N) C[(size_t)row * ldb + n0 + col] = (CT)sum;
   }
 }
 
-// Skinny path for inputs the DMA cannot take (f32 or unaligned): one thread per (column, 4 rows).
-template <typename AT, typename BT, typename CT, int K>
+// Skinny path for inputs the DMA cannot take (f32 or unaligned): one thread per (column, 4 MT rows).
+template <typename AT, typename BT, typename CT, int K, int MT>
 static __device__ __forceinline__ void eas_gemm_skinny_simple(const AT* __restrict__ A, const BT* __restrict__ B,
                                                               CT* __restrict__ C, int ldb, int M, int N) {
+  constexpr int R = 4 * MT;  // rows per thread: r0, r0 + 4, ...
   const int tid = threadIdx.x, col = blockIdx.x * 64 + (tid & 63), r0 = tid >> 6;
   if (col >= N) return;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float acc[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) acc[i] = 0.0f;
   for (int k = 0; k < K; ++k) {
     const float b = (float)(_Float16)B[(size_t)k * ldb + col];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < R; ++i) {
       const int row = r0 + 4 * i;
       const float a = row < M ? (float)(_Float16)A[(size_t)row * K + k] : 0.0f;
       acc[i] = __builtin_fmaf(a, b, acc[i]);
     }
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < R; ++i)
     if (r0 + 4 * i < M) C[(size_t)(r0 + 4 * i) * ldb + col] = (CT)acc[i];
 }
 
@@ -904,21 +920,24 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
   const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
   // one LDS array for all bodies: DMA ring 4 x 2 x 16 KB, register body 2 x 2 x 256 x 72 halves,
-  // skinny path 4 waves x 4 stages x 5 KB
+  // skinny path 4 waves x 4 stages x (4 + MT) KB
   __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 2 * 256 * 72];
   // DMA loads take any 4-byte aligned rows (16-byte chunks may straddle alignment and the buffer range,
   // which is checked per dword); the skinny path also wants whole 16-byte chunks per row of A
   const bool dma_ok = F16_IN && (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
                       ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
   const bool skinny_dma_ok = dma_ok && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0);
-  if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns
+  if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns; 1, 2 or 4 row tiles of 16
     if constexpr (F16_IN) {
       if (skinny_dma_ok) {
-        eas_gemm_skinny_dma<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
+        if (M <= 16) eas_gemm_skinny_dma<CT, K, 1>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
+        else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
+        else eas_gemm_skinny_dma<CT, K, 4>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
         return;
       }
     }
-    eas_gemm_skinny_simple<AT, BT, CT, K>(A, B, C, ldb, M, N);
+    if (M <= 16) eas_gemm_skinny_simple<AT, BT, CT, K, 1>(A, B, C, ldb, M, N);
+    else eas_gemm_skinny_simple<AT, BT, CT, K, 4>(A, B, C, ldb, M, N);
     return;
   }
   int m0, n0;
@@ -1248,7 +1267,7 @@ TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
 PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
-SKINNY_M = 16  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
+SKINNY_M = 64  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
 
 

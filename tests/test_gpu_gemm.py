@@ -58,7 +58,9 @@ def test_lifted_mma_matmul_matches_f64(gpu_runtime, mnk, tile):
     _check(c, a, b, m, n, k)
 
 
-@pytest.mark.parametrize("mnk", [(1, 104, 72), (5, 640, 40), (16, 200, 1000), (12, 64, 8), (16, 136, 4096)])
+@pytest.mark.parametrize("mnk", [(1, 104, 72), (5, 640, 40), (16, 200, 1000), (12, 64, 8), (16, 136, 4096),
+                                 # 2 and 4 row tiles of 16 (17-64 rows)
+                                 (17, 300, 72), (32, 640, 1000), (33, 200, 40), (48, 128, 8), (64, 136, 4096)])
 def test_skinny_path_matches_f64(gpu_runtime, mnk):
     m, n, k = mnk
     a, b = _inputs(m, n, k)
@@ -67,7 +69,8 @@ def test_skinny_path_matches_f64(gpu_runtime, mnk):
     _check(c, a, b, m, n, k)
 
 
-@pytest.mark.parametrize("mnk,dtype", [((7, 101, 64), np.float16), ((16, 96, 72), np.float32)])
+@pytest.mark.parametrize("mnk,dtype", [((7, 101, 64), np.float16), ((16, 96, 72), np.float32),
+                                       ((40, 101, 64), np.float16), ((64, 96, 72), np.float32)])
 def test_skinny_fallback_unaligned_or_f32(gpu_runtime, mnk, dtype):
     m, n, k = mnk  # N = 101: rows of B are not 16-byte aligned; f32 inputs are rounded to f16
     a, b = _inputs(m, n, k, dtype)
@@ -76,10 +79,11 @@ def test_skinny_fallback_unaligned_or_f32(gpu_runtime, mnk, dtype):
     _check(c, a.astype(np.float16), b.astype(np.float16), m, n, k)
 
 
-def test_decode_shape_f16_out(gpu_runtime):
+@pytest.mark.parametrize("m", [16, 64])
+def test_decode_shape_f16_out(gpu_runtime, m):
     import torch
 
-    m, n, k = 16, 14336, 4096
+    n, k = 14336, 4096
     rng = np.random.default_rng(3)
     a = rng.standard_normal(m * k, dtype=np.float32).astype(np.float16)
     b = (0.02 * rng.standard_normal(k * n, dtype=np.float32)).astype(np.float16)
@@ -194,11 +198,12 @@ def test_full_size_4096_sampled_rows(gpu_runtime, k):
     assert ops.rel_err(c[rows], ref) <= 1e-5 * math.sqrt(k)
 
 
-@pytest.mark.parametrize("mnk", [(300, 520, 200), (257, 264, 72), (520, 256, 1000), (64, 128, 36), (17, 300, 8),
+@pytest.mark.parametrize("mnk", [(300, 520, 200), (257, 264, 72), (520, 256, 1000), (72, 128, 36), (65, 300, 8),
                                  (130, 260, 4100)])
 def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
     """The 8-wave (ping-pong), 128-tile and 4-wave entries on the same launch: each within
-    tolerance of float64 (edge tiles, K tails of 8 and of 4, one stage, 17 rows)."""
+    tolerance of float64 (edge tiles, K tails of 8 and of 4, one stage, 65 rows: just above the
+    skinny path)."""
     from easy_as_amd.runtime.hip import plan_launch
 
     m, n, k = mnk
