@@ -1,6 +1,6 @@
 """gfx950 MFMA GEMM emitted for kernels that ``gemm_lift`` proved to be dense GEMMs.
 
-Launches of more than 64 rows tile C into 256 x 256 workgroup tiles (or 128 x
+Launches of more than 128 rows tile C into 256 x 256 workgroup tiles (or 128 x
 128, below; the fp32 templates at the end of this module use 64 x 64 and 128 x 128).  The f16 source has two
 entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
 
@@ -10,7 +10,7 @@ entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
   wave holding 128 x 64 of the tile (4 x 2 ``v_mfma_f32_32x32x16_f16``
   accumulators).
 * ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
-  AGPRs): the skinny path (launches of at most 64 rows), the 4-wave DMA body,
+  AGPRs): the skinny path (launches of at most 128 rows), the 4-wave DMA body,
   and the register body; a uniform branch picks one per launch.
 
 DMA bodies (f16 A and B; K and ldb even and 4-byte aligned bases, so every row
@@ -608,16 +608,16 @@ static __device__ __forceinline__ void eas_gemm_t128(const _Float16* __restrict_
       }
 }
 
-// Skinny path (M <= 64, decode-like): one workgroup per 64 columns, the four waves split K.
-// Each wave streams its K range of B (and A) HBM -> LDS into a private 4-stage ring (no
-// barriers in the loop), multiplies MT row tiles of 16 (MT = ceil(M / 16), 1, 2 or 4) by four
+// Skinny path (M <= 128, decode-like): one workgroup per 64 columns, the four waves split K.
+// Each wave streams its K range of B (and A) HBM -> LDS into a private 4-stage ring (3 stages for
+// 8 row tiles; no barriers in the loop), multiplies MT row tiles of 16 (1, 2, 4 or 8) by four
 // column tiles with v_mfma_f32_16x16x32_f16 (B transposed by ds_read_b64_tr_b16), and the waves
 // add their 16 MT x 64 partial sums through LDS at the end.
 template <typename CT, int K, int MT>
 static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
                                                            CT* __restrict__ C, int ldb, int M, int N, _Float16* smem) {
   typedef float eas_f32x4_acc __attribute__((ext_vector_type(4)));
-  constexpr int NT = 64, KS = 32, NST = 4, MR = 16 * MT;
+  constexpr int NT = 64, KS = 32, NST = MT > 4 ? 3 : 4, MR = 16 * MT;  // 8 row tiles: 3 stages fit the LDS
   constexpr int KW = ((K + 4 * KS - 1) / (4 * KS)) * KS;  // k rows per wave
   constexpr int BST = KS * NT, AST = MR * KS, STH = BST + AST;  // halves per stage: B [32][64], A [MR][32]
   constexpr int LOADS = 4 + MT;                                   // DMA instructions per stage
@@ -920,24 +920,26 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
   const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
   // one LDS array for all bodies: DMA ring 4 x 2 x 16 KB, register body 2 x 2 x 256 x 72 halves,
-  // skinny path 4 waves x 4 stages x (4 + MT) KB
+  // skinny path 4 waves x 4 stages x (4 + MT) KB (3 stages x 12 KB for 8 row tiles)
   __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 2 * 256 * 72];
   // DMA loads take any 4-byte aligned rows (16-byte chunks may straddle alignment and the buffer range,
   // which is checked per dword); the skinny path also wants whole 16-byte chunks per row of A
   const bool dma_ok = F16_IN && (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
                       ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
   const bool skinny_dma_ok = dma_ok && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0);
-  if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns; 1, 2 or 4 row tiles of 16
+  if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns; 1, 2, 4 or 8 row tiles of 16
     if constexpr (F16_IN) {
       if (skinny_dma_ok) {
         if (M <= 16) eas_gemm_skinny_dma<CT, K, 1>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
         else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
-        else eas_gemm_skinny_dma<CT, K, 4>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
+        else if (M <= 64) eas_gemm_skinny_dma<CT, K, 4>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
+        else eas_gemm_skinny_dma<CT, K, 8>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
         return;
       }
     }
     if (M <= 16) eas_gemm_skinny_simple<AT, BT, CT, K, 1>(A, B, C, ldb, M, N);
-    else eas_gemm_skinny_simple<AT, BT, CT, K, 4>(A, B, C, ldb, M, N);
+    else if (M <= 64) eas_gemm_skinny_simple<AT, BT, CT, K, 4>(A, B, C, ldb, M, N);
+    else eas_gemm_skinny_simple<AT, BT, CT, K, 8>(A, B, C, ldb, M, N);
     return;
   }
   int m0, n0;
@@ -1267,7 +1269,7 @@ TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
 PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
-SKINNY_M = 64  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
+SKINNY_M = 128  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
 
 

@@ -1014,13 +1014,23 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
         if have is not None and have < n_need:
             raise ValueError(f"buffer {name!r} holds {have} elements; this launch touches {n_need}")
     hidden = (m_lo, m_hi, n_lo, n_hi)
-    if m_hi - m_lo <= p.get("skinny_m", 0):
-        # the kernel's skinny path: one workgroup per skinny_n columns, all rows
-        return LaunchPlan((-(-(n_hi - n_lo) // p["skinny_n"]), 1, 1), (p["threads"], 1, 1), hidden)
     m, n = m_hi - m_lo, n_hi - n_lo
     tiles = -(-m // p["BM"]) * -(-n // p["BN"])
     tiles128 = -(-m // 128) * -(-n // 128)
     choice = _gemm_entry_choice()
+    if m <= p.get("skinny_m", 0):
+        # The 4-wave entry runs its skinny path for every launch of at most skinny_m rows (one
+        # workgroup per skinny_n columns, all rows), so it is only ever launched on that grid.
+        # From 17 rows on, a launch whose skinny grid would take more than one round of CUs goes
+        # to the 128 x 128 entry instead (or to the entry EAS_HIP_GEMM_ENTRY names).
+        groups = -(-n // p["skinny_n"])
+        other = None
+        if m > SKINNY_CUT and p.get("pp_entry") and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
+            if choice == "tile128" or (choice == "auto" and groups > compute_units):
+                other = LaunchPlan((tiles128, 1, 1), (p["threads"], 1, 1), hidden, entry=p["t128_entry"])
+            elif choice == "8wave":
+                other = LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
+        return other or LaunchPlan((groups, 1, 1), (p["threads"], 1, 1), hidden)
     if p.get("f32"):
         # fp32: 128 x 128 tiles (a quarter of the DMA bytes per flop) while they still give every CU one
         if p.get("t128_entry") and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n, elem=4) and (
@@ -1036,6 +1046,7 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
 
 
 _ENTRY_CHOICES = ("auto", "8wave", "tile128", "4wave")
+SKINNY_CUT = 16  # up to this many rows a launch always takes the skinny path
 
 
 def _gemm_entry_choice() -> str:

@@ -200,13 +200,19 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
     assert plan.block == (256, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(3, 2, 1))  # partial grid: 64 x 96 rectangle
     assert plan.hidden == (0, 64, 0, 96) and plan.grid == (2, 1, 1)  # 64 rows: skinny, 64 columns per workgroup
-    # M <= 64 (decode-like): one workgroup per 64 columns, on the 4-wave entry
-    for m in (16, 17, 64):
+    # M <= 128 (decode-like): one workgroup per 64 columns, on the 4-wave entry
+    for m in (16, 17, 64, 128):
         plan = plan_launch(ck, {"M": m, "N": 14336}, grid=(448, K.cdiv(m, 32), 1))
         assert plan.hidden == (0, m, 0, 14336) and plan.grid == (224, 1, 1)
         assert plan.block == (256, 1, 1) and plan.entry is None
-    plan = plan_launch(ck, {"M": 65, "N": 14336}, grid=(448, 3, 1))
-    assert plan.hidden == (0, 65, 0, 14336) and plan.grid == (112, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
+    # 17-128 rows with more column groups than CUs: 128 x 128 tiles instead of two skinny rounds
+    plan = plan_launch(ck, {"M": 128, "N": 28672}, grid=(896, 4, 1))
+    assert plan.grid == (224, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
+    plan = plan_launch(ck, {"M": 16, "N": 28672}, grid=(896, 1, 1))
+    assert plan.grid == (448, 1, 1) and plan.entry is None
+    plan = plan_launch(ck, {"M": 129, "N": 14336}, grid=(448, 5, 1))
+    assert plan.hidden == (0, 129, 0, 14336) and plan.grid == (2 * 112, 1, 1)
+    assert plan.entry == "matmul_mma_kernel__t128"
 
 
 @pytest.mark.parametrize("mn,entry,grid", [((4096, 4096), "__pp", 256), ((3072, 3072), "__pp", 144),
