@@ -1,0 +1,222 @@
+"""Structure of the emitted gfx950 HIP source (CPU only, no GPU).
+
+Each test mirrors one of the reference's codegen tests, stated for the HIP text
+this backend emits instead of the Metal text:
+
+* ``tests/test_f16_codegen.py:24-32``        f16 buffers -> ``const _Float16*`` (read) / ``_Float16*`` (written)
+* ``tests/test_spmd_codegen.py:20-37``       SPMD mode, block size, program ids only (no thread ids)
+* ``tests/test_fma.py:44-121``               ``fma`` emitted, early return for a single-store mask, no per-load branches
+* ``tests/test_dot_f16_codegen.py:38-59``    f16 dot loads widened to float; TN4 vector load under an alignment test
+* ``tests/test_dot_codegen_unique_vars.py``  repeated dot groups do not redeclare their index variables
+* ``tests/test_matmul_tiled.py:126``         the literal tiled lowering reads four B columns with one vector load
+* ``tests/test_mma_codegen.py:34-39``        the MMA kernel lowers to MFMA
+
+The last test compiles every emitted source with hiprtc for gfx950 (no GPU is
+needed for that), which is what proves a redeclaration or any other C++ error
+absent.
+"""
+
+from __future__ import annotations
+
+import re
+
+import numpy as np
+import pytest
+
+import eas
+from eas import mk
+
+import kernels as K
+
+
+@eas.kernel
+def add_f16_kernel(a, b, c, N, BLOCK: eas.constexpr):
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.arange(0, BLOCK)
+    mask = offs < N
+    av = mk.load(a, offs, mask)
+    bv = mk.load(b, offs, mask)
+    mk.store(c, offs, av + bv, mask)
+
+
+@eas.kernel
+def simple_fma_kernel(a, b, c, d, N, BLOCK: eas.constexpr):
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.tid(0, BLOCK)
+    mask = offs < N
+    d_val = mk.load(a, offs, mask) * mk.load(b, offs, mask) + mk.load(c, offs, mask)
+    mk.store(d, offs, d_val, mask)
+
+
+@eas.kernel
+def matmul_with_fma(a, b, c, M, N, BLOCK: eas.constexpr, K: eas.constexpr):
+    row = mk.program_id(0)
+    tile = mk.program_id(1)
+    col = tile * BLOCK + mk.tid(0, BLOCK)
+    out = row * N + col
+    mask = mk.where(row < M, col < N, False)
+    acc = 0.0
+    for k in range(K):
+        acc = acc + mk.load(a, row * K + k, mask) * mk.load(b, k * N + col, mask)
+    mk.store(c, out, acc, mask)
+
+
+@eas.kernel
+def dot_f16_scalar_kernel(a, b, out, K, BLOCK: eas.constexpr):
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.tid(0, BLOCK)
+    v = mk.dot(a, offs * K, 1, b, 0, 1, K)
+    mk.store(out, offs, v, offs < (BLOCK * 2))
+
+
+@eas.kernel
+def dot_f16_tn4_kernel(a, b, out, K, BLOCK: eas.constexpr):
+    pid = mk.program_id(0)
+    _ = mk.tid(0, BLOCK)
+    base = pid * 4
+    d0 = mk.dot(a, 0, 1, b, base, 1, K)
+    d1 = mk.dot(a, 0, 1, b, base + 1, 1, K)
+    d2 = mk.dot(a, 0, 1, b, base + 2, 1, K)
+    d3 = mk.dot(a, 0, 1, b, base + 3, 1, K)
+    mk.store(out, base + 0, d0, True)
+    mk.store(out, base + 1, d1, True)
+    mk.store(out, base + 2, d2, True)
+    mk.store(out, base + 3, d3, True)
+
+
+@eas.kernel
+def many_dot_kernel(out, K: eas.constexpr, BLOCK: eas.constexpr):
+    _ = mk.tid(0, BLOCK)
+    As = mk.alloc_tg(1 * K)
+    Bs = mk.alloc_tg(K * 1)
+    mk.barrier()
+    acc = 0.0
+    for _i in range(20):
+        acc = acc + mk.dot(As, 0, 1, Bs, 0, 1, K)
+    mk.store(out, 0, acc, True)
+
+
+def _h(n: int) -> np.ndarray:
+    return np.zeros(n, np.float16)
+
+
+def _f(n: int) -> np.ndarray:
+    return np.zeros(n, np.float32)
+
+
+def _params(src: str, name: str) -> list[str]:
+    """The parameter declarations of kernel ``name`` in ``src``, one per entry."""
+    m = re.search(rf"\b{re.escape(name)}\(\s*(.*?)\)\s*\{{", src, re.S)
+    assert m, f"kernel {name} not found"
+    return [p.strip() for p in m.group(1).split(",")]
+
+
+def test_f16_buffers_emit_half_pointers():
+    ck = add_f16_kernel.compile(_h(256), _h(256), _h(256), 256, BLOCK=256)
+    params = _params(ck.src, "add_f16_kernel")
+    assert "const _Float16* __restrict__ a" in params
+    assert "const _Float16* __restrict__ b" in params
+    assert "_Float16* __restrict__ c" in params  # written: not const
+
+
+def test_spmd_mode_block_size_and_program_ids_only():
+    block = 128
+    ck = K.add_kernel.compile(_f(1027), _f(1027), _f(1027), 1027, BLOCK=block)
+    assert ck.launch_mode == "spmd" and int(ck.block_size) == block
+    params = _params(ck.src, "add_kernel")
+    # an SPMD launch counts programs, not threads
+    assert "const uint32_t __eas_nprog" in params and not any("__eas_nthreads" in p for p in params)
+    # each program's BLOCK lanes are spread over threads: no per-program serial lane loop
+    assert not re.search(rf"for \(uint32_t \w+ = 0; \w+ < {block}u;", ck.src)
+    assert "__pid < __eas_nprog" in ck.src
+
+
+def test_fma_emitted_with_early_return_for_single_store_mask():
+    z = _f(256)
+    ck = simple_fma_kernel.compile(z, z, z, z.copy(), 256, BLOCK=256)
+    assert "__builtin_fmaf(" in ck.src
+    assert re.search(r"\bif \(!v\d+\) return;", ck.src)
+    assert not re.search(r"\bif \(v\d+\) \{", ck.src)
+
+
+def test_matmul_fma_chain_has_no_per_load_branches():
+    m, n, k = 32, 64, 8
+    ck = matmul_with_fma.compile(_f(m * k), _f(k * n), _f(m * n), m, n, BLOCK=32, K=k)
+    src = ck.src
+    assert src.count("__builtin_fmaf(") == k
+    assert re.search(r"\bif \(!v\d+\) return;", src)
+    assert not re.search(r"\bif \(v\d+\) \{", src)
+    lines = src.split("\n")
+    per_load_branches = sum(
+        1 for i, line in enumerate(lines[:-1])
+        if "= 0.0f;" in line and "if (" in lines[i + 1] and "{" in lines[i + 1] and "[" in lines[i + 1])
+    assert per_load_branches == 0
+    # every load is a plain indexed read after the guard
+    assert len(re.findall(r"= (a|b)\[v\d+\];", src)) == 2 * k
+
+
+def test_dot_f16_scalar_loads_cast_to_float():
+    ck = dot_f16_scalar_kernel.compile(_h(256), _h(256), _f(256), 8, BLOCK=128)
+    params = _params(ck.src, "dot_f16_scalar_kernel")
+    assert "const _Float16* __restrict__ a" in params
+    assert "const _Float16* __restrict__ b" in params
+    assert "float* __restrict__ out" in params
+    assert "(float)a[" in ck.src and "(float)b[" in ck.src
+
+
+def test_dot_f16_tn4_uses_vector_load_when_aligned():
+    ck = dot_f16_tn4_kernel.compile(_h(256), _h(256), _f(256), 8, BLOCK=128)
+    src = ck.src
+    # four adjacent B columns: one 8-byte half4 load when the address allows it,
+    # element loads otherwise (the reference tests the index with ``& 3u``)
+    assert "*(const eas_f16x4*)" in src
+    assert re.search(r"\(\(\(uint64_t\)__bp\) & 7ull\) == 0ull", src)
+    assert src.count("__builtin_fmaf(") == 8  # 4 on the vector path, 4 on the element path
+
+
+def test_dot_groups_do_not_redeclare_index_variables():
+    ck = many_dot_kernel.compile(_f(1), K=16, BLOCK=32)
+    src = ck.src
+    assert "uint a_idx =" not in src
+    # the index pair of every dot lives in its own scope
+    assert src.count("{ uint32_t __ai =") == 20
+    assert len(re.findall(r"^\s*uint32_t __ai\b", src, re.M)) == 0
+
+
+def test_literal_tiled_lowering_reads_b_columns_as_float4(monkeypatch):
+    monkeypatch.setenv("EAS_HIP_DISABLE_GEMM_LIFT", "1")
+    z = _f(64 * 64)
+    ck = eas.kernel(K.matmul_tiled_kernel.fn).compile(z, z, z.copy(), 64, 64, 0, 0, BM=32, BN=32, BK=16, K=64,
+                                                      NT=256)
+    assert ck.launch_mode == "thread"
+    assert "*(const eas_f32x4*)" in ck.src
+    assert "__shared__" in ck.src and "__syncthreads();" in ck.src
+
+
+def test_mma_kernel_lowers_to_mfma():
+    ck = K.matmul_mma_kernel.compile(_h(64 * 64), _h(64 * 64), _f(64 * 64), 64, 64, BM=32, BN=32, BK=8, K=64,
+                                     NT=512)
+    assert "__builtin_amdgcn_mfma_f32_32x32x16_f16" in ck.src
+
+
+def _sources() -> list[tuple[str, str]]:
+    h, f = _h(256), _f(256)
+    cks = [
+        ("add_f16_kernel", add_f16_kernel.compile(h, h, h.copy(), 256, BLOCK=256)),
+        ("simple_fma_kernel", simple_fma_kernel.compile(f, f, f, f.copy(), 256, BLOCK=256)),
+        ("matmul_with_fma", matmul_with_fma.compile(f, f, f.copy(), 32, 64, BLOCK=32, K=8)),
+        ("dot_f16_scalar_kernel", dot_f16_scalar_kernel.compile(h, h, f, 8, BLOCK=128)),
+        ("dot_f16_tn4_kernel", dot_f16_tn4_kernel.compile(h, h, f, 8, BLOCK=128)),
+        ("many_dot_kernel", many_dot_kernel.compile(_f(1), K=16, BLOCK=32)),
+    ]
+    return [(name, ck.src) for name, ck in cks]
+
+
+@pytest.mark.parametrize("name,src", _sources(), ids=lambda v: v if isinstance(v, str) and len(v) < 40 else "src")
+def test_emitted_source_compiles_for_gfx950(name, src):
+    from easy_as_amd.runtime.hip import COMPILE_OPTIONS
+    from easy_as_amd.runtime.hip_ext import load_hip_ext
+
+    mod = load_hip_ext(require=True)
+    code = mod.compile_to_code(src, f"{name}.hip", list(COMPILE_OPTIONS))
+    assert code[:4] == b"\x7fELF"
