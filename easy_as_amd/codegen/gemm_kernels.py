@@ -85,18 +85,37 @@ static __device__ __forceinline__ void eas_dma16(eas_rsrc r, uint32_t voff, uint
 }
 """
 
-_TEMPLATE = r"""
-typedef _Float16 eas_h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 eas_h4 __attribute__((ext_vector_type(4)));
+# The MFMA operand type of the 16-bit templates: f16 or bf16 (the dtype of the kernel's
+# threadgroup tiles).  Both have 16-bit elements, so the DMA, LDS layout and transposed
+# reads are the same; only the element type, the MFMA and the transposing read differ.
+_OP_TYPES = {
+    DType.F16: r"""
+typedef _Float16 eas_op_t;
 typedef __fp16 eas_h4t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+#define EAS_MFMA32 __builtin_amdgcn_mfma_f32_32x32x16_f16
+#define EAS_MFMA16 __builtin_amdgcn_mfma_f32_16x16x32_f16
+#define EAS_DS_TR16 __builtin_amdgcn_ds_read_tr16_b64_v4f16
+""",
+    DType.BF16: r"""
+typedef __bf16 eas_op_t;
+typedef __bf16 eas_h4t __attribute__((ext_vector_type(4)));
+#define EAS_MFMA32 __builtin_amdgcn_mfma_f32_32x32x16_bf16
+#define EAS_MFMA16 __builtin_amdgcn_mfma_f32_16x16x32_bf16
+#define EAS_DS_TR16 __builtin_amdgcn_ds_read_tr16_b64_v4bf16
+""",
+}
+
+_TEMPLATE = r"""
+typedef eas_op_t eas_h8 __attribute__((ext_vector_type(8)));
+typedef eas_op_t eas_h4 __attribute__((ext_vector_type(4)));
 
 template <typename T> static __device__ __forceinline__ eas_h8 eas_load8(const T* p);
-template <> __device__ __forceinline__ eas_h8 eas_load8<_Float16>(const _Float16* p) { return *(const eas_h8*)p; }
+template <> __device__ __forceinline__ eas_h8 eas_load8<eas_op_t>(const eas_op_t* p) { return *(const eas_h8*)p; }
 template <> __device__ __forceinline__ eas_h8 eas_load8<float>(const float* p) {
   const eas_f32x4 lo = *(const eas_f32x4*)p, hi = *(const eas_f32x4*)(p + 4);
   eas_h8 v;
-  v[0] = (_Float16)lo[0]; v[1] = (_Float16)lo[1]; v[2] = (_Float16)lo[2]; v[3] = (_Float16)lo[3];
-  v[4] = (_Float16)hi[0]; v[5] = (_Float16)hi[1]; v[6] = (_Float16)hi[2]; v[7] = (_Float16)hi[3];
+  v[0] = (eas_op_t)lo[0]; v[1] = (eas_op_t)lo[1]; v[2] = (eas_op_t)lo[2]; v[3] = (eas_op_t)lo[3];
+  v[4] = (eas_op_t)hi[0]; v[5] = (eas_op_t)hi[1]; v[6] = (eas_op_t)hi[2]; v[7] = (eas_op_t)hi[3];
   return v;
 }
 
@@ -113,7 +132,7 @@ template <typename T, int AL> static __device__ __forceinline__ eas_h8 eas_load8
   } else if constexpr (AL == 1) {
     eas_h8 v;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = (_Float16)p[e];
+    for (int e = 0; e < 8; ++e) v[e] = (eas_op_t)p[e];
     return v;
   } else {
     constexpr int W = AL > 8 ? 8 : AL;
@@ -123,20 +142,20 @@ template <typename T, int AL> static __device__ __forceinline__ eas_h8 eas_load8
     for (int e = 0; e < 8; e += W) {
       const vec_t x = *(const vec_t*)(p + e);
 #pragma unroll
-      for (int i = 0; i < W; ++i) v[e + i] = (_Float16)x[i];
+      for (int i = 0; i < W; ++i) v[e + i] = (eas_op_t)x[i];
     }
     return v;
   }
 }
 
 template <typename CT, int K>
-static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+static __device__ __forceinline__ void eas_gemm_dma(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                     CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
-                                                    _Float16* smem) {
+                                                    eas_op_t* smem) {
   constexpr int BM = 256, BN = 256, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
   constexpr int STAGE_H = BM * BK;  // halves per operand per stage (16 KB)
-  _Float16* As = smem;
-  _Float16* Bs = smem + NSTAGE * STAGE_H;
+  eas_op_t* As = smem;
+  eas_op_t* Bs = smem + NSTAGE * STAGE_H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -157,7 +176,7 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
     const int c_b = (lane & 31) ^ (4 * (r_b & 3));
     b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
   }
-  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS _Float16*)As, lds_b = (uint32_t)(size_t)(EAS_LDS _Float16*)Bs;
+  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS eas_op_t*)As, lds_b = (uint32_t)(size_t)(EAS_LDS eas_op_t*)Bs;
   auto dma_one = [&](int kt, int d) {  // d in 0..7: 0..3 A, 4..7 B
     const int s = kt % NSTAGE, i = d & 3;
     const uint32_t dst = (uint32_t)((s * STAGE_H + (wave * 4 + i) * 512) * 2);
@@ -179,9 +198,9 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
     if constexpr (K % 8 != 0) {
       constexpr int KR = K % BK, CP = KR / 8, E0 = KR % 8;
       const int r = tid;
-      _Float16* row = As + ((KT - 1) % NSTAGE) * STAGE_H + r * BK + ((CP ^ ((r >> 2) & 3)) * 8);
+      eas_op_t* row = As + ((KT - 1) % NSTAGE) * STAGE_H + r * BK + ((CP ^ ((r >> 2) & 3)) * 8);
 #pragma unroll
-      for (int e = E0; e < 8; ++e) row[e] = (_Float16)0.0f;
+      for (int e = E0; e < 8; ++e) row[e] = (eas_op_t)0.0f;
     }
   };
   // fragment offsets (halves within a stage)
@@ -210,9 +229,9 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
   eas_h8 fa[2][4], fb[2][4];
   auto read_a = [&](int s, int ks, int i) { fa[ks][i] = *(const eas_h8*)(As + s * STAGE_H + fa_off[ks][i]); };
   auto read_b = [&](int s, int ks, int j) {
-    const _Float16* bs = Bs + s * STAGE_H;
-    const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
-    const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
+    const eas_op_t* bs = Bs + s * STAGE_H;
+    const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
+    const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
     const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
     fb[ks][j] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
   };
@@ -223,7 +242,7 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
     for (int j = 0; j < 4; ++j) acc[i][j] = (eas_f32x16){};
   auto mfma_row = [&](int ks, int i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < 4; ++j) acc[i][j] = EAS_MFMA32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
   };
   // this wave's loads of the awaited stage are done; `later` newer stages (8 loads each) may stay in flight
   auto wait_stage = [&](int later) {
@@ -277,13 +296,13 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
     for (int i = 0; i < 4; ++i) {
       if (issue) dma_one(kt + NSTAGE - 1, 2 * i);
       if (next) read_b(sn, 0, i);
-      acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][i], fb[1][0], acc[i][0], 0, 0, 0);
-      acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][i], fb[1][1], acc[i][1], 0, 0, 0);
+      acc[i][0] = EAS_MFMA32(fa[1][i], fb[1][0], acc[i][0], 0, 0, 0);
+      acc[i][1] = EAS_MFMA32(fa[1][i], fb[1][1], acc[i][1], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
       if (issue) dma_one(kt + NSTAGE - 1, 2 * i + 1);
       if (next) read_a(sn, 0, i);
-      acc[i][2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][i], fb[1][2], acc[i][2], 0, 0, 0);
-      acc[i][3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][i], fb[1][3], acc[i][3], 0, 0, 0);
+      acc[i][2] = EAS_MFMA32(fa[1][i], fb[1][2], acc[i][2], 0, 0, 0);
+      acc[i][3] = EAS_MFMA32(fa[1][i], fb[1][3], acc[i][3], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -310,13 +329,13 @@ static __device__ __forceinline__ void eas_gemm_dma(const _Float16* __restrict__
 // the 4-wave DMA body's.  When K is not a multiple of 8, the A fragments of the tail stage are
 // masked to zero past K in registers (the last 16-byte chunk of a row reaches into the next row).
 template <typename CT, int K>
-static __device__ __forceinline__ void eas_gemm_pp(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                    CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
-                                                   _Float16* smem) {
+                                                   eas_op_t* smem) {
   constexpr int BM = 256, BN = 256, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
   constexpr int STAGE_H = BM * BK;
-  _Float16* As = smem;
-  _Float16* Bs = smem + NSTAGE * STAGE_H;
+  eas_op_t* As = smem;
+  eas_op_t* Bs = smem + NSTAGE * STAGE_H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = wave >> 2, p = wave & 3;
@@ -338,7 +357,7 @@ static __device__ __forceinline__ void eas_gemm_pp(const _Float16* __restrict__ 
     b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
     b_k[i] = r_b;
   }
-  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS _Float16*)As, lds_b = (uint32_t)(size_t)(EAS_LDS _Float16*)Bs;
+  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS eas_op_t*)As, lds_b = (uint32_t)(size_t)(EAS_LDS eas_op_t*)Bs;
   auto dma_one = [&](int kt, int d) {  // d: 0, 1 A; 2, 3 B
     const int s = kt % NSTAGE, i = d & 1;
     const uint32_t dst = (uint32_t)((s * STAGE_H + (wave * 2 + i) * 512) * 2);
@@ -377,9 +396,9 @@ static __device__ __forceinline__ void eas_gemm_pp(const _Float16* __restrict__ 
   eas_h8 fa[2][4], fb[2][2];
   auto read_a = [&](int s, int ks, int i) { fa[ks][i] = *(const eas_h8*)(As + s * STAGE_H + fa_off[ks][i]); };
   auto read_b = [&](int s, int ks, int j) {
-    const _Float16* bs = Bs + s * STAGE_H;
-    const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
-    const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
+    const eas_op_t* bs = Bs + s * STAGE_H;
+    const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
+    const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
     const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
     fb[ks][j] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
   };
@@ -430,7 +449,7 @@ static __device__ __forceinline__ void eas_gemm_pp(const _Float16* __restrict__ 
           for (int e = 0; e < 8; ++e) {
             const bool past = kt * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) fa[ks][i][e] = past ? (_Float16)0.0f : fa[ks][i][e];
+            for (int i = 0; i < 4; ++i) fa[ks][i][e] = past ? (eas_op_t)0.0f : fa[ks][i][e];
           }
       }
     }
@@ -444,7 +463,7 @@ static __device__ __forceinline__ void eas_gemm_pp(const _Float16* __restrict__ 
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) acc[i][j] = EAS_MFMA32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
     if (g == 0 && kt + 1 < KT) wait_stage(later);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
@@ -475,7 +494,7 @@ static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict
     if (row >= M || col >= N) continue;
     float acc = 0.0f;
     for (int k = 0; k < K; ++k)
-      acc = __builtin_fmaf((float)(_Float16)A[(size_t)row * K + k], (float)(_Float16)B[(size_t)k * ldb + col], acc);
+      acc = __builtin_fmaf((float)(eas_op_t)A[(size_t)row * K + k], (float)(eas_op_t)B[(size_t)k * ldb + col], acc);
     C[(size_t)row * ldb + col] = (CT)acc;
   }
 }
@@ -486,13 +505,13 @@ static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict
 // Per stage: wait for this wave's DMA, barrier, issue this wave's quarter of the DMA three stages
 // ahead, read the stage's fragments, 8 MFMAs.
 template <typename CT, int K>
-static __device__ __forceinline__ void eas_gemm_t128(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
+static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
-                                                     _Float16* smem) {
+                                                     eas_op_t* smem) {
   constexpr int BM = 128, BN = 128, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
   constexpr int STAGE_H = BM * BK;  // halves per operand per stage (8 KB)
-  _Float16* As = smem;
-  _Float16* Bs = smem + NSTAGE * STAGE_H;
+  eas_op_t* As = smem;
+  eas_op_t* Bs = smem + NSTAGE * STAGE_H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -514,7 +533,7 @@ static __device__ __forceinline__ void eas_gemm_t128(const _Float16* __restrict_
     b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
     b_k[i] = r_b;
   }
-  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS _Float16*)As, lds_b = (uint32_t)(size_t)(EAS_LDS _Float16*)Bs;
+  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS eas_op_t*)As, lds_b = (uint32_t)(size_t)(EAS_LDS eas_op_t*)Bs;
   auto dma_stage = [&](int kt) {
     const int s = kt % NSTAGE;
 #pragma unroll
@@ -565,16 +584,16 @@ static __device__ __forceinline__ void eas_gemm_t128(const _Float16* __restrict_
     wait_stage(KT - 1 - kt < NSTAGE - 2 ? KT - 1 - kt : NSTAGE - 2);
     __syncthreads();
     if (kt + NSTAGE - 1 < KT) dma_stage(kt + NSTAGE - 1);
-    const _Float16* as = As + (kt % NSTAGE) * STAGE_H;
-    const _Float16* bs = Bs + (kt % NSTAGE) * STAGE_H;
+    const eas_op_t* as = As + (kt % NSTAGE) * STAGE_H;
+    const eas_op_t* bs = Bs + (kt % NSTAGE) * STAGE_H;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       eas_h8 fa[2], fb[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         fa[i] = *(const eas_h8*)(as + fa_off[ks][i]);
-        const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][0]));
-        const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][1]));
+        const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][0]));
+        const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][1]));
         const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
         fb[i] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
       }
@@ -584,14 +603,14 @@ static __device__ __forceinline__ void eas_gemm_t128(const _Float16* __restrict_
           for (int e = 0; e < 8; ++e) {
             const bool past = kt * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) fa[i][e] = past ? (_Float16)0.0f : fa[i][e];
+            for (int i = 0; i < 2; ++i) fa[i][e] = past ? (eas_op_t)0.0f : fa[i][e];
           }
         }
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) acc[i][j] = EAS_MFMA32(fa[i], fb[j], acc[i][j], 0, 0, 0);
     }
   }
   const bool full = (m0 + BM <= M) && (n0 + BN <= N);
@@ -614,8 +633,8 @@ static __device__ __forceinline__ void eas_gemm_t128(const _Float16* __restrict_
 // column tiles with v_mfma_f32_16x16x32_f16 (B transposed by ds_read_b64_tr_b16), and the waves
 // add their 16 MT x 64 partial sums through LDS at the end.
 template <typename CT, int K, int MT>
-static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __restrict__ A, const _Float16* __restrict__ B,
-                                                           CT* __restrict__ C, int ldb, int M, int N, _Float16* smem) {
+static __device__ __forceinline__ void eas_gemm_skinny_dma(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
+                                                           CT* __restrict__ C, int ldb, int M, int N, eas_op_t* smem) {
   typedef float eas_f32x4_acc __attribute__((ext_vector_type(4)));
   constexpr int NT = 64, KS = 32, NST = MT > 4 ? 3 : 4, MR = 16 * MT;  // 8 row tiles: 3 stages fit the LDS
   constexpr int KW = ((K + 4 * KS - 1) / (4 * KS)) * KS;  // k rows per wave
@@ -626,8 +645,8 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __res
   const int n0 = blockIdx.x * NT;
   const int kb = wave * KW, ke = min(K, kb + KW);
   const int nsteps = ke > kb ? (ke - kb + KS - 1) / KS : 0;
-  _Float16* ws = smem + wave * NST * STH;
-  const uint32_t lds_ws = (uint32_t)(size_t)(EAS_LDS _Float16*)ws;
+  eas_op_t* ws = smem + wave * NST * STH;
+  const uint32_t lds_ws = (uint32_t)(size_t)(EAS_LDS eas_op_t*)ws;
   const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
   const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
   // B DMA q: rows 8q + lane/8 of the stage, chunk lane%8 stored at chunk ^ s(row),
@@ -688,18 +707,18 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const _Float16* __res
     else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(LOADS));
     else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
     if (t + NST - 1 < nsteps) dma_step(t + NST - 1);  // refills the stage read at step t-1
-    const _Float16* st = ws + (t % NST) * STH;
+    const eas_op_t* st = ws + (t % NST) * STH;
     eas_h8 a[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) a[mt] = *(const eas_h8*)(st + BST + mt * 16 * KS + fa);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const eas_h4t lo = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(st + fb[j][0]));
-      const eas_h4t hi = __builtin_amdgcn_ds_read_tr16_b64_v4f16((EAS_LDS eas_h4t*)(st + fb[j][1]));
+      const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(st + fb[j][0]));
+      const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(st + fb[j][1]));
       const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
       const eas_h8 b = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt], b, acc[mt][j], 0, 0, 0);
+      for (int mt = 0; mt < MT; ++mt) acc[mt][j] = EAS_MFMA16(a[mt], b, acc[mt][j], 0, 0, 0);
     }
   }
   __syncthreads();
@@ -733,11 +752,11 @@ static __device__ __forceinline__ void eas_gemm_skinny_simple(const AT* __restri
 #pragma unroll
   for (int i = 0; i < R; ++i) acc[i] = 0.0f;
   for (int k = 0; k < K; ++k) {
-    const float b = (float)(_Float16)B[(size_t)k * ldb + col];
+    const float b = (float)(eas_op_t)B[(size_t)k * ldb + col];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int row = r0 + 4 * i;
-      const float a = row < M ? (float)(_Float16)A[(size_t)row * K + k] : 0.0f;
+      const float a = row < M ? (float)(eas_op_t)A[(size_t)row * K + k] : 0.0f;
       acc[i] = __builtin_fmaf(a, b, acc[i]);
     }
   }
@@ -749,12 +768,12 @@ static __device__ __forceinline__ void eas_gemm_skinny_simple(const AT* __restri
 template <typename AT, typename BT, typename CT, int K>
 static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, const BT* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
-                                                     _Float16* smem) {
+                                                     eas_op_t* smem) {
   constexpr int BM = 256, BN = 256, BK = 64, WN = 2, NTHREADS = 256, TI = 4, TJ = 4;
   constexpr int PITCH = BK + 8, KC = BK / 8, A_IT = BM * BK / 8 / NTHREADS, NBLK = BK * BN / 64;
   constexpr int B_IT = (NBLK + NTHREADS - 1) / NTHREADS;
-  _Float16* As0 = smem;  // [2][BM * PITCH]
-  _Float16* Bs0 = smem + 2 * BM * PITCH;  // [2][BN * PITCH]
+  eas_op_t* As0 = smem;  // [2][BM * PITCH]
+  eas_op_t* Bs0 = smem + 2 * BM * PITCH;  // [2][BN * PITCH]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   // A rows (length K, compile time) load A_AL elements per vector; B rows need 16-byte vectors
@@ -779,8 +798,8 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
     }
   };
   auto sstore_regs = [&](int buf) {
-    _Float16* As = As0 + buf * BM * PITCH;
-    _Float16* Bs = Bs0 + buf * BN * PITCH;
+    eas_op_t* As = As0 + buf * BM * PITCH;
+    eas_op_t* Bs = Bs0 + buf * BN * PITCH;
 #pragma unroll
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + NTHREADS * i, row = c / KC, kc = c % KC;
@@ -802,15 +821,15 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
   // edge tiles and the K tail: element loads with zero fill, written straight to LDS
   // (rolled loops keep register pressure low; these tiles are few)
   auto sstore_masked = [&](int buf, int k0) {
-    _Float16* As = As0 + buf * BM * PITCH;
-    _Float16* Bs = Bs0 + buf * BN * PITCH;
+    eas_op_t* As = As0 + buf * BM * PITCH;
+    eas_op_t* Bs = Bs0 + buf * BN * PITCH;
 #pragma unroll 1
     for (int i = 0; i < A_IT; ++i) {
       const int c = tid + NTHREADS * i, row = c / KC, kc = c % KC;
       const int gm_ = m0 + row, gk = k0 + kc * 8;
       eas_h8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (gm_ < M && gk + e < K) ? (_Float16)A[(size_t)gm_ * K + gk + e] : (_Float16)0.0f;
+      for (int e = 0; e < 8; ++e) v[e] = (gm_ < M && gk + e < K) ? (eas_op_t)A[(size_t)gm_ * K + gk + e] : (eas_op_t)0.0f;
       *(eas_h8*)(&As[row * PITCH + kc * 8]) = v;
     }
 #pragma unroll 1
@@ -824,7 +843,7 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
           const int gk = k0 + kg * 8 + r;
-          col[r] = (gk < K && gn + j < N) ? (_Float16)B[(size_t)gk * ldb + gn + j] : (_Float16)0.0f;
+          col[r] = (gk < K && gn + j < N) ? (eas_op_t)B[(size_t)gk * ldb + gn + j] : (eas_op_t)0.0f;
         }
         *(eas_h8*)(&Bs[(nc * 8 + j) * PITCH + kg * 8]) = col;
       }
@@ -838,8 +857,8 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
 
   constexpr int KT = (K + BK - 1) / BK, KFULL = K / BK;
   auto compute = [&](int kt) {
-    const _Float16* As = As0 + (kt & 1) * BM * PITCH;
-    const _Float16* Bs = Bs0 + (kt & 1) * BN * PITCH;
+    const eas_op_t* As = As0 + (kt & 1) * BM * PITCH;
+    const eas_op_t* Bs = Bs0 + (kt & 1) * BN * PITCH;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       eas_h8 a[TI], b[TJ];
@@ -851,7 +870,7 @@ static __device__ __forceinline__ void eas_gemm_regs(const AT* __restrict__ A, c
 #pragma unroll
       for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TJ; ++j) acc[i][j] = EAS_MFMA32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
   };
   if (mn_full) {
@@ -909,7 +928,7 @@ static __device__ __forceinline__ void eas_tile_origin(int M, int N, int& m0, in
 extern "C" __global__ __launch_bounds__(256) void @NAME@(
     @PARAMS@) {
   constexpr int K = @K@, SKINNY_M = @SKINNY_M@;
-  constexpr bool F16_IN = @F16_IN@;
+  constexpr bool OP_IN = @OP_IN@;
   typedef @AT@ AT;
   typedef @BT@ BT;
   typedef @CT@ CT;
@@ -921,19 +940,19 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
   // one LDS array for all bodies: DMA ring 4 x 2 x 16 KB, register body 2 x 2 x 256 x 72 halves,
   // skinny path 4 waves x 4 stages x (4 + MT) KB (3 stages x 12 KB for 8 row tiles)
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 2 * 256 * 72];
+  __shared__ __attribute__((aligned(1024))) eas_op_t smem[2 * 2 * 256 * 72];
   // DMA loads take any 4-byte aligned rows (16-byte chunks may straddle alignment and the buffer range,
   // which is checked per dword); the skinny path also wants whole 16-byte chunks per row of A
-  const bool dma_ok = F16_IN && (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
+  const bool dma_ok = OP_IN && (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
                       ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
   const bool skinny_dma_ok = dma_ok && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0);
   if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns; 1, 2, 4 or 8 row tiles of 16
-    if constexpr (F16_IN) {
+    if constexpr (OP_IN) {
       if (skinny_dma_ok) {
-        if (M <= 16) eas_gemm_skinny_dma<CT, K, 1>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
-        else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
-        else if (M <= 64) eas_gemm_skinny_dma<CT, K, 4>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
-        else eas_gemm_skinny_dma<CT, K, 8>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, smem);
+        if (M <= 16) eas_gemm_skinny_dma<CT, K, 1>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, smem);
+        else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, smem);
+        else if (M <= 64) eas_gemm_skinny_dma<CT, K, 4>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, smem);
+        else eas_gemm_skinny_dma<CT, K, 8>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, smem);
         return;
       }
     }
@@ -944,9 +963,9 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   }
   int m0, n0;
   eas_tile_origin(M, N, m0, n0);
-  if constexpr (F16_IN) {
+  if constexpr (OP_IN) {
     if (dma_ok) {
-      eas_gemm_dma<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
+      eas_gemm_dma<CT, K>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
       return;
     }
   }
@@ -970,13 +989,13 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__pp(
   const BT* __restrict__ B = @B@ + __eas_n_lo;
   CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
   const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 4 * 256 * 32];  // DMA ring 4 x 2 x 16 KB
+  __shared__ __attribute__((aligned(1024))) eas_op_t smem[2 * 4 * 256 * 32];  // DMA ring 4 x 2 x 16 KB
   const bool dma_ok = (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
                       ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
   int m0, n0;
   eas_tile_origin(M, N, m0, n0);
   if (dma_ok)
-    eas_gemm_pp<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
+    eas_gemm_pp<CT, K>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
   else
     eas_gemm_elementwise<AT, BT, CT, K>(A, B, C, ldb, M, N, m0, n0);
 }
@@ -993,13 +1012,13 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
   const BT* __restrict__ B = @B@ + __eas_n_lo;
   CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
   const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
-  __shared__ __attribute__((aligned(1024))) _Float16 smem[2 * 4 * 128 * 32];  // DMA ring 4 x 2 x 8 KB
+  __shared__ __attribute__((aligned(1024))) eas_op_t smem[2 * 4 * 128 * 32];  // DMA ring 4 x 2 x 8 KB
   const bool dma_ok = (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
                       ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
   int m0, n0;
   eas_tile_origin<128, 128>(M, N, m0, n0);
   if (dma_ok)
-    eas_gemm_t128<CT, K>((const _Float16*)A, (const _Float16*)B, C, ldb, M, N, m0, n0, smem);
+    eas_gemm_t128<CT, K>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
   else
     eas_gemm_elementwise<AT, BT, CT, K, 128>(A, B, C, ldb, M, N, m0, n0);
 }
@@ -1288,7 +1307,8 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
             params.append(f"const {ctype(arg.dtype)} __eas_a{i}")
     params += ["const uint32_t __eas_m_lo", "const uint32_t __eas_m_hi", "const uint32_t __eas_n_lo",
                "const uint32_t __eas_n_hi"]
-    f16_in = spec.a_dtype == DType.F16 and spec.b_dtype == DType.F16
+    # the DMA bodies copy A and B as they lie in HBM: both must already be the MFMA operand type
+    op_in = spec.a_dtype == spec.op_dtype and spec.b_dtype == spec.op_dtype
     assert SKINNY_N == 64, "the skinny path's tile width is fixed by its LDS layout"
     if spec.f32:
         bm, bn = TILE_F32
@@ -1297,7 +1317,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "@SKINNY_M@": str(SKINNY_M),
         "@PARAMS@": ",\n    ".join(params),
         "@K@": str(spec.K),
-        "@F16_IN@": "true" if f16_in else "false",
+        "@OP_IN@": "true" if op_in else "false",
         "@AT@": ctype(spec.a_dtype),
         "@BT@": ctype(spec.b_dtype),
         "@CT@": ctype(spec.c_dtype),
@@ -1306,8 +1326,8 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "@C@": pname[spec.c],
         "@LDB@": pname[spec.n_sym],
     }
-    src = _DMA_HELPERS + (_TEMPLATE_F32 + _TEMPLATE_F32_T128 if spec.f32 else _TEMPLATE)
-    pingpong = f16_in and not spec.f32 and spec.K % 2 == 0  # odd K: rows of A are not 4-byte aligned
+    src = _DMA_HELPERS + (_TEMPLATE_F32 + _TEMPLATE_F32_T128 if spec.f32 else _OP_TYPES[spec.op_dtype] + _TEMPLATE)
+    pingpong = op_in and not spec.f32 and spec.K % 2 == 0  # odd K: rows of A are not 4-byte aligned
     if pingpong:
         src += _TEMPLATE_PP_ENTRY
     for k, v in subs.items():
@@ -1323,5 +1343,6 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "col_masked": spec.col_masked,
         "pp_entry": f"{ir.name}__pp" if pingpong else None, "pp_threads": PP_THREADS,
         "t128_entry": f"{ir.name}__t128" if (pingpong or spec.f32) else None, "f32": spec.f32,
-        "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value})
+        "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value,
+        "op_dtype": "f32" if spec.f32 else spec.op_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

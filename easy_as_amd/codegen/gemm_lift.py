@@ -112,7 +112,7 @@ class Rec:
     buf: str = ""        # global buffer name (gload)
     off: Poly | None = None
     cond: Cond | None = None
-    to_f16: bool = False
+    rnd: str = ""        # rounded to "f16" or "bf16" after the load ("": as loaded)
     src_rec: np.ndarray | None = None   # lds: record id per thread
     src_thr: np.ndarray | None = None   # lds: writer thread per thread
     frag: Any = None                    # frag: (sg, i, j) arrays per thread
@@ -137,11 +137,12 @@ class GemmSpec:
     a_dtype: DType
     b_dtype: DType
     c_dtype: DType
-    c_f16: bool            # output rounded to f16
-    f32: bool = False      # fp32 products and sums (the `mk.dot` tiled pattern); else f16 MFMA operands
+    c_f16: bool            # output rounded from the f32 accumulator to C's 16-bit type (f16 or bf16)
+    f32: bool = False      # fp32 products and sums (the `mk.dot` tiled pattern); else 16-bit MFMA operands
     row_base: str | None = None   # tile rows start at TM * (program_id + row_base) when set
     col_base: str | None = None
     col_masked: bool = True       # outputs/operands bounded by col < N (else by the launched grid)
+    op_dtype: DType = DType.F16   # MFMA operand type: the dtype of the threadgroup tiles A and B pass through
 
 
 # ---------------------------------------------------------------------------
@@ -158,6 +159,7 @@ class _SymExec:
         self.floats: dict[int, int] = {}   # value id -> record id
         self.recs: list[Rec] = []
         self.frags: dict[int, Frag] = {}
+        self.op_dtype: DType | None = None   # threadgroup tile dtype of the mma operands
         self.tg: dict[int, tuple[np.ndarray, np.ndarray, DType]] = {}
         self.global_bufs: dict[int, str] = {}
         self.scalars: dict[int, str] = {}
@@ -304,11 +306,11 @@ class _SymExec:
             return
         if op == "cast":
             src = a[0]
-            if out.dtype == DType.F16 and src.dtype == DType.F32 and src.id in self.floats:
+            if out.dtype in (DType.F16, DType.BF16) and src.dtype == DType.F32 and src.id in self.floats:
                 r = self.recs[self.floats[src.id]]
                 if r.kind != "gload" and r.kind != "lds":
                     raise Unsupported("cast of a computed float")
-                self.floats[out.id] = self.new_rec(Rec(**{**r.__dict__, "to_f16": True}))
+                self.floats[out.id] = self.new_rec(Rec(**{**r.__dict__, "rnd": out.dtype.value}))
                 return
             raise Unsupported(f"cast {src.dtype}->{out.dtype} in a GEMM kernel")
         if op == "alloc_tg":
@@ -378,8 +380,12 @@ class _SymExec:
             a_buf, a_base, a_st, b_buf, b_base, b_st, acc = a
             if a_buf.id not in self.tg or b_buf.id not in self.tg:
                 raise Unsupported("mma operands must come from threadgroup memory")
-            if self.tg[a_buf.id][2] != DType.F16 or self.tg[b_buf.id][2] != DType.F16:
-                raise Unsupported("only f16 threadgroup tiles are lifted")
+            tile_dts = (self.tg[a_buf.id][2], self.tg[b_buf.id][2])
+            if tile_dts not in ((DType.F16, DType.F16), (DType.BF16, DType.BF16)):
+                raise Unsupported("only f16 or bf16 threadgroup tiles (both alike) are lifted")
+            if self.op_dtype not in (None, tile_dts[0]):
+                raise Unsupported("mma operand type changes between steps")
+            self.op_dtype = tile_dts[0]
             prev = self.frags.get(acc.id)
             if prev is None:
                 raise Unsupported("mma accumulator chain not rooted at mma_zero")
@@ -712,7 +718,7 @@ def analyze(ir: IRModule, block: int) -> GemmSpec:
     # --- copy-out: every tile element stored once to C[row*ldb + col] ---
     seen = np.zeros((S, 8, 8), np.int64)
     frag_rid = recs.index(frag_recs[0])
-    c_f16 = None
+    c_rnd = None
     for name, off, cond, rid in ex.stores:
         r = recs[rid]
         if r.kind != "lds":
@@ -720,9 +726,9 @@ def analyze(ir: IRModule, block: int) -> GemmSpec:
         sel = cond.base & (r.src_rec >= 0)
         if np.any((r.src_rec != frag_rid) & sel):
             raise Unsupported("output element not from the accumulator")
-        if c_f16 is None:
-            c_f16 = r.to_f16
-        if r.to_f16 != c_f16:
+        if c_rnd is None:
+            c_rnd = r.rnd
+        if r.rnd != c_rnd:
             raise Unsupported("mixed output conversions")
         t = np.nonzero(sel)[0]
         code = r.src_thr[t]
@@ -763,11 +769,12 @@ def analyze(ir: IRModule, block: int) -> GemmSpec:
     if m_sym not in args or ldb_sym not in args:
         raise Unsupported("bounds are not kernel arguments")
     a_dt, b_dt, c_dt = args[a_buf].dtype, args[b_buf].dtype, args[c_name].dtype
-    if c_dt == DType.F16 and not c_f16:
-        raise Unsupported("f16 output without an explicit conversion")
+    if c_rnd != ("" if c_dt == DType.F32 else c_dt.value):
+        raise Unsupported(f"{c_dt.value} output without an explicit conversion")
+    assert ex.op_dtype is not None
     return GemmSpec(a=a_buf, b=b_buf, c=c_name, m_sym=m_sym, n_sym=ldb_sym, K=int(K), TM=TM, TN=TN,
-                    row_axis=int(r_axis[2:]), a_dtype=a_dt, b_dtype=b_dt, c_dtype=c_dt, c_f16=bool(c_f16),
-                    row_base=r_base, col_base=c_base)
+                    row_axis=int(r_axis[2:]), a_dtype=a_dt, b_dtype=b_dt, c_dtype=c_dt, c_f16=bool(c_rnd),
+                    row_base=r_base, col_base=c_base, op_dtype=ex.op_dtype)
 
 
 def analyze_dot(ir: IRModule, block: int) -> GemmSpec:

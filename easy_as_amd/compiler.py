@@ -75,7 +75,9 @@ def _torch_buffer_dtype(v: Any) -> DType:
         return DType.F32
     if v.dtype == torch.float16:
         return DType.F16
-    raise TypeError(f"unsupported torch dtype: {v.dtype} (expected float32 or float16)")
+    if v.dtype == torch.bfloat16:
+        return DType.BF16
+    raise TypeError(f"unsupported torch dtype: {v.dtype} (expected float32, float16 or bfloat16)")
 
 
 def _scalar_dtype(v: Any) -> DType:
@@ -246,8 +248,8 @@ class _IRBuilder:
             raise TypeError("alloc_tg(size) requires a Python int (compile-time constant)")
         if size <= 0:
             raise ValueError("alloc_tg(size) must be > 0")
-        if dtype not in (DType.F16, DType.F32):
-            raise TypeError(f"alloc_tg(dtype=...) must be f16/f32, got {dtype}")
+        if dtype not in (DType.F16, DType.BF16, DType.F32):
+            raise TypeError(f"alloc_tg(dtype=...) must be f16/bf16/f32, got {dtype}")
         v = self.emit("alloc_tg", dtype, (size,))
         self.buffer_ids.add(v.ref.id)
         return v
@@ -311,8 +313,10 @@ class _IRBuilder:
         a = self._buffer(a_buffer, f"{op} a_buffer")
         b = self._buffer(b_buffer, f"{op} b_buffer")
         for buf, what in ((a, "a_buffer"), (b, "b_buffer")):
-            if buf.dtype not in (DType.F16, DType.F32):
-                raise TypeError(f"{op} {what} must be f16/f32")
+            if buf.dtype not in (DType.F16, DType.BF16, DType.F32):
+                raise TypeError(f"{op} {what} must be f16/bf16/f32")
+        if op == "mma" and DType.BF16 in (a.dtype, b.dtype) and a.dtype != b.dtype:
+            raise TypeError(f"mma a/b buffers must both be bf16 or neither, got {a.dtype} and {b.dtype}")
         idx = [self._index(v, f"{op} {n}") for v, n in ((a_base, "a_base"), (a_stride, "a_stride"),
                                                         (b_base, "b_base"), (b_stride, "b_stride"))]
         return (a.ref, idx[0].ref, idx[1].ref, b.ref, idx[2].ref, idx[3].ref)

@@ -3,8 +3,9 @@
 The IR is the contract between the tracer (``compiler.py``) and the gfx950
 emitter (``codegen/hip.py``).  Its types, op set and typing rules are the
 reference's (``eas/ir.py:10-83`` for the data model, ``eas/ir.py:86-518`` for
-the rules ``validate_ir`` enforces), so kernels trace to the same IR.  The
-verifier here is table driven: every op maps to one checker function.
+the rules ``validate_ir`` enforces), so kernels trace to the same IR.  One
+addition: the ``bf16`` dtype (buffers, threadgroup arrays, casts, MMA operands).
+The verifier here is table driven: every op maps to one checker function.
 """
 
 from __future__ import annotations
@@ -17,6 +18,10 @@ from typing import Any, Callable, Iterable, Literal, TypeAlias
 class DType(str, Enum):
     BOOL = "bool"
     F16 = "f16"
+    # bfloat16: an addition to the reference's dtypes (buffers from torch.bfloat16
+    # tensors, threadgroup tiles, casts and MMA operands); values convert to f32
+    # for arithmetic and round back to nearest-even.
+    BF16 = "bf16"
     F32 = "f32"
     U32 = "u32"
     # Opaque 8x8 f32 matrix fragment owned by one 32-lane simdgroup.
@@ -93,9 +98,9 @@ class IRModule:
         return (arg for arg in self.args if arg.kind == "scalar")
 
 
-NUMERIC = (DType.U32, DType.F16, DType.F32)
-FLOATS = (DType.F16, DType.F32)
-CASTABLE = (DType.BOOL, DType.U32, DType.F16, DType.F32)
+NUMERIC = (DType.U32, DType.F16, DType.BF16, DType.F32)
+FLOATS = (DType.F16, DType.BF16, DType.F32)
+CASTABLE = (DType.BOOL, DType.U32, DType.F16, DType.BF16, DType.F32)
 
 
 def broadcast(a: int, b: int) -> int | None:
@@ -204,7 +209,7 @@ class _Verifier:
         self.nargs(inst, 1)
         size = inst.args[0]
         self.check(isinstance(size, int) and size > 0, "alloc_tg(size) requires a positive Python int size")
-        self.check(out.dtype in FLOATS, f"alloc_tg output must be f16/f32, got {out.dtype}")
+        self.check(out.dtype in FLOATS, f"alloc_tg output must be f16/bf16/f32, got {out.dtype}")
         self.define(out)
         self.buffers.add(out.id)
 
@@ -241,7 +246,7 @@ class _Verifier:
         a = self.use(inst.args[0], f"{inst.op} lhs")
         b = self.use(inst.args[1], f"{inst.op} rhs")
         self.check(a.dtype == b.dtype, f"{inst.op} dtype mismatch: {a.dtype} vs {b.dtype}")
-        self.check(a.dtype in NUMERIC, f"{inst.op} operands must be u32/f16/f32, got {a.dtype}")
+        self.check(a.dtype in NUMERIC, f"{inst.op} operands must be u32/f16/bf16/f32, got {a.dtype}")
         self.check(out.dtype == a.dtype, f"{inst.op} output dtype must match operands")
         self.check(out.lanes == self.lanes2(a, b, f"{inst.op} operands"), f"{inst.op} output lanes must broadcast operands")
         if inst.op in ("floordiv", "mod"):
@@ -254,7 +259,7 @@ class _Verifier:
         a = self.use(inst.args[0], "lt lhs")
         b = self.use(inst.args[1], "lt rhs")
         self.check(a.dtype == b.dtype, f"lt dtype mismatch: {a.dtype} vs {b.dtype}")
-        self.check(a.dtype in NUMERIC, f"lt operands must be u32/f16/f32, got {a.dtype}")
+        self.check(a.dtype in NUMERIC, f"lt operands must be u32/f16/bf16/f32, got {a.dtype}")
         self.check(out.dtype == DType.BOOL, "lt output must be bool")
         self.check(out.lanes == self.lanes2(a, b, "lt operands"), "lt output lanes mismatch")
         self.define(out)
@@ -301,7 +306,7 @@ class _Verifier:
         self.check(isinstance(dst, DType), "cast target must be a DType")
         self.check(out.dtype == dst, "cast output dtype must match target dtype")
         self.check(out.lanes == x.lanes, "cast output lanes must match input")
-        self.check(x.dtype in CASTABLE and dst in CASTABLE, "cast only supports bool/u32/f16/f32")
+        self.check(x.dtype in CASTABLE and dst in CASTABLE, "cast only supports bool/u32/f16/bf16/f32")
         self.define(out)
 
     def op_fma(self, inst: Inst) -> None:
@@ -311,7 +316,7 @@ class _Verifier:
         y = self.use(inst.args[1], "fma y")
         z = self.use(inst.args[2], "fma z")
         self.check(x.dtype == y.dtype == z.dtype, "fma operands must have same dtype")
-        self.check(x.dtype in FLOATS, f"fma operands must be f16/f32, got {x.dtype}")
+        self.check(x.dtype in FLOATS, f"fma operands must be f16/bf16/f32, got {x.dtype}")
         self.check(out.dtype == x.dtype, "fma output dtype must match operands")
         n = self.lanes2(x, y, "fma x/y")
         n2 = broadcast(z.lanes, n)
@@ -326,7 +331,7 @@ class _Verifier:
         buf = self.buffer(inst.args[0], "load buffer")
         off = self.use(inst.args[1], "load offset")
         mask = self.use(inst.args[2], "load mask")
-        self.check(buf.dtype in FLOATS, f"load buffer dtype must be f16/f32, got {buf.dtype}")
+        self.check(buf.dtype in FLOATS, f"load buffer dtype must be f16/bf16/f32, got {buf.dtype}")
         self.check(off.dtype == DType.U32, "load offset must be u32")
         self.check(mask.dtype == DType.BOOL, "load mask must be bool")
         self.check(out.dtype == buf.dtype, "load output dtype must match buffer dtype")
@@ -341,7 +346,7 @@ class _Verifier:
         off = self.use(inst.args[1], "store offset")
         val = self.use(inst.args[2], "store value")
         mask = self.use(inst.args[3], "store mask")
-        self.check(buf.dtype in FLOATS, f"store buffer dtype must be f16/f32, got {buf.dtype}")
+        self.check(buf.dtype in FLOATS, f"store buffer dtype must be f16/bf16/f32, got {buf.dtype}")
         self.check(off.dtype == DType.U32, "store offset must be u32")
         self.check(mask.dtype == DType.BOOL, "store mask must be bool")
         self.check(val.dtype == buf.dtype, "store value dtype must match buffer dtype")
@@ -354,7 +359,7 @@ class _Verifier:
         a_buf, a_base, a_stride, b_buf, b_base, b_stride, k = inst.args
         for ref, what in ((a_buf, "dot a_buffer"), (b_buf, "dot b_buffer")):
             r = self.buffer(ref, what)
-            self.check(r.dtype in FLOATS, f"{what} must be f16/f32")
+            self.check(r.dtype in FLOATS, f"{what} must be f16/bf16/f32")
         for ref, what in ((a_base, "dot a_base"), (a_stride, "dot a_stride"), (b_base, "dot b_base"),
                           (b_stride, "dot b_stride"), (k, "dot K")):
             self.scalar_u32(ref, what)
@@ -373,9 +378,13 @@ class _Verifier:
         out = self.out(inst)
         self.nargs(inst, 7)
         a_buf, a_base, a_stride, b_buf, b_base, b_stride, acc = inst.args
+        bufs = []
         for ref, what in ((a_buf, "mma a_buffer"), (b_buf, "mma b_buffer")):
             r = self.buffer(ref, what)
-            self.check(r.dtype in FLOATS, f"{what} must be f16/f32")
+            self.check(r.dtype in FLOATS, f"{what} must be f16/bf16/f32")
+            bufs.append(r.dtype)
+        # bf16 fragments multiply bf16 fragments only: the MFMA takes one operand type
+        self.check((DType.BF16 in bufs) <= (bufs[0] == bufs[1]), "mma a/b buffers must both be bf16 or neither")
         for ref, what in ((a_base, "mma a_base"), (a_stride, "mma a_stride"), (b_base, "mma b_base"),
                           (b_stride, "mma b_stride")):
             self.scalar_u32(ref, what)

@@ -123,6 +123,11 @@ def alloc_tg_f16(size: int) -> val:
     return _b().alloc_tg(size, dtype=DType.F16)
 
 
+def alloc_tg_bf16(size: int) -> val:
+    """Threadgroup (LDS) array of ``size`` bf16 (an addition to the reference's DSL)."""
+    return _b().alloc_tg(size, dtype=DType.BF16)
+
+
 def barrier() -> None:
     """Threadgroup barrier with threadgroup-memory ordering."""
     _b().barrier()
@@ -157,6 +162,11 @@ def to_f32(x: Any) -> val:
 
 def to_f16(x: Any) -> val:
     return _b().cast(x, DType.F16)
+
+
+def to_bf16(x: Any) -> val:
+    """Round to bfloat16 (nearest-even; an addition to the reference's DSL)."""
+    return _b().cast(x, DType.BF16)
 
 
 def to_u32(x: Any) -> val:

@@ -212,6 +212,7 @@ class HipRuntime:
                 import torch  # type: ignore
 
                 self._torch = torch
+                self._torch_dtypes = {DType.F32: torch.float32, DType.F16: torch.float16, DType.BF16: torch.bfloat16}
             except Exception:
                 self._torch = None
         return self._torch
@@ -248,7 +249,10 @@ class HipRuntime:
         argv: list[Any] = []
         writable: list[bool] = []
         copy_back: list[tuple[Any, np.ndarray]] = []
-        staged: dict[int, Any] = {}
+        # host arrays staged into device buffers, by id: the same array passed twice is staged
+        # once.  The arrays are held here because an id is only unique while its object lives
+        # (the NumPy views made of torch host tensors below are temporaries).
+        staged: dict[int, tuple[Any, np.ndarray]] = {}
         cuda_device = None
         for arg in ir.args:
             v = runtime_args[arg.name]
@@ -259,8 +263,8 @@ class HipRuntime:
             want = np.float16 if arg.dtype == DType.F16 else np.float32
             w = arg.name in writes
             if torch is not None and isinstance(v, torch.Tensor):
-                if v.dtype != (torch.float16 if arg.dtype == DType.F16 else torch.float32):
-                    raise TypeError(f"{arg.name!r} must be {np.dtype(want).name}, got {v.dtype}")
+                if v.dtype != self._torch_dtypes[arg.dtype]:
+                    raise TypeError(f"{arg.name!r} must be {arg.dtype.value}, got {v.dtype}")
                 dev = v.device
                 if dev.type == "cuda":
                     if not v.is_contiguous():
@@ -272,7 +276,12 @@ class HipRuntime:
                     continue
                 if dev.type != "cpu":
                     raise TypeError(f"unsupported torch device for {arg.name!r}: {dev}")
-                v = v.detach().contiguous().numpy()
+                if arg.dtype == DType.BF16:
+                    # NumPy has no bfloat16: stage the raw 16-bit patterns (same memory)
+                    v = v.detach().contiguous().view(torch.int16).numpy()
+                    want = np.int16
+                else:
+                    v = v.detach().contiguous().numpy()
             if _is_eas_tensor(v):
                 if v.device == "hip":
                     if np.dtype(v.dtype) != np.dtype(want):
@@ -286,14 +295,17 @@ class HipRuntime:
                     raise TypeError(f"{arg.name!r} must be {np.dtype(want).name}, got {v.dtype}")
                 if not v.flags.c_contiguous:
                     raise ValueError(f"{arg.name!r} must be C-contiguous")
-                buf = staged.get(id(v))
-                if buf is None:
+                hit = staged.get(id(v))
+                if hit is None:
                     buf = mod.alloc_buffer(max(int(v.nbytes), 1), "private")
                     if v.nbytes:
                         mod.copy_from_host(buf, v)
-                    staged[id(v)] = buf
-                    if w and v.nbytes:
-                        copy_back.append((buf, v))
+                    staged[id(v)] = (buf, v)
+                else:
+                    buf = hit[0]
+                # an array passed twice is copied back once if either use writes it
+                if w and v.nbytes and not any(b is buf for b, _ in copy_back):
+                    copy_back.append((buf, v))
                 argv.append(buf)
                 writable.append(w)
                 continue

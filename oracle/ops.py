@@ -15,6 +15,13 @@ the ``cpu_baseline`` leg of ``bench.py`` as the checker; the product
                      rounding to odd", IEEE TC 2008).  Used only to pin
                      ``fmaf``; the two must agree bit for bit.
 * ``matmul_ref``   — float64 matmul reference (tests/test_matmul.py:55).
+* ``f32_to_bf16``  — binary32 -> bfloat16, round to nearest even, as 16-bit
+                     patterns; ``bf16_to_f32`` widens them back (exact).
+* ``add_bf16``     — bf16 + bf16: the binary32 sum rounded once to bfloat16.
+                     bfloat16 is not among the reference's dtypes (it is this
+                     backend's addition), so there is no reference call site:
+                     both are pinned against exact rational rounding and
+                     against torch's bfloat16 conversion in tests/test_oracle.py.
 """
 
 from __future__ import annotations
@@ -115,3 +122,32 @@ def rel_err(c: np.ndarray, ref: np.ndarray) -> float:
     ref = np.asarray(ref, np.float64)
     denom = float(np.max(np.abs(ref))) or 1.0
     return float(np.max(np.abs(np.asarray(c, np.float64) - ref))) / denom
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    """bfloat16 bit patterns (uint16) of binary32 ``x``, rounded to nearest even.
+
+    bfloat16 keeps binary32's sign and 8-bit exponent and the top 7 stored
+    significand bits, so rounding is on the low 16 bits: add half an ulp minus
+    one plus the kept last bit, then drop them (a carry may ripple into the
+    exponent, which is right: it rounds up to the next binade or to infinity).
+    A NaN stays a NaN: its top half with the quiet bit set."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    keep = (u >> 16) & 1
+    r = ((u + 0x7FFF + keep) >> 16) & 0xFFFF
+    nan = np.isnan(np.asarray(x, np.float32))
+    r = np.where(nan, ((u >> 16) | 0x40) & 0xFFFF, r)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(h: np.ndarray) -> np.ndarray:
+    """binary32 values of bfloat16 bit patterns (exact)."""
+    return (np.asarray(h, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def add_bf16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """bf16 + bf16 on bit patterns: the binary32 sum (RNE) rounded to bfloat16 (RNE).
+    binary32's 24 bits are at least twice bfloat16's 8 plus 2, so this double
+    rounding equals rounding the exact sum once (Figueroa, "When is double
+    rounding innocuous?", SIGNUM 1995)."""
+    return f32_to_bf16(add_f32(bf16_to_f32(a), bf16_to_f32(b)))

@@ -595,3 +595,85 @@ def matmul_mma_variant_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexp
         mk.store(c, off, mk.load(Cs, r * ldc + cc, True), mask)
     if V == 8:
         mk.store(c, base_m * N + base_n, mk.load(Cs, 0, True), mk.where(base_m < M, base_n < N, False))
+
+
+@eas.kernel
+def matmul_mma_bf16_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexpr, BK: eas.constexpr,
+                           K: eas.constexpr, NT: eas.constexpr, OUT16: eas.constexpr = False):
+    """matmul_mma_kernel with bf16 threadgroup tiles (``mk.alloc_tg_bf16``; inputs
+    rounded with ``mk.to_bf16``, a no-op for bf16 inputs); with OUT16 the copy-out
+    rounds the f32 accumulator into a bf16 ``c``.  bf16 is an addition to the
+    reference's dtypes."""
+    if BM % 8 != 0 or BN % 8 != 0 or BK % 8 != 0:
+        raise ValueError("BM/BN/BK must be divisible by 8 for 8x8 MMA")
+    if NT != (BM // 8) * (BN // 8) * 32:
+        raise ValueError("NT must be (BM/8)*(BN/8)*32 for 8x8 MMA")
+    pid_n = mk.program_id(0)
+    pid_m = mk.program_id(1)
+    tid = mk.tid(0, NT)
+    sg = mk.sg_id()
+    base_m = pid_m * BM
+    base_n = pid_n * BN
+    sgn = BN // 8
+    sg_m = sg // sgn
+    sg_n = sg % sgn
+    lda = BK + 1
+    ldb = BN + 1
+    ldc = BN + 1
+    As = mk.alloc_tg_bf16(BM * lda)
+    Bs = mk.alloc_tg_bf16(BK * ldb)
+    Cs = mk.alloc_tg(BM * ldc)
+    acc = mk.mma_zero()
+    for k0 in range(0, K, BK):
+        for i in range(0, BM * BK, NT):
+            a_idx = tid + i
+            a_r = a_idx // BK
+            a_c = a_idx % BK
+            a_row = base_m + a_r
+            a_col = k0 + a_c
+            in_tile = a_idx < BM * BK
+            a_mask = mk.where(in_tile, mk.where(a_row < M, a_col < K, False), False)
+            mk.store(As, a_r * lda + a_c, mk.to_bf16(mk.load(a, a_row * K + a_col, a_mask)), in_tile)
+        for i in range(0, BK * BN, NT):
+            b_idx = tid + i
+            b_r = b_idx // BN
+            b_c = b_idx % BN
+            b_row = k0 + b_r
+            b_col = base_n + b_c
+            in_tile = b_idx < BK * BN
+            b_mask = mk.where(in_tile, mk.where(b_row < K, b_col < N, False), False)
+            mk.store(Bs, b_r * ldb + b_c, mk.to_bf16(mk.load(b, b_row * N + b_col, b_mask)), in_tile)
+        mk.barrier()
+        for kk in range(0, BK, 8):
+            acc = mk.mma(As, (sg_m * 8) * lda + kk, lda, Bs, kk * ldb + (sg_n * 8), ldb, acc)
+        mk.barrier()
+    mk.mma_store(Cs, (sg_m * 8) * ldc + (sg_n * 8), ldc, acc)
+    mk.barrier()
+    for i in range(0, BM * BN, NT):
+        c_idx = tid + i
+        r = c_idx // BN
+        cc = c_idx % BN
+        row = base_m + r
+        col = base_n + cc
+        v = mk.load(Cs, r * ldc + cc, True)
+        mk.store(c, row * N + col, mk.to_bf16(v) if OUT16 else v, mk.where(row < M, col < N, False))
+
+
+@eas.kernel
+def add_bf16_kernel(a, b, c, N, BLOCK: eas.constexpr):
+    """SPMD add on bf16 buffers (each sum computed in f32 and rounded once to bf16)."""
+    offs = mk.program_id(0) * BLOCK + mk.arange(0, BLOCK)
+    mask = offs < N
+    mk.store(c, offs, mk.load(a, offs, mask) + mk.load(b, offs, mask), mask)
+
+
+@eas.kernel
+def bf16_convert_kernel(x, y, z, N, BLOCK: eas.constexpr):
+    """y = bf16(x) (round to nearest even), z = f32(bf16(x)) * x (a product of a bf16
+    value and an f32 value, rounded to f32)."""
+    offs = mk.program_id(0) * BLOCK + mk.tid(0, BLOCK)
+    mask = offs < N
+    v = mk.load(x, offs, mask)
+    h = mk.to_bf16(v)
+    mk.store(y, offs, h, mask)
+    mk.store(z, offs, mk.to_f32(h) * v, mask)

@@ -220,3 +220,53 @@ def test_emitted_source_compiles_for_gfx950(name, src):
     mod = load_hip_ext(require=True)
     code = mod.compile_to_code(src, f"{name}.hip", list(COMPILE_OPTIONS))
     assert code[:4] == b"\x7fELF"
+
+
+# ---- bfloat16 (an addition to the reference's dtypes) ---------------------------
+
+def test_bf16_buffers_lower_to_bf16_pointers_and_f32_arithmetic():
+    torch = pytest.importorskip("torch")
+    z = torch.zeros(256, dtype=torch.bfloat16)
+    ck = K.add_bf16_kernel.compile(z, z, z.clone(), 256, BLOCK=256)
+    params = _params(ck.src, "add_bf16_kernel")
+    assert "const __bf16* __restrict__ a" in params and "__bf16* __restrict__ c" in params
+    # each sum is formed in f32 and rounded once; loads and stores stay 16-byte vectors
+    assert re.search(r"\(\(__bf16\)\(\(float\)v\d+\[0\] \+ \(float\)v\d+\[0\]\)\)", ck.src)
+    assert "eas_bf16x8" in ck.src
+    ck = K.bf16_convert_kernel.compile(np.zeros(64, np.float32), torch.zeros(64, dtype=torch.bfloat16),
+                                       np.zeros(64, np.float32), 64, BLOCK=64)
+    assert "((__bf16)(v" in ck.src and "((float)(v" in ck.src
+
+
+def test_bf16_mma_lifts_to_bf16_mfma():
+    torch = pytest.importorskip("torch")
+    z = torch.zeros(64 * 64, dtype=torch.bfloat16)
+    ck = K.matmul_mma_bf16_kernel.compile(z, z, np.zeros(64 * 64, np.float32), 64, 64, BM=32, BN=32, BK=8, K=64,
+                                          NT=512)
+    assert ck.geometry.kind == "gemm" and ck.geometry.params["op_dtype"] == "bf16"
+    assert ck.geometry.params["pp_entry"] == "matmul_mma_bf16_kernel__pp"
+    assert "__builtin_amdgcn_mfma_f32_32x32x16_bf16" in ck.src and "mfma_f32_32x32x16_f16" not in ck.src
+    # f32 inputs rounded to bf16 tiles: the lift keeps bf16 operands, the DMA entries drop out
+    f = np.zeros(64 * 64, np.float32)
+    ck = K.matmul_mma_bf16_kernel.compile(f, f, f, 64, 64, BM=32, BN=32, BK=8, K=64, NT=512)
+    assert ck.geometry.params["op_dtype"] == "bf16" and ck.geometry.params["pp_entry"] is None
+
+
+def _bf16_sources() -> list[tuple[str, str]]:
+    torch = pytest.importorskip("torch")
+    z, f = torch.zeros(64 * 64, dtype=torch.bfloat16), np.zeros(64 * 64, np.float32)
+    return [
+        ("add_bf16_kernel", K.add_bf16_kernel.compile(z, z, z.clone(), 256, BLOCK=256).src),
+        ("bf16_convert_kernel", K.bf16_convert_kernel.compile(f, z, f.copy(), 64, BLOCK=64).src),
+        ("matmul_mma_bf16_kernel", K.matmul_mma_bf16_kernel.compile(z, z, z.clone(), 64, 64, BM=32, BN=32, BK=8,
+                                                                    K=64, NT=512, OUT16=True).src),
+    ]
+
+
+def test_bf16_sources_compile_for_gfx950():
+    from easy_as_amd.runtime.hip import COMPILE_OPTIONS
+    from easy_as_amd.runtime.hip_ext import load_hip_ext
+
+    mod = load_hip_ext(require=True)
+    for name, src in _bf16_sources():
+        assert mod.compile_to_code(src, f"{name}.hip", list(COMPILE_OPTIONS))[:4] == b"\x7fELF", name

@@ -348,6 +348,47 @@ def test_numpy_add_argv_contract(monkeypatch, tmp_path):
     assert ext.d2h == [(("buf", 3), 4 * n)]
 
 
+class _FillingExt(_RecordingExt):
+    """Copies back a fixed byte pattern, so a test sees which host memory a result reaches."""
+
+    def copy_to_host(self, buf, arr):
+        super().copy_to_host(buf, arr)
+        np.asarray(arr).view(np.uint8)[:] = 0x3F
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float16", "bfloat16"])
+def test_torch_host_tensors_are_staged_and_copied_back(monkeypatch, tmp_path, dtype):
+    torch = pytest.importorskip("torch")
+    monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
+    ext = _FillingExt()
+    rt = HipRuntime(ext=ext)
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    n = 1031
+    dt = getattr(torch, dtype)
+    a, b, c = torch.ones(n, dtype=dt), torch.ones(n, dtype=dt), torch.zeros(n, dtype=dt)
+    kern = K.add_bf16_kernel if dtype == "bfloat16" else K.add_kernel
+    kern(a, b, c, n, BLOCK=256)
+    _, argv, writable, _, _ = ext.launches[0]
+    # three distinct staged buffers, even though the host views are temporaries
+    assert argv[:3] == [("buf", 1), ("buf", 2), ("buf", 3)] and writable[:3] == [False, False, True]
+    assert ext.d2h == [(("buf", 3), n * c.element_size())]
+    # the result lands in the torch tensor itself; the inputs are untouched
+    assert bool((c.view(torch.uint8) == 0x3F).all()) and bool((a == 1).all())
+
+
+def test_array_passed_twice_is_staged_once_and_copied_back(monkeypatch, tmp_path):
+    monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
+    ext = _RecordingExt()
+    rt = HipRuntime(ext=ext)
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    n = 1031
+    a, b = np.ones(n, np.float32), np.ones(n, np.float32)
+    K.add_kernel(a, b, a, n, BLOCK=256)  # in place: a = a + b
+    _, argv, writable, _, _ = ext.launches[0]
+    assert argv[0] == argv[2] == ("buf", 1) and argv[1] == ("buf", 2)
+    assert ext.d2h == [(("buf", 1), 4 * n)]
+
+
 def test_scalar_packing_errors(monkeypatch, tmp_path):
     monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
     rt = HipRuntime(ext=_RecordingExt())

@@ -308,3 +308,43 @@ def test_trace_is_thread_local():
     for t in ts:
         t.join()
     assert not errors
+
+
+def test_bf16_typing_rules():
+    torch = pytest.importorskip("torch")
+    bf = torch.zeros(64, dtype=torch.bfloat16)
+
+    @eas.kernel
+    def bf16_plus_literal(a, BLOCK: eas.constexpr):
+        i = mk.tid(0, BLOCK)
+        mk.store(a, i, mk.load(a, i) + 1.0)  # bf16 + f32 literal: no implicit conversion
+
+    with pytest.raises(TypeError):
+        bf16_plus_literal.compile(bf, BLOCK=64)
+
+    @eas.kernel
+    def mixed_mma(c, BLOCK: eas.constexpr):
+        _ = mk.tid(0, BLOCK)
+        a = mk.alloc_tg_f16(64)
+        b = mk.alloc_tg_bf16(64)
+        mk.mma_store(c, 0, 8, mk.mma(a, 0, 8, b, 0, 8, mk.mma_zero()))
+
+    with pytest.raises(TypeError, match="bf16"):
+        mixed_mma.compile(f32(64), BLOCK=32)
+
+    # the verifier holds the same rule for IR built by hand
+    tg_a, tg_b = ValueRef(0, DType.F16), ValueRef(1, DType.BF16)
+    z, u = ValueRef(2, DType.SG_F32_8X8), ValueRef(3, DType.U32)
+    insts = (Inst("alloc_tg", tg_a, (64,)), Inst("alloc_tg", tg_b, (64,)), Inst("mma_zero", z, ()),
+             Inst("const", u, (0,)), Inst("mma", ValueRef(4, DType.SG_F32_8X8), (tg_a, u, u, tg_b, u, u, z)))
+    with pytest.raises(ValueError, match="bf16"):
+        validate_ir(IRModule("k", (), insts))
+
+    @eas.kernel
+    def round_trip(a, b, BLOCK: eas.constexpr):
+        i = mk.tid(0, BLOCK)
+        mk.store(b, i, mk.to_f32(mk.to_bf16(mk.load(a, i))))
+
+    ck = round_trip.compile(f32(64), f32(64), BLOCK=64)
+    assert [i.op for i in ck.ir.insts].count("cast") == 2
+    assert any(i.op == "cast" and i.out.dtype == DType.BF16 for i in ck.ir.insts)

@@ -284,3 +284,104 @@ def test_interp_tiled_matmul_matches_brute_force():
                             BM=16, BN=16, BK=16, K=k, NT=64, _grid=(K.cdiv(n, 16), K.cdiv(m, 16), 1))["c"]
     ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
     assert ops.rel_err(out.reshape(m, n), ref) <= 1e-5 * math.sqrt(k)
+
+
+# ---- bfloat16 (an addition to the reference's dtypes) -------------------------
+
+def _bf16_of_rational(q, negative_zero: bool = False) -> int:
+    """bfloat16 bit pattern of the exact rational ``q`` rounded to nearest even,
+    from the definition: 8 significant bits, exponents down to -126 (subnormal
+    spacing 2^-133), overflow to infinity past the largest finite value.  A zero
+    result keeps the sign of ``q`` (``negative_zero`` for an exact -0)."""
+    from fractions import Fraction
+
+    q = Fraction(q)
+    sign = 0x8000 if q < 0 or (q == 0 and negative_zero) else 0
+    a = abs(q)
+    if a == 0:
+        return sign
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    e = max(e, -126)
+    ulp = Fraction(2) ** (e - 7)
+    n = round(a / ulp)  # Fraction rounds half to even
+    r = n * ulp
+    if r >= Fraction(2) ** 128 - Fraction(2) ** (127 - 8):  # at or past the halfway point above max
+        return sign | 0x7F80
+    return sign | int(np.array([float(r)], np.float32).view(np.uint32)[0] >> 16)
+
+
+def _bf16_probe_values() -> np.ndarray:
+    rng = np.random.default_rng(11)
+    vals = [rng.standard_normal(2000, dtype=np.float32) * np.float32(100.0),
+            rng.integers(0, 2 ** 32, 3000, dtype=np.uint64).astype(np.uint32).view(np.float32)]
+    # exact ties and near-ties: low 16 bits 0x8000 (tie), 0x7FFF, 0x8001, for even and odd kept bits
+    hi = rng.integers(0, 2 ** 16, 400, dtype=np.uint64).astype(np.uint32) << 16
+    for low in (0x8000, 0x7FFF, 0x8001, 0x0000, 0xFFFF):
+        vals.append((hi | np.uint32(low)).view(np.float32))
+    vals.append(SPECIALS)
+    v = np.concatenate(vals).astype(np.float32)
+    return v[~np.isnan(v)]
+
+
+def test_bf16_rounding_matches_exact_rational_rounding():
+    from fractions import Fraction
+
+    x = _bf16_probe_values()
+    got = ops.f32_to_bf16(x)
+    fin = np.isfinite(x)
+    want = np.array([_bf16_of_rational(Fraction(float(v)), bool(np.signbit(v))) for v in x[fin]], np.uint16)
+    assert np.array_equal(got[fin], want)
+    assert np.array_equal(got[~fin], np.where(x[~fin] > 0, 0x7F80, 0xFF80).astype(np.uint16))
+    # the widening is exact, and a bf16 value converts to itself
+    assert np.array_equal(ops.f32_to_bf16(ops.bf16_to_f32(got)), got)
+
+
+def test_bf16_rounding_matches_torch_and_keeps_nans():
+    torch = pytest.importorskip("torch")
+    x = _bf16_probe_values()
+    t = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ops.f32_to_bf16(x), t)
+    nan = ops.f32_to_bf16(np.array([np.nan, -np.nan], np.float32))
+    assert np.all(np.isnan(ops.bf16_to_f32(nan)))
+
+
+def test_bf16_known_answers():
+    one = 0x3F80
+    u = np.array([0x7F7F7FFF, 0x7F7F8000], np.uint32).view(np.float32)  # below / at the tie above max finite
+    x = np.array([1 + 2.0 ** -8,               # tie between 1 and 1 + 2^-7: even is 1
+                  1 + 3 * 2.0 ** -8,           # tie between 1 + 2^-7 and 1 + 2^-6: even is 1 + 2^-6
+                  1 + 2.0 ** -8 + 2.0 ** -20,  # just above the tie: up
+                  F32.max,                     # past the tie above bf16's largest finite value: inf
+                  u[0], u[1],
+                  -2.0 ** -134,                # half of the smallest subnormal 2^-133: tie to -0
+                  -3 * 2.0 ** -135], np.float32)  # 0.75 of it: -2^-133
+    got = ops.f32_to_bf16(x)
+    assert got.tolist() == [one, one + 2, one + 1, 0x7F80, 0x7F7F, 0x7F80, 0x8000, 0x8001]
+
+
+def test_bf16_planted_truncation_fails_the_rational_check():
+    from fractions import Fraction
+
+    x = _bf16_probe_values()
+    x = x[np.isfinite(x)]
+    truncated = (x.view(np.uint32) >> 16).astype(np.uint16)  # round toward zero: a plausible mistake
+    want = np.array([_bf16_of_rational(Fraction(float(v)), bool(np.signbit(v))) for v in x], np.uint16)
+    assert not np.array_equal(truncated, want)
+
+
+def test_add_bf16_is_the_correctly_rounded_exact_sum():
+    from fractions import Fraction
+
+    rng = np.random.default_rng(12)
+    a = ops.f32_to_bf16(rng.standard_normal(3000, dtype=np.float32) * np.float32(2.0) ** rng.integers(-30, 30, 3000))
+    b = ops.f32_to_bf16(rng.standard_normal(3000, dtype=np.float32) * np.float32(2.0) ** rng.integers(-30, 30, 3000))
+    # add the cases with exponent gaps where binary32 must round before bfloat16 does
+    a = np.concatenate([a, ops.f32_to_bf16(np.array([1.0, 1.0, 1.0, 2.0 ** 100, 1.5], np.float32))])
+    b = np.concatenate([b, ops.f32_to_bf16(np.array([2.0 ** -8 + 2.0 ** -15, 2.0 ** -30, -2.0 ** -9, 1.0, 2.0 ** -8],
+                                                    np.float32))])
+    got = ops.add_bf16(a, b)
+    fa, fb = ops.bf16_to_f32(a), ops.bf16_to_f32(b)
+    want = np.array([_bf16_of_rational(Fraction(float(x)) + Fraction(float(y))) for x, y in zip(fa, fb)], np.uint16)
+    assert np.array_equal(got, want)
