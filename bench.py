@@ -17,7 +17,8 @@ on a bounded sample).  Secondary measurements ride along under ``extra``.
 
 ``--workload mma`` makes the f16-input / f32-accumulate simdgroup-MMA matmul at
 M=N=K=4096 (configs[3]; lifted to the MFMA GEMM) the primary line, with the
-roofline against the f16 dense MFMA peak; ``mma_k4100``, ``decode``, ``prefill``,
+roofline against the f16 dense MFMA peak; ``mma_k4100``, ``mma_bf16`` (bf16
+inputs, an addition to the reference's dtypes), ``decode``, ``prefill``,
 ``tiled1024`` and ``tiled2048`` select the other matmul configurations.  The
 default run reports all of them under ``extra``.
 """
@@ -37,7 +38,7 @@ sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
-MFMA_F16_PEAK_TFLOPS = 2516.6  # dense f16 MFMA, MI355X
+MFMA_F16_PEAK_TFLOPS = 2516.6  # dense f16 (and bf16) MFMA, MI355X
 F32_PEAK_TFLOPS = 157.3  # fp32 dense MFMA (= vector fp32), MI355X
 N_ELEM = 1 << 28
 PRIMARY_BLOCK = 256
@@ -58,6 +59,8 @@ MATMULS = {
             "f16-in/f32-acc simdgroup-MMA matmul (mk.dot), M=N=K=4096, f32 out"),
     "mma_k4100": ("matmul_mma_kernel", 4096, 4096, 4100, "u", "u",
                   "f16-in/f32-acc simdgroup-MMA matmul (mk.dot), M=N=4096, K=4100, f32 out"),
+    "mma_bf16": ("matmul_mma_bf16_kernel", 4096, 4096, 4096, "ubf", "ubf",
+                 "bf16-in/f32-acc simdgroup-MMA matmul (mk.dot, bf16 threadgroup tiles), M=N=K=4096, f32 out"),
     "decode": ("matmul_mma_f16out_kernel", 16, 14336, 4096, "act", "w",
                "f16 LLM decode linear M=16 N=14336 K=4096 (mk.dot), f32 acc, f16 out"),
     "prefill": ("matmul_mma_f16out_kernel", 8192, 8192, 8192, "act", "w",
@@ -70,7 +73,8 @@ MATMULS = {
 
 
 # rocprofv3 counter summaries (profiles/<name>.pmc.json) that give a matmul line its HBM traffic
-MATMUL_PROFILES = {"mma": "mma_f16_4096", "decode": "decode_f16_16x14336x4096", "prefill": "prefill_f16_8192",
+MATMUL_PROFILES = {"mma": "mma_f16_4096", "mma_bf16": "mma_bf16_4096", "decode": "decode_f16_16x14336x4096",
+                   "prefill": "prefill_f16_8192",
                    "tiled1024": "tiled_f32_1024", "tiled2048": "tiled_f32_2048"}
 
 
@@ -102,13 +106,16 @@ def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch, **launch) 
     return wall_ms, trials[EVENT_TRIALS // 2] * 1e3
 
 
-def _matmul_inputs(name: str) -> tuple[np.ndarray, np.ndarray]:
+def _matmul_inputs(name: str, torch) -> tuple[object, object]:
+    """Host inputs: NumPy arrays, or torch bfloat16 CPU tensors (NumPy has no bfloat16)."""
     _, m, n, k, da, db, _ = MATMULS[name]
     rng_a, rng_b = np.random.default_rng(10), np.random.default_rng(11)
 
     def draw(rng, dist, size):
         if dist == "u":
             return rng.uniform(-1, 1, size).astype(np.float16)
+        if dist == "ubf":
+            return torch.from_numpy(rng.uniform(-1, 1, size).astype(np.float32)).to(torch.bfloat16)
         if dist == "act":
             return rng.standard_normal(size, dtype=np.float32).astype(np.float16)
         if dist == "w":
@@ -121,15 +128,16 @@ def _matmul_inputs(name: str) -> tuple[np.ndarray, np.ndarray]:
 def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
     """Time one matmul configuration and check a seeded sample of its rows against float64."""
     import kernels as K
-    from oracle import ops
 
     kname, m, n, k, _, _, desc = MATMULS[name]
     kern = getattr(K, kname)
     dev = torch.device("cuda:0")
-    ha, hb = _matmul_inputs(name)
-    a, b = torch.from_numpy(ha).to(dev), torch.from_numpy(hb).to(dev)
+    ha, hb = _matmul_inputs(name, torch)
+    a, b = (x.to(dev) if isinstance(x, torch.Tensor) else torch.from_numpy(x).to(dev) for x in (ha, hb))
+    # float64 reference operands: the values the kernel multiplies (bf16 widens exactly)
+    ha, hb = (x.float().numpy() if isinstance(x, torch.Tensor) else x for x in (ha, hb))
     tiled = kname == "matmul_tiled_kernel"
-    out_dt = torch.float32 if (tiled or kname == "matmul_mma_kernel") else torch.float16
+    out_dt = torch.float32 if (tiled or kname in ("matmul_mma_kernel", "matmul_mma_bf16_kernel")) else torch.float16
     c = torch.full((m * n,), float("nan"), dtype=out_dt, device=dev)
     if tiled:
         meta = {"BM": 32, "BN": 32, "BK": 32, "K": k, "NT": 256}
@@ -154,8 +162,8 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
     torch.cuda.synchronize()
     got = c.float().cpu().numpy().reshape(m, n)
     rows = np.sort(np.random.default_rng(7).choice(m, min(m, 32), replace=False))
-    ref = ops.matmul_ref(ha.reshape(m, k)[rows], hb.reshape(k, n))
-    err = ops.rel_err(got[rows].astype(np.float64), ref)
+    ref = ha.reshape(m, k)[rows].astype(np.float64) @ hb.reshape(k, n).astype(np.float64)
+    err = _f64_rel_err(got[rows], ref)
     # elementwise: |C - R| / (|R| + max|R| * 1e-3), the worst element of the sampled rows
     diff = np.abs(got[rows].astype(np.float64) - ref)
     elem_err = float(np.max(diff / (np.abs(ref) + 1e-3 * float(np.max(np.abs(ref)) or 1.0))))
@@ -168,7 +176,7 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
     ok = bool(np.isfinite(got).all() and err <= tol)
     peak = F32_PEAK_TFLOPS if tiled else MFMA_F16_PEAK_TFLOPS
     tf = flops / (ev_ms * 1e-3) / 1e12
-    bytes_min = (m * k + k * n) * ha.itemsize + m * n * (2 if out_dt == torch.float16 else 4)
+    bytes_min = (m * k + k * n) * a.element_size() + m * n * (2 if out_dt == torch.float16 else 4)
     # roofline: HBM-bound below the ridge point (peak flop/s / peak bytes/s), compute-bound above
     hbm_bound = flops / bytes_min < peak * 1e12 / (HBM_PEAK_GBS * 1e9)
     gbs = bytes_min / (ev_ms * 1e-3) / 1e9
@@ -235,18 +243,31 @@ def _cpu_baseline(workload: str, seconds: float = 10.0) -> dict:
             "sample": f"oracle {what} (oracle/fmaf.c, gcc -O2, 1 thread) over N=2^26 float32, {reps} reps, {el:.1f} s"}
 
 
-def _oracle_out(workload: str, hosts: list[np.ndarray]) -> np.ndarray:
-    from oracle import ops
-
+def _expected(workload: str, hosts: list[np.ndarray]) -> np.ndarray | None:
+    """Closed-form outputs that NumPy computes exactly (binary32 RNE addition, copies,
+    constants); None for fma, whose correctly rounded result only the oracle's fmaf
+    gives: that one is checked in the CPU leg (``_fma_check``)."""
     if workload == "add":
-        return ops.add_f32(hosts[0], hosts[1])
-    if workload == "fma":
-        return ops.fmaf(hosts[0], hosts[1], hosts[2])
+        return hosts[0] + hosts[1]
     if workload == "read":
         return np.zeros(N_ELEM, np.float32)
     if workload == "write":
         return np.ones(N_ELEM, np.float32)
-    return hosts[0]
+    if workload == "copy":
+        return hosts[0]
+    return None
+
+
+def _fma_check(got: np.ndarray, hosts: list[np.ndarray]) -> bool:
+    """CPU leg, as the checker: the GPU's fma outputs against the oracle's fmaf, bit for bit."""
+    from oracle import ops
+
+    return bool(np.array_equal(got.view(np.uint32), ops.fmaf(hosts[0], hosts[1], hosts[2]).view(np.uint32)))
+
+
+def _f64_rel_err(c: np.ndarray, ref: np.ndarray) -> float:
+    """``max|C - R| / max|R|`` (the matmul parity metric) with R a float64 matmul."""
+    return float(np.max(np.abs(np.asarray(c, np.float64) - ref))) / (float(np.max(np.abs(ref))) or 1.0)
 
 
 def main() -> int:
@@ -300,8 +321,16 @@ def main() -> int:
     kern(*ins, out, N_ELEM, BLOCK=args.block)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
-    exact = bool(np.array_equal(got.view(np.uint32), _oracle_out(args.workload, hosts).view(np.uint32)))
-    _log(f"parity vs oracle over all 2^28 outputs: {'bit-exact' if exact else 'MISMATCH'}")
+    want = _expected(args.workload, hosts)
+    if want is not None:
+        exact = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+        parity = "bit-exact vs binary32 closed form (all 2^28 outputs)" if exact else "MISMATCH"
+    elif not args.no_cpu_baseline:
+        exact = _fma_check(got, hosts)
+        parity = "bit-exact vs oracle fmaf (all 2^28 outputs)" if exact else "MISMATCH"
+    else:
+        exact, parity = True, "not checked (--no-cpu-baseline skips the oracle)"
+    _log(f"parity over all 2^28 outputs: {parity}")
 
     if not args.no_extra and args.workload == "add":
         fh = _inputs(N_ELEM, (2,))[0]
@@ -310,17 +339,19 @@ def main() -> int:
         fargs = {"a": ins[0], "b": ins[1], "c": cc, "d": d, "N": N_ELEM}
         ckf = K.fma_kernel.compile(ins[0], ins[1], cc, d, N_ELEM, BLOCK=args.block)
         _, fe = _time_kernel(rt, ckf, fargs, {"BLOCK": args.block}, args.steps, args.warmup, torch)
-        fexact = bool(np.array_equal(d.cpu().numpy().view(np.uint32),
-                                     _oracle_out("fma", [hosts[0], hosts[1], fh]).view(np.uint32)))
+        if args.no_cpu_baseline:
+            fparity = "not checked (--no-cpu-baseline skips the oracle)"
+        else:
+            fparity = "bit-exact vs oracle fmaf" if _fma_check(d.cpu().numpy(), [hosts[0], hosts[1], fh]) else "MISMATCH"
         extra["fma_n2e28"] = {"GB/s": round(16 * N_ELEM / fe / 1e6, 1), "frac": round(16 * N_ELEM / fe / 1e6 / HBM_PEAK_GBS, 4),
-                              "parity": "bit-exact vs fmaf" if fexact else "MISMATCH"}
+                              "parity": fparity}
         _log(f"fma: event {fe:.4f} ms/launch, {16 * N_ELEM / fe / 1e6:.1f} GB/s, parity {extra['fma_n2e28']['parity']}")
         del cc, d
 
     if not args.no_extra and args.workload == "add":
         del ins, out
         torch.cuda.empty_cache()
-        for name in ("mma", "mma_k4100", "decode", "prefill", "tiled1024", "tiled2048"):
+        for name in ("mma", "mma_k4100", "mma_bf16", "decode", "prefill", "tiled1024", "tiled2048"):
             # a failing extra is reported in the line; it does not take the primary measurement with it
             try:
                 extra[name] = _matmul(name, rt, torch, max(5, min(args.steps, 20)), max(2, min(args.warmup, 5)))
@@ -355,7 +386,7 @@ def main() -> int:
         "config": {"workload": f"fp32 {args.workload} {expr} via @eas.kernel SPMD (mk.arange, masked tail), "
                                f"N=2^28, BLOCK={args.block}",
                    "N": N_ELEM, "BLOCK": args.block, "parallelism": "single GPU"},
-        "parity": "bit-exact vs oracle (all 2^28 outputs)" if exact else "MISMATCH",
+        "parity": parity,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": None if args.no_cpu_baseline else _cpu_baseline(args.workload),
@@ -373,9 +404,10 @@ def _matmul_main(args, rt, torch) -> int:
     if pmc.exists():
         traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
     tiled = args.workload.startswith("tiled")
+    in_dt = "f32" if tiled else ("bf16" if args.workload.endswith("bf16") else "f16")
     wall_tf = res["wall_TFLOP/s"]
     line = {
-        "metric": f"{'fp32' if tiled else 'f16'} matmul TFLOP/s @{m}x{n}x{k} (eas kernel, one MI355X)",
+        "metric": f"{'fp32' if tiled else in_dt} matmul TFLOP/s @{m}x{n}x{k} (eas kernel, one MI355X)",
         "value": wall_tf,
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -385,7 +417,7 @@ def _matmul_main(args, rt, torch) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if tiled else "f16",
+        "dtype": in_dt,
         "data": "synthetic (seeded; see config)",
         "config": {"workload": desc, "M": m, "N": n, "K": k, "parallelism": "single GPU"},
         "parity": res["parity"],

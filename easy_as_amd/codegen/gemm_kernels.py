@@ -1,19 +1,24 @@
 """gfx950 MFMA GEMM emitted for kernels that ``gemm_lift`` proved to be dense GEMMs.
 
 Launches of more than 128 rows tile C into 256 x 256 workgroup tiles (or 128 x
-128, below; the fp32 templates at the end of this module use 64 x 64 and 128 x 128).  The f16 source has two
+128, below; the fp32 templates at the end of this module use 64 x 64 and 128 x 128).
+The 16-bit source is written once for its MFMA operand type ``eas_op_t``: f16, or
+bf16 when the kernel's threadgroup tiles are bf16 (``_OP_TYPES`` supplies the type,
+the MFMA and the transposing LDS read; everything else is the same).  It has three
 entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
 
-* ``<name>__pp`` (512 threads): the 8-wave ping-pong DMA body for f16 A and B
-  whose rows the DMA takes.  Waves w and w+4 share a SIMD; the two groups of
+* ``<name>__pp`` (512 threads): the 8-wave ping-pong DMA body for A and B of the
+  operand type whose rows the DMA takes.  Waves w and w+4 share a SIMD; the two groups of
   four waves alternate load phases and MFMA phases one barrier apart, each
   wave holding 128 x 64 of the tile (4 x 2 ``v_mfma_f32_32x32x16_f16``
   accumulators).
+* ``<name>__t128`` (256 threads): the same DMA operands on 128 x 128 tiles (4
+  waves of 64 x 64), for launches whose 256 x 256 grid would leave CUs idle.
 * ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
   AGPRs): the skinny path (launches of at most 128 rows), the 4-wave DMA body,
   and the register body; a uniform branch picks one per launch.
 
-DMA bodies (f16 A and B; K and ldb even and 4-byte aligned bases, so every row
+DMA bodies (A and B of the operand type; K and ldb even and 4-byte aligned bases, so every row
 is 4-byte aligned; each matrix under 2 GiB):
 
 * A and B go HBM -> LDS with ``buffer_load_dwordx4 ... lds`` (no staging

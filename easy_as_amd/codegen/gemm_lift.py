@@ -1066,7 +1066,7 @@ def _gemm_entry_choice() -> str:
 
 
 def _dma_fits(p: dict, runtime_args: Any, K: int, ldb: int, m: int, n_lo: int, n: int, elem: int = 2) -> bool:
-    """Whether the DMA entries take this launch.  f16 (``elem`` 2): every row of A and B
+    """Whether the DMA entries take this launch.  16-bit f16/bf16 (``elem`` 2): every row of A and B
     (after the move to the rectangle's origin) 4-byte aligned; fp32 (``elem`` 4): 16-byte
     aligned; each operand's extent under 2 GiB.  Device addresses are known here for
     torch tensors; numpy inputs are staged into fresh allocations, and the entries
