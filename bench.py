@@ -125,7 +125,12 @@ def _matmul_inputs(name: str, torch) -> tuple[object, object]:
     return draw(rng_a, da, m * k), draw(rng_b, db, k * n)
 
 
-def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
+# --data for matmul workloads: the configs' seeded distributions (the metric), or the same
+# shapes on constant data, to show how much of the time goes to the MFMA's data-dependent power
+MATMUL_DATA = ("seeded", "zeros", "ones", "signs")
+
+
+def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded") -> dict:
     """Time one matmul configuration and check a seeded sample of its rows against float64."""
     import kernels as K
 
@@ -133,6 +138,12 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int) -> dict:
     kern = getattr(K, kname)
     dev = torch.device("cuda:0")
     ha, hb = _matmul_inputs(name, torch)
+    if data != "seeded":
+        # same dtype and shape; zeros, ones, or the signs (+-1) of the seeded values
+        def const(x):
+            t = x if isinstance(x, torch.Tensor) else torch.from_numpy(x)
+            return {"zeros": torch.zeros_like, "ones": torch.ones_like, "signs": torch.sign}[data](t)
+        ha, hb = const(ha), const(hb)
     a, b = (x.to(dev) if isinstance(x, torch.Tensor) else torch.from_numpy(x).to(dev) for x in (ha, hb))
     # float64 reference operands: the values the kernel multiplies (bf16 widens exactly)
     ha, hb = (x.float().numpy() if isinstance(x, torch.Tensor) else x for x in (ha, hb))
@@ -279,7 +290,12 @@ def main() -> int:
     p.add_argument("--block", type=int, default=PRIMARY_BLOCK)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
+    p.add_argument("--data", choices=MATMUL_DATA, default="seeded",
+                   help="matmul workloads only: input data (anything but 'seeded' is not the metric's data)")
     args = p.parse_args()
+    if args.data != "seeded" and args.workload not in MATMULS:
+        print("--data applies to the matmul workloads only", file=sys.stderr)
+        return 2
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               "(the elementwise path would shard N contiguously per GPU with no exchange).", file=sys.stderr)
@@ -349,6 +365,34 @@ def main() -> int:
         del cc, d
 
     if not args.no_extra and args.workload == "add":
+        # the plumbing sizes, launch-latency bound.  us_per_call is a whole eas call
+        # (binding, specialisation lookup, launch plan, argument packing, async launch) averaged
+        # over back-to-back calls; us_per_launch is the GPU time by HIP events.
+        for n in (1031, 1 << 20):
+            sa, sb = ins[0][:n], ins[1][:n]
+            sc = torch.empty(n, dtype=torch.float32, device=dev)
+            calls = 2000
+            for _ in range(50):
+                K.add_kernel(sa, sb, sc, n, BLOCK=PRIMARY_BLOCK, _sync=False)
+            rt.synchronize()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                K.add_kernel(sa, sb, sc, n, BLOCK=PRIMARY_BLOCK, _sync=False)
+            rt.synchronize()
+            torch.cuda.synchronize()
+            per_call = (time.perf_counter() - t0) / calls
+            cks = K.add_kernel.compile(sa, sb, sc, n, BLOCK=PRIMARY_BLOCK)
+            sargs = {"a": sa, "b": sb, "c": sc, "N": n}
+            ev = sorted(rt.benchmark(cks, sargs, {"BLOCK": PRIMARY_BLOCK}, repeat=200, warmup=20)
+                        for _ in range(EVENT_TRIALS))[EVENT_TRIALS // 2]
+            ok = bool(np.array_equal(sc.cpu().numpy().view(np.uint32), (hosts[0][:n] + hosts[1][:n]).view(np.uint32)))
+            extra[f"add_n{n}"] = {"us_per_call": round(per_call * 1e6, 2), "us_per_launch": round(ev * 1e6, 2),
+                                  "GB/s": round(12 * n / ev / 1e9, 1),
+                                  "parity": "bit-exact vs binary32 closed form" if ok else "MISMATCH"}
+            _log(f"add N={n}: {per_call * 1e6:.2f} us per eas call, {ev * 1e6:.2f} us per launch (events), "
+                 f"parity {extra[f'add_n{n}']['parity']}")
+            del sc
         del ins, out
         torch.cuda.empty_cache()
         for name in ("mma", "mma_k4100", "mma_bf16", "decode", "prefill", "tiled1024", "tiled2048"):
@@ -397,7 +441,7 @@ def main() -> int:
 
 
 def _matmul_main(args, rt, torch) -> int:
-    res = _matmul(args.workload, rt, torch, args.steps, args.warmup)
+    res = _matmul(args.workload, rt, torch, args.steps, args.warmup, args.data)
     _, m, n, k, _, _, desc = MATMULS[args.workload]
     traffic = None
     pmc = ROOT / "profiles" / f"{MATMUL_PROFILES.get(args.workload, args.workload)}.pmc.json"
@@ -418,7 +462,8 @@ def _matmul_main(args, rt, torch) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": in_dt,
-        "data": "synthetic (seeded; see config)",
+        "data": "synthetic (seeded; see config)" if args.data == "seeded" else
+                f"constant inputs ({args.data}): a power probe, not the configs' distribution",
         "config": {"workload": desc, "M": m, "N": n, "K": k, "parallelism": "single GPU"},
         "parity": res["parity"],
         "parity_elementwise_err": res["elementwise_err"], "parity_max_abs_err": res["max_abs_err"],

@@ -389,6 +389,22 @@ def test_array_passed_twice_is_staged_once_and_copied_back(monkeypatch, tmp_path
     assert ext.d2h == [(("buf", 1), 4 * n)]
 
 
+def test_benchmark_rejects_written_numpy_arrays(monkeypatch, tmp_path):
+    """As the reference (eas/runtime/metal.py:455-462): timing with a written host array
+    would time host copies, so benchmark() refuses it before launching anything."""
+    monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
+    ext = _RecordingExt()
+    rt = HipRuntime(ext=ext)
+    x = np.ones(1031, np.float32)
+    ck = K.add_kernel.compile(x, x, x.copy(), 1031, BLOCK=256)
+    args = {"a": x, "b": x, "c": np.zeros(1031, np.float32), "N": 1031}
+    with pytest.raises(ValueError, match="numpy"):
+        rt.benchmark(ck, args, {"BLOCK": 256}, repeat=3)
+    assert ext.launches == []
+    with pytest.raises(ValueError):
+        rt.benchmark(ck, args, {"BLOCK": 256}, repeat=0)
+
+
 def test_scalar_packing_errors(monkeypatch, tmp_path):
     monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
     rt = HipRuntime(ext=_RecordingExt())
