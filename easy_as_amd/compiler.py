@@ -68,16 +68,20 @@ def _is_torch_tensor(v: Any) -> bool:
     return torch is not None and isinstance(v, torch.Tensor)
 
 
+_TORCH_BUFFER_DTYPES: dict[Any, DType] = {}
+
+
 def _torch_buffer_dtype(v: Any) -> DType:
+    dt = _TORCH_BUFFER_DTYPES.get(v.dtype)
+    if dt is not None:
+        return dt
     torch = _torch()
     assert torch is not None
-    if v.dtype == torch.float32:
-        return DType.F32
-    if v.dtype == torch.float16:
-        return DType.F16
-    if v.dtype == torch.bfloat16:
-        return DType.BF16
-    raise TypeError(f"unsupported torch dtype: {v.dtype} (expected float32, float16 or bfloat16)")
+    _TORCH_BUFFER_DTYPES.update({torch.float32: DType.F32, torch.float16: DType.F16, torch.bfloat16: DType.BF16})
+    dt = _TORCH_BUFFER_DTYPES.get(v.dtype)
+    if dt is None:
+        raise TypeError(f"unsupported torch dtype: {v.dtype} (expected float32, float16 or bfloat16)")
+    return dt
 
 
 def _scalar_dtype(v: Any) -> DType:
@@ -122,7 +126,7 @@ def _arg_key(v: Any) -> tuple[str, DType, str | None]:
     else:
         torch = _torch()
         if torch is not None and isinstance(v, torch.Tensor):
-            return ("buffer", _torch_buffer_dtype(v), v.device.type)
+            return ("buffer", _torch_buffer_dtype(v), "cuda" if v.is_cuda else v.device.type)
     s = classify_arg(v)
     return (s.kind, s.dtype, s.device)
 

@@ -43,6 +43,9 @@ def _cdiv(a: int, b: int) -> int:
     return -(-a // b)
 
 
+_NP_DTYPES = {DType.F16: np.float16, DType.F32: np.float32}
+
+
 def pack_scalar(dtype: DType, value: Any) -> bytes:
     """Kernel-argument bytes of a scalar (reference ``metal.py:28-38``)."""
     if dtype == DType.U32:
@@ -181,6 +184,8 @@ class HipRuntime:
         self._max_in_flight: int | None = None
         self._torch: Any = None
         self._torch_probed = False
+        self._raw_stream: Any = None
+        self._arg_specs: dict[int, tuple[IRModule, frozenset[str], tuple[tuple[str, bool, DType, bool], ...]]] = {}
         self._arch_checked = ext is not None
         self._cus = 256
 
@@ -253,48 +258,49 @@ class HipRuntime:
         # once.  The arrays are held here because an id is only unique while its object lives
         # (the NumPy views made of torch host tensors below are temporaries).
         staged: dict[int, tuple[Any, np.ndarray]] = {}
-        cuda_device = None
-        for arg in ir.args:
-            v = runtime_args[arg.name]
-            if arg.kind == "scalar":
-                argv.append(pack_scalar(arg.dtype, v))
+        cuda_index = None
+        tensor_t = torch.Tensor if torch is not None else ()
+        for name, scalar, dtype, w in self._arg_spec(ir, writes):
+            v = runtime_args[name]
+            if scalar:
+                argv.append(pack_scalar(dtype, v))
                 writable.append(False)
                 continue
-            want = np.float16 if arg.dtype == DType.F16 else np.float32
-            w = arg.name in writes
-            if torch is not None and isinstance(v, torch.Tensor):
-                if v.dtype != self._torch_dtypes[arg.dtype]:
-                    raise TypeError(f"{arg.name!r} must be {arg.dtype.value}, got {v.dtype}")
-                dev = v.device
-                if dev.type == "cuda":
+            want = None
+            if isinstance(v, tensor_t):
+                if v.dtype != self._torch_dtypes[dtype]:
+                    raise TypeError(f"{name!r} must be {dtype.value}, got {v.dtype}")
+                if v.is_cuda:
                     if not v.is_contiguous():
-                        raise ValueError(f"{arg.name!r} must be contiguous")
+                        raise ValueError(f"{name!r} must be contiguous")
                     # a non-owning view of the tensor's memory that keeps the tensor alive
-                    argv.append(mod.wrap_pointer(v.data_ptr(), v.numel() * v.element_size(), v))
+                    argv.append(mod.wrap_pointer(v.data_ptr(), v.nbytes, v))
                     writable.append(w)
-                    cuda_device = dev
+                    cuda_index = v.get_device()
                     continue
-                if dev.type != "cpu":
-                    raise TypeError(f"unsupported torch device for {arg.name!r}: {dev}")
-                if arg.dtype == DType.BF16:
+                if v.device.type != "cpu":
+                    raise TypeError(f"unsupported torch device for {name!r}: {v.device}")
+                if dtype == DType.BF16:
                     # NumPy has no bfloat16: stage the raw 16-bit patterns (same memory)
                     v = v.detach().contiguous().view(torch.int16).numpy()
                     want = np.int16
                 else:
                     v = v.detach().contiguous().numpy()
+            if want is None:
+                want = _NP_DTYPES.get(dtype)
             if _is_eas_tensor(v):
                 if v.device == "hip":
                     if np.dtype(v.dtype) != np.dtype(want):
-                        raise TypeError(f"{arg.name!r} dtype mismatch: expected {np.dtype(want)}, got {v.dtype}")
+                        raise TypeError(f"{name!r} dtype mismatch: expected {np.dtype(want)}, got {v.dtype}")
                     argv.append(v._hip_buffer())
                     writable.append(w)
                     continue
                 v = v.numpy()
             if isinstance(v, np.ndarray):
                 if v.dtype != want:
-                    raise TypeError(f"{arg.name!r} must be {np.dtype(want).name}, got {v.dtype}")
+                    raise TypeError(f"{name!r} must be {np.dtype(want).name}, got {v.dtype}")
                 if not v.flags.c_contiguous:
-                    raise ValueError(f"{arg.name!r} must be C-contiguous")
+                    raise ValueError(f"{name!r} must be C-contiguous")
                 hit = staged.get(id(v))
                 if hit is None:
                     buf = mod.alloc_buffer(max(int(v.nbytes), 1), "private")
@@ -309,10 +315,29 @@ class HipRuntime:
                 argv.append(buf)
                 writable.append(w)
                 continue
-            raise TypeError(f"expected numpy.ndarray, eas.Tensor or torch.Tensor for {arg.name!r}, got {type(v)!r}")
+            raise TypeError(f"expected numpy.ndarray, eas.Tensor or torch.Tensor for {name!r}, got {type(v)!r}")
         # launches with torch GPU tensors go on torch's current stream, ordered with torch's own work
-        stream = None if cuda_device is None else torch.cuda.current_stream(cuda_device).cuda_stream
+        stream = None if cuda_index is None else self._current_stream(cuda_index)
         return argv, writable, copy_back, stream
+
+    def _arg_spec(self, ir: IRModule, writes: frozenset[str]) -> tuple[tuple[str, bool, DType, bool], ...]:
+        """Per-argument (name, is scalar, dtype, written) of a kernel, built once per IR."""
+        hit = self._arg_specs.get(id(ir))
+        if hit is not None and hit[0] is ir and hit[1] == writes:
+            return hit[2]
+        spec = tuple((a.name, a.kind == "scalar", a.dtype, a.name in writes) for a in ir.args)
+        self._arg_specs[id(ir)] = (ir, writes, spec)  # holding ir keeps its id unique
+        return spec
+
+    def _current_stream(self, device_index: int) -> int:
+        """torch's current stream on a device, as a raw hipStream_t address."""
+        raw = self._raw_stream
+        if raw is None:
+            torch = self._torch_mod()
+            raw = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
+                lambda i: torch.cuda.current_stream(i).cuda_stream)
+            self._raw_stream = raw
+        return int(raw(device_index))
 
     # -- launching ------------------------------------------------------------------
     def run(

@@ -401,6 +401,35 @@ def test_async_launches_and_synchronize(gpu_runtime):
         assert _bits_equal(o.numpy(), ops.add_f32(a, b))
 
 
+def test_launches_follow_torch_current_stream(gpu_runtime):
+    """An eas launch with torch GPU tensors goes on torch's current stream: inputs that torch
+    writes on a side stream (after a long matmul, so they land late) are seen by the kernel,
+    and torch work queued after it on that stream sees the kernel's output."""
+    import torch
+
+    n = 1 << 22
+    a_np, b_np = seeded_normal(0, n), seeded_normal(1, n)
+    ha, hb = torch.from_numpy(a_np).cuda(), torch.from_numpy(b_np).cuda()
+    a = torch.zeros(n, device="cuda")
+    b = torch.zeros(n, device="cuda")
+    c = torch.zeros(n, device="cuda")
+    big = torch.ones(4096, 4096, device="cuda")
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()  # default priority
+    with torch.cuda.stream(side):
+        for _ in range(4):
+            big = big @ big * (1.0 / 4096)  # a few ms of work ahead of the input copies
+        a.copy_(ha)  # device-to-device, queued behind the matmuls; the host does not wait
+        b.copy_(hb)
+        K.add_kernel(a, b, c, n, BLOCK=256, _sync=False)
+        d = c * 1.0  # torch work after the kernel on the same stream
+    gpu_runtime.synchronize()
+    side.synchronize()
+    want = ops.add_f32(a_np, b_np)
+    assert _bits_equal(c.cpu().numpy(), want)
+    assert _bits_equal(d.cpu().numpy(), want)
+
+
 def test_benchmark_returns_positive_seconds(gpu_runtime):
     n = 1 << 20
     a = eas.tensor(seeded_normal(0, n), device="hip")
