@@ -9,7 +9,11 @@ then exactly K steps between device synchronisations.
 Prints ONE JSON line: the driver's fields plus ``roofline`` (achieved HBM GB/s
 of the kernel from HIP events on its launch stream, vs 8 TB/s) and
 ``cpu_baseline`` (the oracle's C restatement of the same arithmetic, one core,
-on a bounded sample).  Secondary measurements ride along under ``extra``.
+on a bounded sample).  ``vendor`` times the same operation through torch (ROCm:
+``torch.add``, hipBLASLt/rocBLAS ``torch.matmul``) on the same device-resident
+inputs, in the same run, with the same event method; each matmul entry under
+``extra`` carries its ``torch_matmul``.  Secondary measurements ride along under
+``extra``.
 
 ``--workload copy|fma|read|write`` measures the other elementwise kernels the same way
 (``copy`` is the known-size kernel that calibrates HBM byte counters; ``read`` and
@@ -104,6 +108,24 @@ def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch, **launch) 
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     trials = sorted(rt.benchmark(ck, rargs, meta, repeat=steps, warmup=0, **launch) for _ in range(EVENT_TRIALS))
     return wall_ms, trials[EVENT_TRIALS // 2] * 1e3
+
+
+def _torch_event_ms(fn, steps: int, warmup: int, torch) -> float:
+    """ms per call of a torch operation on torch's current stream: the median of EVENT_TRIALS
+    trials of ``steps`` back-to-back calls between torch events (the vendor comparison)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    trials = []
+    for _ in range(EVENT_TRIALS):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            fn()
+        t1.record()
+        t1.synchronize()
+        trials.append(t0.elapsed_time(t1) / steps)
+    return sorted(trials)[EVENT_TRIALS // 2]
 
 
 def _matmul_inputs(name: str, torch) -> tuple[object, object]:
@@ -205,6 +227,16 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded")
     }
     _log(f"{name}: {res['TFLOP/s']} TFLOP/s ({100 * res['frac']:.1f}% of {peak}), {ev_ms:.4f} ms/launch, "
          f"parity {res['parity']}, compile {compile_s:.1f} s")
+    # vendor comparison on the same device-resident operands: torch.matmul (hipBLASLt/rocBLAS),
+    # whose output has the input dtype (the f32-output eas lines write twice its output bytes)
+    if data == "seeded":
+        A2, B2 = a.view(m, k), b.view(k, n)
+        out_t = torch.empty((m, n), dtype=a.dtype, device=dev)
+        tms = _torch_event_ms(lambda: torch.matmul(A2, B2, out=out_t), steps, warmup, torch)
+        res["torch_matmul"] = {"TFLOP/s": round(flops / (tms * 1e-3) / 1e12, 1), "ms_per_launch": round(tms, 5),
+                               "out_dtype": str(a.dtype).replace("torch.", "")}
+        _log(f"{name}: torch.matmul {res['torch_matmul']['TFLOP/s']} TFLOP/s, {tms:.4f} ms/launch")
+        del out_t
     del a, b, c
     torch.cuda.empty_cache()
     return res
@@ -328,6 +360,15 @@ def main() -> int:
         return wall_ms, ev_ms
 
     wall_ms, ev_ms = measure(args.block)
+    # vendor comparison on the same device-resident inputs: the torch (ROCm) operation
+    tfn = {"add": lambda: torch.add(ins[0], ins[1], out=out),
+           "fma": lambda: torch.addcmul(ins[2], ins[0], ins[1], out=out),
+           "copy": lambda: out.copy_(ins[0]), "read": lambda: ins[0].sum(), "write": lambda: out.fill_(1.0)}
+    texpr = {"add": "torch.add(a, b, out=c)", "fma": "torch.addcmul(c, a, b, out=d)", "copy": "c.copy_(a)",
+             "read": "a.sum()", "write": "c.fill_(1.0)"}[args.workload]
+    tms = _torch_event_ms(tfn[args.workload], args.steps, args.warmup, torch)
+    vendor = {"op": texpr, "GB/s": round(per_elem * N_ELEM / tms / 1e6, 1), "ms_per_launch": round(tms, 5)}
+    _log(f"{texpr}: {tms:.4f} ms/launch, {vendor['GB/s']} GB/s")
     extra: dict = {}
     if not args.no_extra and args.workload == "add":
         other = 1024 if args.block != 1024 else 256
@@ -434,6 +475,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": None if args.no_cpu_baseline else _cpu_baseline(args.workload),
+        "vendor": vendor,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
@@ -472,6 +514,7 @@ def _matmul_main(args, rt, torch) -> int:
                      {"bound": res["bound"], "achieved": res["TFLOP/s"], "peak": res["peak_TFLOP/s"],
                       "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic}),
         "cpu_baseline": None if args.no_cpu_baseline else _matmul_cpu_baseline(),
+        "vendor": ({"op": "torch.matmul(A, B, out=C)", **res["torch_matmul"]} if "torch_matmul" in res else None),
         "extra": {},
     }
     print(json.dumps(line), flush=True)

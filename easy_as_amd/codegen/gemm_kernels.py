@@ -10,8 +10,8 @@ entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
 * ``<name>__pp`` (512 threads): the 8-wave ping-pong DMA body for A and B of the
   operand type whose rows the DMA takes.  Waves w and w+4 share a SIMD; the two groups of
   four waves alternate load phases and MFMA phases one barrier apart, each
-  wave holding 128 x 64 of the tile (4 x 2 ``v_mfma_f32_32x32x16_f16``
-  accumulators).
+  wave holding 128 x 64 of the tile (8 x 4 ``v_mfma_f32_16x16x32_f16``
+  accumulators; ``EAS_HIP_GEMM_MFMA=32`` selects 4 x 2 of ``32x32x16``).
 * ``<name>__t128`` (256 threads): the same DMA operands on 128 x 128 tiles (4
   waves of 64 x 64), for launches whose 256 x 256 grid would leave CUs idle.
 * ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
@@ -58,6 +58,8 @@ rectangle is proven to read, (K-1)*ldb + N, so tile-wide reads past it return 0.
 """
 
 from __future__ import annotations
+
+import os
 
 from ..ir import DType, IRModule
 from .gemm_lift import GemmSpec
@@ -333,7 +335,10 @@ static __device__ __forceinline__ void eas_gemm_dma(const eas_op_t* __restrict__
 // a SIMD runs MFMAs the other one loads.  Stage ring, LDS layout, swizzles and range checks are
 // the 4-wave DMA body's.  When K is not a multiple of 8, the A fragments of the tail stage are
 // masked to zero past K in registers (the last 16-byte chunk of a row reaches into the next row).
-template <typename CT, int K>
+// MI selects the MFMA: 32 (v_mfma_f32_32x32x16: each wave's 128 x 64 as 4 x 2 tiles of 32 x 32,
+// two k-steps of 16 per stage) or 16 (v_mfma_f32_16x16x32: 8 x 4 tiles of 16 x 16, one k-step of
+// 32 per stage; fewer accumulator bytes move through the MFMA per flop).  Same LDS reads per stage.
+template <typename CT, int K, int MI = 32>
 static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                    CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
                                                    eas_op_t* smem) {
@@ -398,20 +403,49 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
         fb_off[ks][j][h] = row * BN + chunk * 8 + (col & 7);
       }
   }
-  eas_h8 fa[2][4], fb[2][2];
+  // MI == 16: lane l holds A[row 16 i + l%16][k 8(l/16)..+7] and B[k 8(l/16)..+7][col 16 j + l%16]
+  int fa16_off[8], fb16_off[4][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = g * 128 + i * 16 + (lane & 15);
+    fa16_off[i] = r * BK + (((lane >> 4) ^ ((r >> 2) & 3)) * 8);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int gq = lane >> 4, kq = lane & 15;
+      const int row = 8 * gq + 4 * h + (kq >> 2);
+      const int col = p * 64 + j * 16 + 4 * (kq & 3);
+      const int chunk = (col >> 3) ^ (4 * (row & 3));
+      fb16_off[j][h] = row * BN + chunk * 8 + (col & 7);
+    }
+  eas_h8 fa[2][4], fb[2][2], fa16[8], fb16[4];
   auto read_a = [&](int s, int ks, int i) { fa[ks][i] = *(const eas_h8*)(As + s * STAGE_H + fa_off[ks][i]); };
-  auto read_b = [&](int s, int ks, int j) {
-    const eas_op_t* bs = Bs + s * STAGE_H;
-    const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
-    const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
+  auto read_tr = [&](const eas_op_t* bs, int o0, int o1) {
+    const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + o0));
+    const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + o1));
     const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
-    fb[ks][j] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+    return (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
   };
+  auto read_b = [&](int s, int ks, int j) {
+    fb[ks][j] = read_tr(Bs + s * STAGE_H, fb_off[ks][j][0], fb_off[ks][j][1]);
+  };
+  auto read_a16 = [&](int s, int i) { fa16[i] = *(const eas_h8*)(As + s * STAGE_H + fa16_off[i]); };
+  auto read_b16 = [&](int s, int j) { fb16[j] = read_tr(Bs + s * STAGE_H, fb16_off[j][0], fb16_off[j][1]); };
   eas_f32x16 acc[4][2];
+  eas_f32x4 acc16[8][4];
+  if constexpr (MI == 32) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
+      for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc16[i][j] = (eas_f32x4){};
+  }
   // this wave's loads of the awaited stage are done; `later` newer stages (4 loads each) may stay in flight
   auto wait_stage = [&](int later) {
     if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
@@ -441,21 +475,34 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if (issue) dma_one(kt + NSTAGE - 1, u);
-      read_a(s, u >> 1, 2 * (u & 1));
-      read_a(s, u >> 1, 2 * (u & 1) + 1);
-      read_b(s, u >> 1, u & 1);
+      if constexpr (MI == 32) {
+        read_a(s, u >> 1, 2 * (u & 1));
+        read_a(s, u >> 1, 2 * (u & 1) + 1);
+        read_b(s, u >> 1, u & 1);
+      } else {
+        read_a16(s, 2 * u);
+        read_a16(s, 2 * u + 1);
+        read_b16(s, u);
+      }
     }
     if (g == 1 && kt + 1 < KT) wait_stage(later);
     if constexpr (K % 8 != 0) {
       if (kt == KT - 1) {  // tail stage: halves at k >= K hold the next row of A
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int e = 0; e < 8; ++e) {
+          if constexpr (MI == 32) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const bool past = kt * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
+            for (int ks = 0; ks < 2; ++ks) {
+              const bool past = kt * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) fa[ks][i][e] = past ? (eas_op_t)0.0f : fa[ks][i][e];
+              for (int i = 0; i < 4; ++i) fa[ks][i][e] = past ? (eas_op_t)0.0f : fa[ks][i][e];
+            }
+          } else {
+            const bool past = kt * BK + 8 * (lane >> 4) + e >= K;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) fa16[i][e] = past ? (eas_op_t)0.0f : fa16[i][e];
           }
+        }
       }
     }
     __builtin_amdgcn_s_waitcnt(EAS_WAITLGKM0);
@@ -463,29 +510,50 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     // MFMA phase
+    if constexpr (MI == 32) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = EAS_MFMA32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < 2; ++j) acc[i][j] = EAS_MFMA32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc16[i][j] = EAS_MFMA16(fa16[i], fb16[j], acc16[i][j], 0, 0, 0);
+    }
     if (g == 0 && kt + 1 < KT) wait_stage(later);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
   }
   if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier
   const bool full = (m0 + BM <= M) && (n0 + BN <= N);
-  // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
+  if constexpr (MI == 32) {
+    // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + g * 128 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
-        const int col = n0 + p * 64 + j * 32 + (lane & 31);
-        if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + g * 128 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
+          const int col = n0 + p * 64 + j * 32 + (lane & 31);
+          if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
+        }
+  } else {
+    // lane l, register r of a 16x16 tile holds (row 4*(l/16) + r, col l%16)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + g * 128 + i * 16 + (lane >> 4) * 4 + r;
+          const int col = n0 + p * 64 + j * 16 + (lane & 15);
+          if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc16[i][j][r];
+        }
+  }
 }
 
 // Guard body of the 8-wave and 128-tile entries for inputs the DMA cannot take (the launch plan
@@ -1000,7 +1068,7 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__pp(
   int m0, n0;
   eas_tile_origin(M, N, m0, n0);
   if (dma_ok)
-    eas_gemm_pp<CT, K>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
+    eas_gemm_pp<CT, K, @PP_MI@>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
   else
     eas_gemm_elementwise<AT, BT, CT, K>(A, B, C, ldb, M, N, m0, n0);
 }
@@ -1295,6 +1363,13 @@ THREADS = 256
 PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
 SKINNY_M = 128  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
+# MFMA shape of the 8-wave entry's body: 16 (v_mfma_f32_16x16x32, the default) or 32
+# (v_mfma_f32_32x32x16).  Measured on MI355X with random inputs, where the part runs
+# power-limited: 16 x 16 x 32 is 2.5-5 % faster (4096³ f16 1172-1181 -> 1219-1222 TFLOP/s,
+# 8192³ 1271-1277 -> 1331-1335), since it moves fewer accumulator bytes per flop.
+PP_MFMA = int(os.environ.get("EAS_HIP_GEMM_MFMA", "16") or 16)
+if PP_MFMA not in (16, 32):
+    raise ValueError(f"EAS_HIP_GEMM_MFMA must be 16 or 32, got {PP_MFMA}")
 
 
 def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
@@ -1330,6 +1405,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "@B@": pname[spec.b],
         "@C@": pname[spec.c],
         "@LDB@": pname[spec.n_sym],
+        "@PP_MI@": str(PP_MFMA),
     }
     src = _DMA_HELPERS + (_TEMPLATE_F32 + _TEMPLATE_F32_T128 if spec.f32 else _OP_TYPES[spec.op_dtype] + _TEMPLATE)
     pingpong = op_in and not spec.f32 and spec.K % 2 == 0  # odd K: rows of A are not 4-byte aligned

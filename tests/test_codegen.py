@@ -197,6 +197,22 @@ def test_mma_kernel_lowers_to_mfma():
     ck = K.matmul_mma_kernel.compile(_h(64 * 64), _h(64 * 64), _f(64 * 64), 64, 64, BM=32, BN=32, BK=8, K=64,
                                      NT=512)
     assert "__builtin_amdgcn_mfma_f32_32x32x16_f16" in ck.src
+    # the 8-wave entry's body runs 16 x 16 x 32 MFMAs unless EAS_HIP_GEMM_MFMA=32 asks otherwise
+    assert "__builtin_amdgcn_mfma_f32_16x16x32_f16" in ck.src
+    assert "eas_gemm_pp<CT, K, 16>" in ck.src
+
+
+def test_pp_mfma_switch_is_validated():
+    import subprocess
+    import sys
+
+    code = "import easy_as_amd.codegen.gemm_kernels as g; print(g.PP_MFMA)"
+    env = {**__import__("os").environ, "EAS_HIP_GEMM_MFMA": "32"}
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "32"
+    env["EAS_HIP_GEMM_MFMA"] = "8"
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
+    assert r.returncode != 0 and "EAS_HIP_GEMM_MFMA must be 16 or 32" in r.stderr
 
 
 def _sources() -> list[tuple[str, str]]:
