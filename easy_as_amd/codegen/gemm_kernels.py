@@ -352,7 +352,10 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
   const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
   const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
   // DMA instruction q = 2 wave + i writes 1 KB of a stage.  A: rows 16q + lane/4, chunk lane%4
-  // stored at chunk ^ ((row/4)%4).  B: rows (k) 2q + lane/32, chunk lane%32 stored at chunk ^ 4(row%4).
+  // stored at chunk ^ ((row/4)%4).  B: rows (k) 2q + lane/32, chunk lane%32 stored at chunk ^ bsw(row):
+  // bits 2-3 of the mask spread the four rows of a transposing read over the banks, bit 1 keeps
+  // rows 8 apart (the two 16-lane groups of a half-wave in the 16 x 16 x 32 mapping) apart.
+  auto bsw = [](int row) { return (4 * (row & 3)) ^ (2 * ((row >> 3) & 1)); };
   uint32_t a_off[2], b_off[2];
   int a_k[2], b_k[2];
 #pragma unroll
@@ -363,7 +366,7 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
     a_off[i] = ((uint32_t)(m0 + r_a) * (uint32_t)K + (uint32_t)(c_a * 8)) * 2u;
     a_k[i] = c_a * 8;
     const int r_b = 2 * q + (lane >> 5);
-    const int c_b = (lane & 31) ^ (4 * (r_b & 3));
+    const int c_b = (lane & 31) ^ bsw(r_b);
     b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
     b_k[i] = r_b;
   }
@@ -399,7 +402,7 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
         const int gq = lane >> 4, kq = lane & 15;
         const int row = 16 * ks + 8 * (gq >> 1) + 4 * h + (kq >> 2);
         const int col = p * 64 + j * 32 + 16 * (gq & 1) + 4 * (kq & 3);
-        const int chunk = (col >> 3) ^ (4 * (row & 3));
+        const int chunk = (col >> 3) ^ bsw(row);
         fb_off[ks][j][h] = row * BN + chunk * 8 + (col & 7);
       }
   }
@@ -417,7 +420,7 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
       const int gq = lane >> 4, kq = lane & 15;
       const int row = 8 * gq + 4 * h + (kq >> 2);
       const int col = p * 64 + j * 16 + 4 * (kq & 3);
-      const int chunk = (col >> 3) ^ (4 * (row & 3));
+      const int chunk = (col >> 3) ^ bsw(row);
       fb16_off[j][h] = row * BN + chunk * 8 + (col & 7);
     }
   eas_h8 fa[2][4], fb[2][2], fa16[8], fb16[4];
