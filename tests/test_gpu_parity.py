@@ -17,6 +17,7 @@ import pytest
 
 import eas
 import kernels as K
+from eas import mk
 from conftest import seeded_normal
 from oracle import interp, ops
 
@@ -428,6 +429,56 @@ def test_launches_follow_torch_current_stream(gpu_runtime):
     want = ops.add_f32(a_np, b_np)
     assert _bits_equal(c.cpu().numpy(), want)
     assert _bits_equal(d.cpu().numpy(), want)
+
+
+_TUNE_BLOCKS = (64, 256, 1024)
+
+
+@eas.autotune(configs=[eas.Config(meta={"BLOCK": b}) for b in _TUNE_BLOCKS], key=["N"], warmup=1, repeat=3)
+@eas.kernel
+def _tuned_add_hip(a, b, c, N, BLOCK: eas.constexpr = 64):
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.arange(0, BLOCK)
+    mask = offs < N
+    mk.store(c, offs, mk.load(a, offs, mask) + mk.load(b, offs, mask), mask)
+
+
+class _CountingRuntime:
+    """The HIP runtime, with every benchmark() call recorded and its timing checked."""
+
+    def __init__(self, rt):
+        self.rt, self.benchmarked = rt, []
+
+    def benchmark(self, ck, runtime_args, meta, **kw):
+        self.benchmarked.append(int(meta["BLOCK"]))
+        t = self.rt.benchmark(ck, runtime_args, meta, **kw)
+        assert 0.0 < t < 1.0
+        return t
+
+    def __getattr__(self, name):
+        return getattr(self.rt, name)
+
+
+def test_autotune_on_hip_times_each_config_once_per_key(gpu_runtime, monkeypatch):
+    """@eas.autotune with real HIP-event timings (eas/autotune.py:9-57, eas/kernel.py:73-127):
+    each config is benchmarked once per key value, the chosen config runs and is cached, and the
+    result is the bit-exact sum whichever BLOCK won."""
+    import importlib
+
+    eas_kernel = importlib.import_module("easy_as_amd.kernel")
+    rt = _CountingRuntime(gpu_runtime)
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    for n in (1 << 20, 4099):
+        a_np, b_np = seeded_normal(0, n), seeded_normal(1, n)
+        a, b = eas.tensor(a_np, device="hip"), eas.tensor(b_np, device="hip")
+        for _ in range(2):
+            c = eas.tensor(np.full(n, np.nan, np.float32), device="hip")
+            _tuned_add_hip(a, b, c, n)
+            gpu_runtime.synchronize()
+            assert _bits_equal(c.numpy(), ops.add_f32(a_np, b_np))
+    assert sorted(rt.benchmarked) == sorted(2 * _TUNE_BLOCKS)
+    assert len(_tuned_add_hip._tuned_cache) == 2
+    assert {int(cfg.meta["BLOCK"]) for cfg in _tuned_add_hip._tuned_cache.values()} <= set(_TUNE_BLOCKS)
 
 
 def test_benchmark_returns_positive_seconds(gpu_runtime):
