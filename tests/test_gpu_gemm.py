@@ -258,3 +258,51 @@ def test_dma_entry_guard_for_an_operand_it_cannot_see(gpu_runtime, monkeypatch, 
         _mma(K.matmul_mma_kernel, a_arg, tb, tc, m, n, k)
         torch.cuda.synchronize()
         _check(tc.cpu().numpy(), a, b, m, n, k)
+
+
+# The configurations' own shapes and distributions, every output element checked.  The reference is
+# a float64 matmul of the same (f16/bf16-rounded) operands, computed by torch on the GPU so that
+# the 8192^3 case stays fast; tolerances as above: max|C - R| / max|R| <= 1e-5 sqrt(K) with an f32
+# output, <= 2e-3 with an f16 output (one rounding of the f32 accumulator to 11 significant bits).
+_BASELINE_SHAPES = [
+    # (kernel, M, N, K, operand dtype, A distribution, B distribution, f16 output)
+    ("matmul_mma_kernel", 4096, 4096, 4096, "f16", "u", "u", False),
+    ("matmul_mma_kernel", 4096, 4096, 4100, "f16", "u", "u", False),
+    ("matmul_mma_bf16_kernel", 4096, 4096, 4096, "bf16", "u", "u", False),
+    ("matmul_mma_f16out_kernel", 16, 14336, 4096, "f16", "n1", "n02", True),
+    ("matmul_mma_f16out_kernel", 8192, 8192, 8192, "f16", "n1", "n02", True),
+    ("matmul_tiled_kernel", 1024, 1024, 1024, "f32", "ns", "ns", False),
+    ("matmul_tiled_kernel", 2048, 2048, 2048, "f32", "ns", "ns", False),
+]
+
+
+@pytest.mark.parametrize("case", _BASELINE_SHAPES, ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}x{c[3]}")
+def test_baseline_shapes_every_output_vs_float64(gpu_runtime, case):
+    import torch
+
+    kname, m, n, k, op, da, db, out16 = case
+    gen = torch.Generator(device="cuda").manual_seed(m + 3 * n + 7 * k)
+    dt = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[op]
+
+    def draw(dist, numel):
+        if dist == "u":  # U(-1, 1)
+            x = torch.rand(numel, generator=gen, device="cuda", dtype=torch.float32) * 2 - 1
+        else:  # N(0, 1), N(0, 0.02), or N(0, 1) / sqrt(K) for the fp32 tiled matmul
+            x = torch.randn(numel, generator=gen, device="cuda", dtype=torch.float32)
+            x = x * {"n1": 1.0, "n02": 0.02, "ns": 1.0 / math.sqrt(k)}[dist]
+        return x.to(dt)
+
+    a, b = draw(da, m * k), draw(db, k * n)
+    c = torch.full((m * n,), float("nan"), device="cuda", dtype=torch.float16 if out16 else torch.float32)
+    kern = getattr(K, kname)
+    if kname == "matmul_tiled_kernel":
+        kern(a, b, c, m, n, 0, 0, BM=32, BN=32, BK=32, K=k, NT=256, _grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1),
+             _tptg=(256, 1, 1))
+    else:
+        _mma(kern, a, b, c, m, n, k)
+    torch.cuda.synchronize()
+    ref = a.double().reshape(m, k) @ b.double().reshape(k, n)
+    got = c.double().reshape(m, n)
+    assert bool(torch.isfinite(got).all())
+    err = float((got - ref).abs().max() / ref.abs().max())
+    assert err <= (2e-3 if out16 else 1e-5 * math.sqrt(k)), err
