@@ -468,6 +468,7 @@ def test_autotune_on_hip_times_each_config_once_per_key(gpu_runtime, monkeypatch
     eas_kernel = importlib.import_module("easy_as_amd.kernel")
     rt = _CountingRuntime(gpu_runtime)
     monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    _tuned_add_hip._tuned_cache.clear()  # the choice is per process; start from none
     for n in (1 << 20, 4099):
         a_np, b_np = seeded_normal(0, n), seeded_normal(1, n)
         a, b = eas.tensor(a_np, device="hip"), eas.tensor(b_np, device="hip")
