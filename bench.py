@@ -8,8 +8,10 @@ then exactly K steps between device synchronisations.
 
 Prints ONE JSON line: the driver's fields plus ``roofline`` (achieved HBM GB/s
 of the kernel from HIP events on its launch stream, vs 8 TB/s) and
-``cpu_baseline`` (the oracle's C restatement of the same arithmetic, one core,
-on a bounded sample).  ``vendor`` times the same operation through torch (ROCm:
+``cpu_baseline``: the reference's own CPU expression for the workload (the NumPy
+expressions its tests compute expected values with: ``np.add(a, b, out=c)``,
+``a*b+c``, ``A32 @ B32``, ``A16.astype(np.float32) @ B16.astype(np.float32)``)
+timed on this host's cores on the same arrays, with the host described.  ``vendor`` times the same operation through torch (ROCm:
 ``torch.add``, hipBLASLt/rocBLAS ``torch.matmul``) on the same device-resident
 inputs, in the same run, with the same event method; each matmul entry under
 ``extra`` carries its ``torch_matmul``.  Secondary measurements ride along under
@@ -93,9 +95,40 @@ def _inputs(n: int, seeds: tuple[int, ...]) -> list[np.ndarray]:
 EVENT_TRIALS = 5
 
 
+SETTLE_BATCH = 10
+SETTLE_MAX_LAUNCHES = 400
+SETTLE_LOG: list[dict] = []
+
+
+def _settle_until_stable(batch_seconds, label: str) -> int:
+    """Untimed launches until the device's clocks have settled: after any idle gap (0.2 s is
+    enough) the GPU runs an HBM-bound launch fast for ~3 launches, then up to ~30 % slower for
+    ~20 more while its power management ramps, then steadily.  ``batch_seconds()`` runs
+    SETTLE_BATCH launches and returns their event time; batches run until two in a row agree
+    within 2 % (at most SETTLE_MAX_LAUNCHES launches).  None of them is part of any
+    reported time; the count is logged in the output line."""
+    prev, n = None, 0
+    while n < SETTLE_MAX_LAUNCHES:
+        t = batch_seconds()
+        n += SETTLE_BATCH
+        if prev is not None and n >= 3 * SETTLE_BATCH and abs(t - prev) <= 0.02 * min(t, prev):
+            break
+        prev = t
+    SETTLE_LOG.append({"kernel": label, "launches": n})
+    return n
+
+
+def _settle(rt, ck, rargs, meta, **launch) -> int:
+    label = ck.geometry.entry if ck.geometry is not None else ck.ir.name
+    return _settle_until_stable(lambda: rt.benchmark(ck, rargs, meta, repeat=SETTLE_BATCH, warmup=0, **launch),
+                                label)
+
+
 def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch, **launch) -> tuple[float, float]:
     """(wall ms/step bracketed by device syncs, HIP-event ms/launch on the launch stream: the
-    median of EVENT_TRIALS trials of ``steps`` back-to-back launches)."""
+    median of EVENT_TRIALS trials of ``steps`` back-to-back launches).  The device is settled
+    first (``_settle``), then ``warmup`` untimed steps run, then the ``steps`` timed ones."""
+    _settle(rt, ck, rargs, meta, **launch)
     for _ in range(warmup):
         rt.run(ck, rargs, meta, sync=False, **launch)
     rt.synchronize()
@@ -112,7 +145,19 @@ def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch, **launch) 
 
 def _torch_event_ms(fn, steps: int, warmup: int, torch) -> float:
     """ms per call of a torch operation on torch's current stream: the median of EVENT_TRIALS
-    trials of ``steps`` back-to-back calls between torch events (the vendor comparison)."""
+    trials of ``steps`` back-to-back calls between torch events (the vendor comparison), after
+    the same settling as the eas kernels."""
+
+    def batch() -> float:
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(SETTLE_BATCH):
+            fn()
+        t1.record()
+        t1.synchronize()
+        return t0.elapsed_time(t1) * 1e-3
+
+    _settle_until_stable(batch, "torch")
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -152,8 +197,9 @@ def _matmul_inputs(name: str, torch) -> tuple[object, object]:
 MATMUL_DATA = ("seeded", "zeros", "ones", "signs")
 
 
-def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded") -> dict:
-    """Time one matmul configuration and check a seeded sample of its rows against float64."""
+def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded", cpu_baseline: bool = False) -> dict:
+    """Time one matmul configuration and check a seeded sample of its rows against float64;
+    with ``cpu_baseline``, also time the reference's CPU expression on the same operands."""
     import kernels as K
 
     kname, m, n, k, _, _, desc = MATMULS[name]
@@ -237,53 +283,123 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded")
                                "out_dtype": str(a.dtype).replace("torch.", "")}
         _log(f"{name}: torch.matmul {res['torch_matmul']['TFLOP/s']} TFLOP/s, {tms:.4f} ms/launch")
         del out_t
+    if cpu_baseline and data == "seeded":
+        res["cpu_baseline"] = _matmul_cpu_baseline(name, ha, hb, m, n, k)
+        _log(f"{name}: cpu baseline {res['cpu_baseline']['value']} TFLOP/s ({res['cpu_baseline']['cores']} threads)")
     del a, b, c
     torch.cuda.empty_cache()
     return res
 
 
-def _matmul_cpu_baseline(seconds: float = 10.0) -> dict:
-    """The oracle's float64 matmul (numpy) on 512^3 samples of the f16 inputs, one BLAS thread."""
+def _host_info() -> dict:
+    """The CPU side of the GPU box: core counts, model, NumPy and its BLAS."""
+    import os
+    import subprocess
+
+    info: dict = {"os_cpu_count": os.cpu_count(), "numpy": np.__version__,
+                  "OPENBLAS_NUM_THREADS": os.environ.get("OPENBLAS_NUM_THREADS"),
+                  "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core"):
+                info[key.strip()] = val.strip()
+    except Exception as e:  # noqa: BLE001
+        info["lscpu"] = f"unavailable: {type(e).__name__}"
+    try:
+        from threadpoolctl import threadpool_info
+
+        info["blas"] = [f"{p.get('internal_api')} {p.get('version')} ({p.get('architecture')})"
+                        for p in threadpool_info() if p.get("user_api") == "blas"]
+    except Exception as e:  # noqa: BLE001
+        info["blas"] = f"unavailable: {type(e).__name__}"
+    return info
+
+
+def _cpu_threads() -> int:
+    """BLAS threads for the matmul baselines: os.cpu_count(), capped at the box's CPU share
+    (the GPU box exports OMP_NUM_THREADS for the cores it gives one GPU's job)."""
+    import os
+
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return min(os.cpu_count() or 1, share) if share > 0 else (os.cpu_count() or 1)
+
+
+def _median_seconds(fn, warmup: int, repeat: int) -> float:
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(repeat):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _matmul_cpu_baseline(name: str, ha, hb, m: int, n: int, k: int) -> dict:
+    """The reference's CPU expression for this configuration, timed on this host: ``A32 @ B32``
+    for the fp32 tiled matmuls (tests/test_matmul_tiled.py:172) and
+    ``A16.astype(np.float32) @ B16.astype(np.float32)`` for the f16 (and bf16) MMA matmuls
+    (examples/matmul_simdgroup.py:219-222), NumPy/OpenBLAS with the BLAS thread count set."""
     from threadpoolctl import threadpool_limits
 
+    threads = _cpu_threads()
+    a2, b2 = np.asarray(ha).reshape(m, k), np.asarray(hb).reshape(k, n)
+    tiled = name.startswith("tiled")
+    if tiled:
+        expr = "A32 @ B32"
+        fn = lambda: a2 @ b2  # noqa: E731
+    else:
+        expr = "A16.astype(np.float32) @ B16.astype(np.float32)"
+        fn = lambda: a2.astype(np.float32) @ b2.astype(np.float32)  # noqa: E731
+    one_run = 2.0 * m * n * k >= 1e12
+    with threadpool_limits(threads):
+        s = _median_seconds(fn, 1 if one_run else 3, 1 if one_run else 5)
+    return {"value": round(2.0 * m * n * k / s / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+            "sample": f"the reference's CPU expression {expr} (NumPy {np.__version__}, OpenBLAS, {threads} threads) "
+                      f"at the full {m}x{n}x{k} shape on the configuration's inputs, "
+                      + ("one timed run after one warmup" if one_run else "median of 5 runs after 3 warmups")
+                      + f": {s:.3f} s per matmul"}
+
+
+def _cpu_baseline(workload: str, hosts: list[np.ndarray]) -> dict:
+    """The reference's CPU expression for the elementwise workload on the configuration's own
+    arrays (N = 2^28), timed on this host: ``np.add(a, b, out=c)`` (tests/test_add.py:38,
+    tests/test_tensor.py:59) and NumPy ``a*b+c`` as ``np.multiply(a, b, out=t); np.add(t, c,
+    out=d)`` (tests/test_fma.py:75; two roundings, so it is a timing baseline, not the fma
+    oracle).  NumPy ufuncs run on one thread.  The oracle's C restatement (the fma checker) is
+    timed beside it on a 2^26 sample."""
     from oracle import ops
 
-    rng = np.random.default_rng(0)
-    a = rng.uniform(-1, 1, (512, 512)).astype(np.float16)
-    b = rng.uniform(-1, 1, (512, 512)).astype(np.float16)
-    with threadpool_limits(1):
-        ops.matmul_ref(a, b)
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            ops.matmul_ref(a, b)
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= seconds or reps >= 2000:
-                break
-    return {"value": round(2 * 512 ** 3 * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"oracle matmul_ref (numpy float64, 1 BLAS thread) on 512x512x512 f16 inputs, {reps} reps, {el:.1f} s"}
-
-
-def _cpu_baseline(workload: str, seconds: float = 10.0) -> dict:
-    from oracle import ops
-
-    n = 1 << 26
-    a, b, c = _inputs(n, (0, 1, 2))
-    fn = {"add": lambda: ops.add_f32(a, b), "fma": lambda: ops.fmaf(a, b, c), "copy": lambda: a.copy(),
-          "read": lambda: float(a.sum()), "write": lambda: c.fill(1.0)}[workload]
+    n = hosts[0].size if hosts else N_ELEM
+    out = np.empty(n, np.float32)
+    tmp = np.empty(n, np.float32) if workload == "fma" else None
+    a = hosts[0] if hosts else out
+    fns = {"add": (lambda: np.add(hosts[0], hosts[1], out=out), "np.add(a, b, out=c)"),
+           "fma": (lambda: (np.multiply(hosts[0], hosts[1], out=tmp), np.add(tmp, hosts[2], out=out)),
+                   "np.multiply(a, b, out=t); np.add(t, c, out=d)"),
+           "copy": (lambda: np.copyto(out, a), "np.copyto(c, a)"),
+           "read": (lambda: float(a.sum()), "a.sum()"),
+           "write": (lambda: out.fill(1.0), "c.fill(1.0)")}
+    fn, expr = fns[workload]
+    s = _median_seconds(fn, 3, 5)
     per = WORKLOADS[workload][2]
-    fn()
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        fn()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or reps >= 200:
-            break
-    what = {"add": "add_f32", "fma": "fmaf", "copy": "numpy copy", "read": "numpy sum", "write": "numpy fill"}[workload]
-    return {"value": round(per * n * reps / el / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"oracle {what} (oracle/fmaf.c, gcc -O2, 1 thread) over N=2^26 float32, {reps} reps, {el:.1f} s"}
+    res = {"value": round(per * n / s / 1e9, 2), "unit": "GB/s", "cores": 1, "kind": "reference",
+           "sample": f"the reference's CPU expression {expr} (NumPy {np.__version__}, one thread) on the "
+                     f"configuration's own N=2^28 float32 arrays, median of 5 runs after 3 warmups: "
+                     f"{s * 1e3:.1f} ms per pass",
+           "host": _host_info()}
+    if workload in ("add", "fma"):
+        m = 1 << 26
+        sa, sb, sc = (x[:m] for x in (hosts + hosts)[:3])
+        ofn = (lambda: ops.add_f32(sa, sb)) if workload == "add" else (lambda: ops.fmaf(sa, sb, sc))
+        so = _median_seconds(ofn, 1, 5)
+        res["oracle_port"] = {"value": round(per * m / so / 1e9, 2), "unit": "GB/s", "cores": 1,
+                              "sample": f"oracle {'add_f32' if workload == 'add' else 'fmaf'} (oracle/fmaf.c, "
+                                        f"gcc -O2, one thread) on the first 2^26 elements, median of 5"}
+    del out, tmp
+    return res
 
 
 def _expected(workload: str, hosts: list[np.ndarray]) -> np.ndarray | None:
@@ -343,23 +459,49 @@ def main() -> int:
     if args.workload in MATMULS:
         return _matmul_main(args, rt, torch)
     kname, nin, per_elem = WORKLOADS[args.workload]
-    kern = getattr(K, kname)
     _log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}; generating inputs N=2^28")
-    hosts = _inputs(N_ELEM, tuple(range(nin)))
+    nin_all = 3 if args.workload == "add" and not args.no_extra else nin
+    hosts = _inputs(N_ELEM, tuple(range(nin_all)))
     ins = [torch.from_numpy(h).to(dev) for h in hosts]
     out = torch.zeros(N_ELEM, dtype=torch.float32, device=dev)
-    names = list(kern.sig.parameters)[: nin + 1]
-    rargs = dict(zip(names, ins + [out]))
-    rargs["N"] = N_ELEM
 
-    def measure(block: int) -> tuple[float, float]:
-        ck = kern.compile(*ins, out, N_ELEM, BLOCK=block)
+    def elementwise(workload: str, block: int) -> dict:
+        """Time one elementwise configuration, then check every one of its 2^28 outputs."""
+        kn, k_in, per = WORKLOADS[workload]
+        kern = getattr(K, kn)
+        names = list(kern.sig.parameters)[: k_in + 1]
+        rargs = dict(zip(names, ins[:k_in] + [out]))
+        rargs["N"] = N_ELEM
+        ck = kern.compile(*ins[:k_in], out, N_ELEM, BLOCK=block)
         wall_ms, ev_ms = _time_kernel(rt, ck, rargs, {"BLOCK": block}, args.steps, args.warmup, torch)
-        _log(f"{args.workload} BLOCK={block}: wall {wall_ms:.4f} ms/step, event {ev_ms:.4f} ms/launch, "
-             f"{per_elem * N_ELEM / ev_ms / 1e6:.1f} GB/s")
-        return wall_ms, ev_ms
+        # NaN marks outputs a kernel failed to write; the read kernel writes none, so its
+        # output must stay as filled (zeros)
+        out.fill_(0.0 if workload == "read" else float("nan"))
+        kern(*ins[:k_in], out, N_ELEM, BLOCK=block)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        want = _expected(workload, hosts)
+        if want is not None:
+            exact = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+            parity = "bit-exact vs binary32 closed form (all 2^28 outputs)" if exact else "MISMATCH"
+        elif not args.no_cpu_baseline:
+            exact = _fma_check(got, hosts)
+            parity = "bit-exact vs oracle fmaf (all 2^28 outputs)" if exact else "MISMATCH"
+        else:
+            exact, parity = True, "not checked (--no-cpu-baseline skips the oracle)"
+        geo = ck.geometry
+        res = {"wall_ms": wall_ms, "ev_ms": ev_ms, "GB/s": round(per * N_ELEM / ev_ms / 1e6, 1),
+               "frac": round(per * N_ELEM / ev_ms / 1e6 / HBM_PEAK_GBS, 4), "ms_per_launch": round(ev_ms, 5),
+               "parity": parity, "parity_ok": exact,
+               "launch": f"{geo.wg_size} threads per workgroup, "
+                         + (f"{geo.split} workgroups per program" if geo.split > 1
+                            else f"{geo.programs_per_wg} program(s) per workgroup")}
+        _log(f"{workload} BLOCK={block}: wall {wall_ms:.4f} ms/step, event {ev_ms:.4f} ms/launch, "
+             f"{res['GB/s']} GB/s, {res['launch']}, parity {parity}")
+        return res
 
-    wall_ms, ev_ms = measure(args.block)
+    prim = elementwise(args.workload, args.block)
+    wall_ms, ev_ms, exact, parity = prim["wall_ms"], prim["ev_ms"], prim["parity_ok"], prim["parity"]
     # vendor comparison on the same device-resident inputs: the torch (ROCm) operation
     tfn = {"add": lambda: torch.add(ins[0], ins[1], out=out),
            "fma": lambda: torch.addcmul(ins[2], ins[0], ins[1], out=out),
@@ -371,39 +513,16 @@ def main() -> int:
     _log(f"{texpr}: {tms:.4f} ms/launch, {vendor['GB/s']} GB/s")
     extra: dict = {}
     if not args.no_extra and args.workload == "add":
+        # configs[1] in full: add at the other BLOCK and fma at both, each timed and checked
         other = 1024 if args.block != 1024 else 256
-        extra[f"add_block{other}_gbs"] = round(per_elem * N_ELEM / measure(other)[1] / 1e6, 1)
-
-    # parity of the measured configuration over every output element
-    kern(*ins, out, N_ELEM, BLOCK=args.block)
-    torch.cuda.synchronize()
-    got = out.cpu().numpy()
-    want = _expected(args.workload, hosts)
-    if want is not None:
-        exact = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
-        parity = "bit-exact vs binary32 closed form (all 2^28 outputs)" if exact else "MISMATCH"
-    elif not args.no_cpu_baseline:
-        exact = _fma_check(got, hosts)
-        parity = "bit-exact vs oracle fmaf (all 2^28 outputs)" if exact else "MISMATCH"
-    else:
-        exact, parity = True, "not checked (--no-cpu-baseline skips the oracle)"
-    _log(f"parity over all 2^28 outputs: {parity}")
-
-    if not args.no_extra and args.workload == "add":
-        fh = _inputs(N_ELEM, (2,))[0]
-        cc = torch.from_numpy(fh).to(dev)
-        d = torch.empty_like(out)
-        fargs = {"a": ins[0], "b": ins[1], "c": cc, "d": d, "N": N_ELEM}
-        ckf = K.fma_kernel.compile(ins[0], ins[1], cc, d, N_ELEM, BLOCK=args.block)
-        _, fe = _time_kernel(rt, ckf, fargs, {"BLOCK": args.block}, args.steps, args.warmup, torch)
-        if args.no_cpu_baseline:
-            fparity = "not checked (--no-cpu-baseline skips the oracle)"
-        else:
-            fparity = "bit-exact vs oracle fmaf" if _fma_check(d.cpu().numpy(), [hosts[0], hosts[1], fh]) else "MISMATCH"
-        extra["fma_n2e28"] = {"GB/s": round(16 * N_ELEM / fe / 1e6, 1), "frac": round(16 * N_ELEM / fe / 1e6 / HBM_PEAK_GBS, 4),
-                              "parity": fparity}
-        _log(f"fma: event {fe:.4f} ms/launch, {16 * N_ELEM / fe / 1e6:.1f} GB/s, parity {extra['fma_n2e28']['parity']}")
-        del cc, d
+        for wl, blk in (("add", other), ("fma", 256), ("fma", 1024)):
+            r = elementwise(wl, blk)
+            extra[f"{wl}_block{blk}"] = {k: v for k, v in r.items() if k not in ("wall_ms", "ev_ms", "parity_ok")}
+            exact = exact and r["parity_ok"]
+        cpu_fma = None if args.no_cpu_baseline else _cpu_baseline("fma", hosts)
+        if cpu_fma is not None:
+            cpu_fma.pop("host", None)
+            extra["fma_block256"]["cpu_baseline"] = cpu_fma
 
     if not args.no_extra and args.workload == "add":
         # the plumbing sizes, launch-latency bound.  us_per_call is a whole eas call
@@ -439,7 +558,8 @@ def main() -> int:
         for name in ("mma", "mma_k4100", "mma_bf16", "decode", "prefill", "tiled1024", "tiled2048"):
             # a failing extra is reported in the line; it does not take the primary measurement with it
             try:
-                extra[name] = _matmul(name, rt, torch, max(5, min(args.steps, 20)), max(2, min(args.warmup, 5)))
+                extra[name] = _matmul(name, rt, torch, max(5, min(args.steps, 20)), max(2, min(args.warmup, 5)),
+                                      cpu_baseline=not args.no_cpu_baseline)
             except Exception as e:  # noqa: BLE001
                 _log(f"{name}: {type(e).__name__}: {e}")
                 extra[name] = {"error": f"{type(e).__name__}: {e}"}
@@ -474,8 +594,10 @@ def main() -> int:
         "parity": parity,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
-        "cpu_baseline": None if args.no_cpu_baseline else _cpu_baseline(args.workload),
+        "cpu_baseline": None if args.no_cpu_baseline else _cpu_baseline(args.workload, hosts[:nin]),
         "vendor": vendor,
+        "settle": {"untimed_launches_before_warmup": list(SETTLE_LOG),
+                   "rule": f"batches of {SETTLE_BATCH} until two agree within 2%"},
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
@@ -483,7 +605,8 @@ def main() -> int:
 
 
 def _matmul_main(args, rt, torch) -> int:
-    res = _matmul(args.workload, rt, torch, args.steps, args.warmup, args.data)
+    res = _matmul(args.workload, rt, torch, args.steps, args.warmup, args.data,
+                  cpu_baseline=not args.no_cpu_baseline)
     _, m, n, k, _, _, desc = MATMULS[args.workload]
     traffic = None
     pmc = ROOT / "profiles" / f"{MATMUL_PROFILES.get(args.workload, args.workload)}.pmc.json"
@@ -513,8 +636,10 @@ def _matmul_main(args, rt, torch) -> int:
                       "frac": res["frac_of_bound"], "traffic": traffic} if res["bound"] == "hbm" else
                      {"bound": res["bound"], "achieved": res["TFLOP/s"], "peak": res["peak_TFLOP/s"],
                       "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic}),
-        "cpu_baseline": None if args.no_cpu_baseline else _matmul_cpu_baseline(),
+        "cpu_baseline": (dict(res["cpu_baseline"], host=_host_info()) if "cpu_baseline" in res else None),
         "vendor": ({"op": "torch.matmul(A, B, out=C)", **res["torch_matmul"]} if "torch_matmul" in res else None),
+        "settle": {"untimed_launches_before_warmup": list(SETTLE_LOG),
+                   "rule": f"batches of {SETTLE_BATCH} until two agree within 2%"},
         "extra": {},
     }
     print(json.dumps(line), flush=True)

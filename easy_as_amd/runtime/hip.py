@@ -153,11 +153,9 @@ def plan_launch(
         return None
     geo = ck.geometry
     if geo.kind == "spmd":
-        per_wg = geo.programs_per_wg * geo.unroll
-        nblocks = _cdiv(groups[0], per_wg)
-        persist = int(geo.params.get("persistent_wg_per_cu", 0) or 0)
-        if persist:
-            nblocks = min(nblocks, persist * compute_units)
+        nblocks = _cdiv(groups[0], geo.programs_per_wg * geo.unroll) * geo.split
+        if nblocks * geo.wg_size >= 1 << 32:
+            raise ValueError(f"spmd launch of {groups[0]} programs exceeds 2^32 threads along x")
         return LaunchPlan((nblocks, groups[1], groups[2]), (geo.wg_size, 1, 1), (groups[0],))
     if geo.kind == "thread":
         live = live_x if live_x is not None else groups[0] * block

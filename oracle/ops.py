@@ -14,6 +14,10 @@ the ``cpu_baseline`` leg of ``bench.py`` as the checker; the product
                      FMA and correctly rounded sums: proved algorithms using
                      rounding to odd", IEEE TC 2008).  Used only to pin
                      ``fmaf``; the two must agree bit for bit.
+* ``mul_f16``, ``add_f16`` — binary16 arithmetic rounded once to binary16
+                     (MSL ``half`` operators, eas/codegen/msl.py:224-237).
+* ``fma_f16``      — the reference's f16 fma: fmaf in binary32, then binary16
+                     (eas/codegen/msl.py:291-294).
 * ``matmul_ref``   — float64 matmul reference (tests/test_matmul.py:55).
 * ``f32_to_bf16``  — binary32 -> bfloat16, round to nearest even, as 16-bit
                      patterns; ``bf16_to_f32`` widens them back (exact).
@@ -104,6 +108,36 @@ def fmaf_rto(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
         toward = np.where(e > 0, np.inf, -np.inf)
         s = np.where(fix, np.nextafter(s, toward), s)
         return s.astype(np.float32)  # results past the binary32 range become inf
+
+
+def _f16(x: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(x, dtype=np.float16)
+
+
+def mul_f16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """binary16 ``a * b`` rounded once to binary16 (MSL ``half * half``, eas/codegen/msl.py:224-237).
+    The binary32 product of two binary16 values is exact (11 + 11 significant bits fit in
+    24), so converting it to binary16 (RNE) is the single rounding."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (_f16(a).astype(np.float32) * _f16(b).astype(np.float32)).astype(np.float16)
+
+
+def add_f16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """binary16 ``a + b`` rounded to binary16 (MSL ``half + half``, eas/codegen/msl.py:224-237):
+    the binary32 sum, then binary16.  Rounding twice is innocuous for addition here
+    because binary32's 24 bits are at least 2 * 11 + 2 (Figueroa, SIGNUM 1995)."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (_f16(a).astype(np.float32) + _f16(b).astype(np.float32)).astype(np.float16)
+
+
+def fma_f16(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """The reference's f16 fma, ``half(fma((float)x, (float)y, (float)z))``
+    (eas/codegen/msl.py:291-294): the exact ``a*b+c`` rounded once to binary32, then
+    to binary16.  This double rounding is the reference's definition and can differ
+    from rounding the exact value to binary16 once (the oracle tests hold a case)."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        return fmaf(_f16(a).astype(np.float32), _f16(b).astype(np.float32),
+                    _f16(c).astype(np.float32)).astype(np.float16)
 
 
 def dot_f32(a: np.ndarray, b: np.ndarray) -> np.float32:

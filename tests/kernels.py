@@ -90,6 +90,17 @@ def spmd_tg_rotate_kernel(a, out, N, BLOCK: eas.constexpr):
     mk.store(out, offs, mk.load(tg, (lanes + 1) % BLOCK), mask)
 
 
+@eas.kernel
+def add_first_lane_kernel(a, b, c, first, N, BLOCK: eas.constexpr):
+    """c = a + b, and first[p] = a[p*BLOCK] + b[p*BLOCK] for each program p: a
+    program-uniform load and store next to the lane streams (one store per program)."""
+    pid = mk.program_id(0)
+    offs = pid * BLOCK + mk.arange(0, BLOCK)
+    mask = offs < N
+    mk.store(c, offs, mk.load(a, offs, mask) + mk.load(b, offs, mask), mask)
+    mk.store(first, pid, mk.load(a, pid * BLOCK) + mk.load(b, pid * BLOCK))
+
+
 # -- thread mode -----------------------------------------------------------------
 
 

@@ -143,7 +143,7 @@ def test_matmul_fma_chain_has_no_per_load_branches():
     m, n, k = 32, 64, 8
     ck = matmul_with_fma.compile(_f(m * k), _f(k * n), _f(m * n), m, n, BLOCK=32, K=k)
     src = ck.src
-    assert src.count("__builtin_fmaf(") == k
+    assert src.split('extern "C"', 1)[1].count("__builtin_fmaf(") == k
     assert re.search(r"\bif \(!v\d+\) return;", src)
     assert not re.search(r"\bif \(v\d+\) \{", src)
     lines = src.split("\n")
@@ -237,6 +237,41 @@ def test_emitted_source_compiles_for_gfx950(name, src):
     code = mod.compile_to_code(src, f"{name}.hip", list(COMPILE_OPTIONS))
     assert code[:4] == b"\x7fELF"
 
+
+
+_OBJDUMP = "/opt/rocm/lib/llvm/bin/llvm-objdump"
+
+
+@pytest.mark.parametrize("spmd", [False, True])
+def test_f16_fma_keeps_two_roundings_in_the_code_object(tmp_path, spmd):
+    # half(fma((float)x, (float)y, (float)z)) rounds twice; LLVM would otherwise merge the
+    # f32 fma and the narrowing into v_fma_mixlo_f16, which rounds the exact value once
+    import os
+    import subprocess
+
+    from easy_as_amd.runtime.hip import COMPILE_OPTIONS
+    from easy_as_amd.runtime.hip_ext import load_hip_ext
+
+    if not os.path.exists(_OBJDUMP):
+        pytest.skip("llvm-objdump not installed")
+
+    @eas.kernel
+    def spmd_fma_f16(a, b, c, d, N, BLOCK: eas.constexpr):
+        offs = mk.program_id(0) * BLOCK + mk.arange(0, BLOCK)
+        m = offs < N
+        mk.store(d, offs, mk.fma(mk.load(a, offs, m), mk.load(b, offs, m), mk.load(c, offs, m)), m)
+
+    h = _h(256)
+    kern = spmd_fma_f16 if spmd else K.explicit_fma_kernel
+    ck = kern.compile(h, h, h, h.copy(), 256, BLOCK=256)
+    assert "eas_fma_f16(" in ck.src
+    code = load_hip_ext(require=True).compile_to_code(ck.src, "fma_f16.hip", list(COMPILE_OPTIONS))
+    path = tmp_path / "k.co"
+    path.write_bytes(code)
+    asm = subprocess.run([_OBJDUMP, "-d", "--mcpu=gfx950", str(path)], capture_output=True, text=True,
+                         check=True).stdout
+    assert "v_fma_mixlo_f16" not in asm and "v_fma_mixhi_f16" not in asm
+    assert "v_cvt_f16_f32" in asm
 
 # ---- bfloat16 (an addition to the reference's dtypes) ---------------------------
 

@@ -134,18 +134,107 @@ def test_spmd_lanes_exchange_through_threadgroup_memory(gpu_runtime):
     assert _bits_equal(out, ref)
 
 
-def test_nontemporal_and_unrolled_spmd_variants(gpu_runtime, monkeypatch):
-    n = (1 << 16) + 5
-    a, b = seeded_normal(0, n), seeded_normal(1, n)
-    for env in ({"EAS_HIP_SPMD_NT": "1"}, {"EAS_HIP_SPMD_UNROLL": "4"}, {"EAS_HIP_SPMD_LPT": "16"}):
-        for k, v in env.items():
-            monkeypatch.setenv(k, v)
-        kern = eas.kernel(K.add_kernel.fn)
-        c = np.zeros(n, np.float32)
-        kern(a, b, c, n, BLOCK=1024)
-        assert _bits_equal(c, ops.add_f32(a, b)), env
-        for k in env:
-            monkeypatch.delenv(k)
+_SPMD_ENVS = [{}, {"EAS_HIP_SPMD_WG": "32"}, {"EAS_HIP_SPMD_WG": "64"}, {"EAS_HIP_SPMD_WG": "256"},
+              {"EAS_HIP_SPMD_WG": "1024"}, {"EAS_HIP_SPMD_NT": "0"}, {"EAS_HIP_SPMD_UNROLL": "4"},
+              {"EAS_HIP_SPMD_LPT": "16"}, {"EAS_HIP_SPMD_LPT": "16", "EAS_HIP_SPMD_WG": "32"}]
+
+
+@pytest.mark.parametrize("env", _SPMD_ENVS, ids=lambda e: ",".join(f"{k.replace('EAS_HIP_SPMD_', '')}={v}" for k, v in e.items()) or "default")
+@pytest.mark.parametrize("block", [256, 1024])
+def test_spmd_emitter_variants_bit_exact(gpu_runtime, monkeypatch, env, block):
+    # every SPMD mapping the emitter can take (workgroup size, split programs, unroll, lanes per
+    # thread, plain or nontemporal accesses) on odd sizes, against the oracle
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    n = (1 << 16) + 5 * block + 3
+    a, b, c = seeded_normal(0, n), seeded_normal(1, n), seeded_normal(2, n)
+    add, fma, copy, fill = (eas.kernel(k.fn) for k in (K.add_kernel, K.fma_kernel, K.copy_kernel, K.fill_kernel))
+    first_k, rot = eas.kernel(K.add_first_lane_kernel.fn), eas.kernel(K.spmd_tg_rotate_kernel.fn)
+    out = np.full(n, np.nan, np.float32)
+    add(a, b, out, n, BLOCK=block)
+    assert _bits_equal(out, ops.add_f32(a, b)), env
+    out = np.full(n, np.nan, np.float32)
+    fma(a, b, c, out, n, BLOCK=block)
+    assert _bits_equal(out, ops.fmaf(a, b, c)), env
+    out = np.full(n + 7, 5.0, np.float32)
+    copy(a, out, n, BLOCK=block)
+    assert _bits_equal(out[:n], a) and np.all(out[n:] == 5.0), env
+    out = np.full(n + 7, 5.0, np.float32)
+    fill(out, n, BLOCK=block)
+    assert np.all(out[:n] == 1.0) and np.all(out[n:] == 5.0), env
+    progs = -(-n // block)
+    out, first = np.full(n, np.nan, np.float32), np.full(progs + 3, 9.0, np.float32)
+    first_k(a, b, out, first, n, BLOCK=block)
+    assert _bits_equal(out, ops.add_f32(a, b)), env
+    assert _bits_equal(first[:progs], ops.add_f32(a[::block], b[::block])) and np.all(first[progs:] == 9.0), env
+    out = np.full(n, np.nan, np.float32)
+    rot(a, out, n, BLOCK=block)
+    padded = np.zeros(progs * block, np.float32)
+    padded[:n] = a
+    assert _bits_equal(out, np.roll(padded.reshape(progs, block), -1, axis=1).reshape(-1)[:n]), env
+
+
+@pytest.fixture(scope="module")
+def inputs_n2e28():
+    """a, b, c ~ N(0,1) float32 from seeds 0, 1, 2, N = 2^28 (1 GiB each)."""
+    n = 1 << 28
+    return n, seeded_normal(0, n), seeded_normal(1, n), seeded_normal(2, n)
+
+
+@pytest.mark.parametrize("block", [256, 1024])
+def test_add_and_fma_n2e28_every_output_bit_exact(gpu_runtime, inputs_n2e28, block):
+    """configs[1] at its own size on device-resident torch tensors: every one of the 2^28
+    outputs of c = a + b and d = a*b + c (one fused rounding) against the oracle."""
+    import torch
+
+    n, a, b, c = inputs_n2e28
+    dev = torch.device("cuda:0")
+    ta, tb, tc = (torch.from_numpy(x).to(dev) for x in (a, b, c))
+    out = torch.full((n,), float("nan"), dtype=torch.float32, device=dev)
+    K.add_kernel(ta, tb, out, n, BLOCK=block)
+    torch.cuda.synchronize()
+    assert _bits_equal(out.cpu().numpy(), ops.add_f32(a, b))
+    out.fill_(float("nan"))
+    K.fma_kernel(ta, tb, tc, out, n, BLOCK=block)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    step = 1 << 26
+    for s in range(0, n, step):
+        assert _bits_equal(got[s:s + step], ops.fmaf(a[s:s + step], b[s:s + step], c[s:s + step])), s
+    del ta, tb, tc, out
+    torch.cuda.empty_cache()
+
+
+def _f16_triples(n: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Seeded f16 operands with frequent cancellation, plus the triple on which the
+    reference's half(fma(float...)) and a single rounding of the exact value differ."""
+    a, b = seeded_normal(0, n, np.float16), seeded_normal(1, n, np.float16)
+    c = seeded_normal(2, n, np.float16)
+    c[::3] = (-(a[::3].astype(np.float32) * b[::3].astype(np.float32)) * np.float32(1.0009765625)).astype(np.float16)
+    a[0], b[0], c[0] = np.float16(1044 * 2.0 ** -10), np.float16(2009 * 2.0 ** -22), np.float16(1.0)
+    return a, b, c
+
+
+@pytest.mark.parametrize("kern", ["fma_kernel", "simple_fma_kernel"])
+def test_f16_mul_then_add_rounds_twice_in_f16(gpu_runtime, kern):
+    # on f16 values the fusion pass does not apply (eas/compiler.py:1019-1096 fuses f32 only):
+    # the product is rounded to f16, then the sum
+    n = 4099
+    a, b, c = _f16_triples(n)
+    d = np.zeros(n, np.float16)
+    getattr(K, kern)(a, b, c, d, n, BLOCK=256)
+    assert _bits_equal(d, ops.add_f16(ops.mul_f16(a, b), c))
+    assert d[0] == np.float16(1.0)
+
+
+def test_f16_explicit_fma_is_half_of_fmaf(gpu_runtime):
+    # mk.fma on f16 values: half(fma((float)x, (float)y, (float)z)) (eas/codegen/msl.py:291-294)
+    n = 4099
+    a, b, c = _f16_triples(n)
+    d = np.zeros(n, np.float16)
+    K.explicit_fma_kernel(a, b, c, d, n, BLOCK=256)
+    assert _bits_equal(d, ops.fma_f16(a, b, c))
+    assert d[0] == np.float16(1.0)  # the double-rounding witness
 
 
 # -- thread mode / index known answers -----------------------------------------------

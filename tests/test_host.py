@@ -163,17 +163,47 @@ def _add_ck(block=256):
     return K.add_kernel.compile(z, z, z, 1031, BLOCK=block)
 
 
-def test_plan_spmd_add_packs_programs():
-    ck = _add_ck()
+@pytest.mark.parametrize("block", [256, 1024])
+def test_plan_spmd_add_splits_programs(block):
+    # c = a + b reads two streams and writes one: 512 bytes of each stream per workgroup
+    # (32 threads of 16 bytes), so one BLOCK-lane program spans BLOCK/128 workgroups
+    ck = _add_ck(block)
     n = 1 << 28
     plan = plan_launch(ck, {"N": n})
     geo = ck.geometry
-    programs = -(-n // 256)
+    programs = -(-n // block)
+    assert geo.wg_size == 32 and geo.programs_per_wg == 1 and geo.split == block // 128
     assert plan.hidden == (programs,)
-    assert plan.grid == (-(-programs // (geo.programs_per_wg * geo.unroll)), 1, 1)
-    assert plan.block == (geo.wg_size, 1, 1)
-    # the workgroup's lanes cover its programs' BLOCK elements exactly
-    assert (256 * geo.programs_per_wg) % geo.wg_size == 0
+    assert plan.grid == (programs * geo.split, 1, 1)
+    assert plan.block == (32, 1, 1)
+    # the split workgroups' lanes cover the program's BLOCK elements exactly
+    assert geo.split * geo.wg_size * geo.params["lanes_per_thread"] == block
+
+
+def test_spmd_workgroup_size_follows_stream_count():
+    z = np.zeros(1, np.float32)
+    shapes = {name: getattr(K, name).compile(*args, BLOCK=256).geometry for name, args in (
+        ("fill_kernel", (z, 1)), ("copy_kernel", (z, z, 1)), ("add_kernel", (z, z, z, 1)),
+        ("fma_kernel", (z, z, z, z, 1)), ("read_kernel", (z, z, 1)), ("spmd_tg_rotate_kernel", (z, z, 1)))}
+    # bytes per stream per workgroup: 4 KiB (one stream), 1 KiB (two), 512 B (three or more)
+    assert (shapes["fill_kernel"].wg_size, shapes["fill_kernel"].programs_per_wg) == (256, 4)
+    assert (shapes["copy_kernel"].wg_size, shapes["copy_kernel"].split) == (64, 1)
+    assert (shapes["add_kernel"].wg_size, shapes["add_kernel"].split) == (32, 2)
+    assert (shapes["fma_kernel"].wg_size, shapes["fma_kernel"].split) == (32, 2)
+    # no dense output stream: 64 bytes per thread, 256 threads
+    assert shapes["read_kernel"].wg_size == 256
+    # threadgroup memory keeps a program in one workgroup
+    assert shapes["spmd_tg_rotate_kernel"].split == 1
+
+
+def test_spmd_workgroup_override_is_validated(monkeypatch):
+    z = np.zeros(1, np.float32)
+    monkeypatch.setenv("EAS_HIP_SPMD_WG", "1024")
+    geo = eas.kernel(K.add_kernel.fn).compile(z, z, z, 1, BLOCK=256).geometry
+    assert (geo.wg_size, geo.programs_per_wg, geo.split) == (1024, 16, 1)
+    monkeypatch.setenv("EAS_HIP_SPMD_WG", "96")
+    with pytest.raises(ValueError, match="EAS_HIP_SPMD_WG"):
+        eas.kernel(K.add_kernel.fn).compile(z, z, z, 1, BLOCK=256)
 
 
 def test_plan_zero_extent_and_tptg_rules():

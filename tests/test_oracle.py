@@ -257,6 +257,23 @@ def test_interp_tptg_independent_arange_and_tg_copy():
     assert np.array_equal(_bits(out), _bits(a))
 
 
+@pytest.mark.parametrize("n,block", [(1000, 256), (256, 256), (3000, 1024), (1, 128)])
+def test_interp_spmd_threadgroup_rotate_closed_form(n, block):
+    # the kernel's own statement: out[p*BLOCK + l] = a'[p*BLOCK + (l+1) % BLOCK], a' = a with 0 past N;
+    # written with numpy index arithmetic, independently of the interpreter
+    a = np.random.default_rng(14).standard_normal(n, dtype=np.float32)
+    out = interp.run_kernel(K.spmd_tg_rotate_kernel, a, np.full(n, np.nan, np.float32), n, BLOCK=block)["out"]
+    progs = -(-n // block)
+    padded = np.zeros(progs * block, np.float32)
+    padded[:n] = a
+    want = np.roll(padded.reshape(progs, block), -1, axis=1).reshape(-1)[:n]
+    assert np.array_equal(_bits(out), _bits(want))
+    if n > 2:
+        # a planted off-by-one (rotation the other way) is told apart
+        wrong = np.roll(padded.reshape(progs, block), 1, axis=1).reshape(-1)[:n]
+        assert not np.array_equal(_bits(wrong), _bits(want))
+
+
 def test_interp_masked_tail_leaves_outside_untouched():
     a = np.ones(1031, np.float32)
     res = interp.run_kernel(K.add_kernel, a, a, np.full(1100, 7.0, np.float32), 1031, BLOCK=256)["c"]
@@ -385,3 +402,96 @@ def test_add_bf16_is_the_correctly_rounded_exact_sum():
     fa, fb = ops.bf16_to_f32(a), ops.bf16_to_f32(b)
     want = np.array([_bf16_of_rational(Fraction(float(x)) + Fraction(float(y))) for x, y in zip(fa, fb)], np.uint16)
     assert np.array_equal(got, want)
+
+
+# ---- binary16 arithmetic (mul, add, the reference's f16 fma) ------------------------
+
+def _f16_of_rational(q) -> np.float16:
+    """Round the exact rational ``q`` to binary16, nearest even, from the definition: 11
+    significant bits, exponents down to -14 (subnormal spacing 2^-24), infinity from the
+    halfway point above the largest finite value (65504 + 16) on."""
+    from fractions import Fraction
+
+    q = Fraction(q)
+    if q == 0:
+        return np.float16(0.0)
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    if a >= 65520:
+        return np.float16(sign * np.inf)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    e = max(e, -14)
+    ulp = Fraction(2) ** (e - 10)
+    r = round(a / ulp) * ulp  # Fraction rounds half to even
+    return np.float16(sign * float(r))
+
+
+def _f16_probe_pairs(n: int, seed: int) -> tuple[np.ndarray, np.ndarray]:
+    """Random finite binary16 bit patterns (every exponent, subnormals included)."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(0, 1 << 16, (2, n * 2), dtype=np.uint32).astype(np.uint16).view(np.float16)
+    fin = np.isfinite(x[0]) & np.isfinite(x[1])
+    return x[0][fin][:n], x[1][fin][:n]
+
+
+def _f16_bits(x) -> np.ndarray:
+    x = np.asarray(x, np.float16).copy()
+    x[np.isnan(x)] = np.float16(np.nan)
+    return x.view(np.uint16)
+
+
+def test_f16_mul_and_add_round_once():
+    from fractions import Fraction
+
+    a, b = _f16_probe_pairs(3000, 15)
+    prod, summ = ops.mul_f16(a, b), ops.add_f16(a, b)
+    want_p = [_f16_of_rational(Fraction(float(x)) * Fraction(float(y))) for x, y in zip(a, b)]
+    want_s = [_f16_of_rational(Fraction(float(x)) + Fraction(float(y))) for x, y in zip(a, b)]
+    # the sign of an exact zero result is not part of this check (compare values for zeros)
+    for got, want in ((prod, want_p), (summ, want_s)):
+        want = np.array(want, np.float16)
+        nz = want != 0
+        assert np.array_equal(_f16_bits(got[nz]), _f16_bits(want[nz]))
+        assert np.all(got[~nz] == 0)
+
+
+def test_f16_fma_is_fmaf_then_binary16():
+    from fractions import Fraction
+
+    a, b = _f16_probe_pairs(1500, 16)
+    c, _ = _f16_probe_pairs(1500, 17)
+    # magnitudes near a*b make cancellation (and so rounding at low exponents) frequent
+    with np.errstate(over="ignore"):
+        c[::2] = (-(a[::2].astype(np.float32) * b[::2].astype(np.float32)) * np.float32(1.001)).astype(np.float16)
+    ok = np.isfinite(c)
+    a, b, c = a[ok], b[ok], c[ok]
+    got = ops.fma_f16(a, b, c)
+    for i in range(a.size):
+        exact = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        r32 = _round_f32(exact)
+        want = np.float16(np.inf if np.isinf(r32) else 0.0) if not np.isfinite(r32) else \
+            _f16_of_rational(Fraction(float(r32)))
+        if want == 0:
+            assert got[i] == 0, (a[i], b[i], c[i])
+        else:
+            assert _f16_bits(got[i]) == _f16_bits(want), (a[i], b[i], c[i])
+
+
+def test_f16_fma_double_rounding_witness():
+    # a*b + c = 1 + 2^-11 + 244 * 2^-32: just above the binary16 midpoint between 1 and
+    # 1 + 2^-10.  Rounded to binary32 first it becomes the midpoint itself, which binary16
+    # rounds to even (1.0); rounded once it goes up.  The reference's half(fma(float...))
+    # gives 1.0, so an oracle that rounded the exact value once would fail here.
+    from fractions import Fraction
+
+    a = np.array([1044 * 2.0 ** -10], np.float16)
+    b = np.array([2009 * 2.0 ** -22], np.float16)
+    c = np.array([1.0], np.float16)
+    exact = Fraction(1044, 2 ** 10) * Fraction(2009, 2 ** 22) + 1
+    assert exact - 1 - Fraction(1, 2 ** 11) == Fraction(244, 2 ** 32)
+    assert ops.fma_f16(a, b, c)[0] == np.float16(1.0)
+    assert _f16_of_rational(exact) == np.float16(1 + 2.0 ** -10)
+    # unfused f16 (mul rounded to binary16, then add): a third answer
+    assert ops.add_f16(ops.mul_f16(a, b), c)[0] == np.float16(1.0)
