@@ -1370,9 +1370,12 @@ SKINNY_N = 64
 # (v_mfma_f32_32x32x16).  Measured on MI355X with random inputs, where the part runs
 # power-limited: 16 x 16 x 32 is 2.5-5 % faster (4096³ f16 1172-1181 -> 1219-1222 TFLOP/s,
 # 8192³ 1271-1277 -> 1331-1335), since it moves fewer accumulator bytes per flop.
-PP_MFMA = int(os.environ.get("EAS_HIP_GEMM_MFMA", "16") or 16)
-if PP_MFMA not in (16, 32):
-    raise ValueError(f"EAS_HIP_GEMM_MFMA must be 16 or 32, got {PP_MFMA}")
+def pp_mfma() -> int:
+    """``EAS_HIP_GEMM_MFMA``: 16 (default) or 32, read each time a GEMM source is emitted."""
+    v = os.environ.get("EAS_HIP_GEMM_MFMA", "16").strip() or "16"
+    if v not in ("16", "32"):
+        raise ValueError(f"EAS_HIP_GEMM_MFMA must be 16 or 32, got {v!r}")
+    return int(v)
 
 
 def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
@@ -1408,7 +1411,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "@B@": pname[spec.b],
         "@C@": pname[spec.c],
         "@LDB@": pname[spec.n_sym],
-        "@PP_MI@": str(PP_MFMA),
+        "@PP_MI@": str(pp_mfma()),
     }
     src = _DMA_HELPERS + (_TEMPLATE_F32 + _TEMPLATE_F32_T128 if spec.f32 else _OP_TYPES[spec.op_dtype] + _TEMPLATE)
     pingpong = op_in and not spec.f32 and spec.K % 2 == 0  # odd K: rows of A are not 4-byte aligned

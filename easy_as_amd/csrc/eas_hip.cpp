@@ -37,6 +37,7 @@ struct eas_hip_kernel {
   hipModule_t module;
   hipFunction_t function;
   int device;
+  eas_hip_launch_shape shape;  // kind EAS_HIP_KIND_RAW until set
 };
 
 namespace {
@@ -385,13 +386,6 @@ int eas_hip_copy_d2d(void* dst, const void* src, size_t nbytes) {
   return EAS_HIP_OK;
 }
 
-int eas_hip_memset(void* dst, int value, size_t nbytes, void* stream) {
-  if (!nbytes) return EAS_HIP_OK;
-  if (!dst) return fail(EAS_HIP_ERR_INVALID, "NULL pointer in memset");
-  HIP_TRY(hipMemsetAsync(dst, value, nbytes, static_cast<hipStream_t>(stream)));
-  return EAS_HIP_OK;
-}
-
 static int launch_n(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],
                     const uint32_t block[3], uint32_t dynamic_lds, void* stream, int n) {
   if (!k || !grid || !block) return fail(EAS_HIP_ERR_INVALID, "kernel/grid/block must not be NULL");
@@ -417,16 +411,201 @@ static int launch_n(const eas_hip_kernel* k, const void* kernarg, size_t kernarg
   return EAS_HIP_OK;
 }
 
+// ---- launch shapes -----------------------------------------------------------
+
+static int check_shape(const eas_hip_launch_shape* s) {
+  if (!s) return fail(EAS_HIP_ERR_INVALID, "launch shape must not be NULL");
+  if (s->kind < EAS_HIP_KIND_RAW || s->kind > EAS_HIP_KIND_GEMM) return fail(EAS_HIP_ERR_INVALID, "unknown launch kind %d", s->kind);
+  if (s->hidden > EAS_HIP_MAX_HIDDEN) return fail(EAS_HIP_ERR_INVALID, "too many hidden arguments: %u", s->hidden);
+  if (s->kind == EAS_HIP_KIND_RAW) return EAS_HIP_OK;
+  if (s->block_size == 0 || s->wg_size == 0 || s->wg_size > 1024 || s->programs_per_wg == 0 || s->split == 0)
+    return fail(EAS_HIP_ERR_INVALID, "launch shape has a zero or oversized dimension");
+  if ((s->kind == EAS_HIP_KIND_SPMD || s->kind == EAS_HIP_KIND_THREAD) && s->hidden != 1)
+    return fail(EAS_HIP_ERR_INVALID, "spmd and thread kernels take exactly one hidden extent");
+  if (s->kind == EAS_HIP_KIND_THREAD && s->wg_size != s->block_size)
+    return fail(EAS_HIP_ERR_INVALID, "a thread-mode kernel's workgroup is its BLOCK");
+  return EAS_HIP_OK;
+}
+
+int eas_hip_launch_shape_parse(const char* src, eas_hip_launch_shape* out) {
+  if (!src || !out) return fail(EAS_HIP_ERR_INVALID, "src/out must not be NULL");
+  const char* tag = "// eas-launch:";
+  const char* p = strstr(src, tag);
+  if (!p) return fail(EAS_HIP_ERR_INVALID, "source has no '%s' line", tag);
+  p += strlen(tag);
+  const char* end = strchr(p, '\n');
+  std::string line(p, end ? (size_t)(end - p) : strlen(p));
+  eas_hip_launch_shape s{};
+  s.programs_per_wg = 1;
+  s.split = 1;
+  bool have_kind = false;
+  size_t pos = 0;
+  while (pos < line.size()) {
+    while (pos < line.size() && line[pos] == ' ') ++pos;
+    size_t stop = line.find(' ', pos);
+    std::string item = line.substr(pos, stop == std::string::npos ? std::string::npos : stop - pos);
+    pos = stop == std::string::npos ? line.size() : stop;
+    if (item.empty()) continue;
+    size_t eq = item.find('=');
+    if (eq == std::string::npos) return fail(EAS_HIP_ERR_INVALID, "malformed eas-launch item '%s'", item.c_str());
+    std::string key = item.substr(0, eq), val = item.substr(eq + 1);
+    if (key == "kind") {
+      have_kind = true;
+      if (val == "spmd") s.kind = EAS_HIP_KIND_SPMD;
+      else if (val == "thread") s.kind = EAS_HIP_KIND_THREAD;
+      else if (val == "gemm") s.kind = EAS_HIP_KIND_GEMM;
+      else if (val == "raw") s.kind = EAS_HIP_KIND_RAW;
+      else return fail(EAS_HIP_ERR_INVALID, "unknown eas-launch kind '%s'", val.c_str());
+      continue;
+    }
+    char* e = nullptr;
+    unsigned long v = strtoul(val.c_str(), &e, 10);
+    if (val.empty() || *e || v > 0xFFFFFFFFul) return fail(EAS_HIP_ERR_INVALID, "bad eas-launch value '%s'", item.c_str());
+    if (key == "block") s.block_size = (uint32_t)v;
+    else if (key == "wg") s.wg_size = (uint32_t)v;
+    else if (key == "ppw") s.programs_per_wg = (uint32_t)v;
+    else if (key == "split") s.split = (uint32_t)v;
+    else if (key == "args") s.arg_bytes = (uint32_t)v;
+    else if (key == "hidden") s.hidden = (uint32_t)v;
+    else return fail(EAS_HIP_ERR_INVALID, "unknown eas-launch key '%s'", key.c_str());
+  }
+  if (!have_kind) return fail(EAS_HIP_ERR_INVALID, "eas-launch line has no kind");
+  int rc = check_shape(&s);
+  if (rc) return rc;
+  *out = s;
+  return EAS_HIP_OK;
+}
+
+int eas_hip_kernel_set_shape(eas_hip_kernel* k, const eas_hip_launch_shape* shape) {
+  if (!k) return fail(EAS_HIP_ERR_INVALID, "kernel must not be NULL");
+  int rc = check_shape(shape);
+  if (rc) return rc;
+  k->shape = *shape;
+  return EAS_HIP_OK;
+}
+
+int eas_hip_kernel_get_shape(const eas_hip_kernel* k, eas_hip_launch_shape* out) {
+  if (!k || !out) return fail(EAS_HIP_ERR_INVALID, "kernel/out must not be NULL");
+  *out = k->shape;
+  return EAS_HIP_OK;
+}
+
+int eas_hip_plan_dispatch(const eas_hip_launch_shape* s, int by_groups, const uint64_t size[3], const uint32_t tptg[3],
+                          uint32_t grid[3], uint32_t block[3], uint32_t* hidden, int max_hidden) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if (!size || !tptg || !grid || !block || (!hidden && s->hidden))
+    return fail(EAS_HIP_ERR_INVALID, "size/tptg/grid/block/hidden must not be NULL");
+  if (max_hidden < (int)s->hidden) return fail(EAS_HIP_ERR_INVALID, "hidden holds %d, the kernel needs %u", max_hidden, s->hidden);
+  if (s->kind == EAS_HIP_KIND_RAW)
+    return fail(EAS_HIP_ERR_INVALID, "the kernel's launch shape is unknown (a source without an eas-launch line): "
+                                     "launch it with workgroup counts (launch_groups / eas_hip_launch)");
+  if (s->kind == EAS_HIP_KIND_GEMM)
+    return fail(EAS_HIP_ERR_INVALID, "this kernel was lifted to an MFMA GEMM, whose workgroup grid and hidden extents "
+                                     "depend on M, N, K and its buffers: launch it through HipRuntime.run, or with the "
+                                     "entry, grid, block and hidden of plan_launch through launch_groups / eas_hip_launch");
+  const char* what = by_groups ? "threadgroups" : "threads_per_grid";
+  for (int i = 0; i < 3; ++i)
+    if (size[i] == 0) return fail(EAS_HIP_ERR_INVALID, "%s dims must be > 0", what);
+  const bool auto_tg = tptg[0] == 0 && tptg[1] == 0 && tptg[2] == 0;
+  if (s->kind == EAS_HIP_KIND_THREAD) {
+    if (!auto_tg && (tptg[0] != s->block_size || tptg[1] != 1 || tptg[2] != 1))
+      return fail(EAS_HIP_ERR_INVALID, "threads_per_threadgroup must be (%u, 1, 1) for this kernel, which was compiled "
+                                       "for BLOCK=%u threadgroups; got (%u, %u, %u)",
+                  s->block_size, s->block_size, tptg[0], tptg[1], tptg[2]);
+    uint64_t groups_x = by_groups ? size[0] : (size[0] + s->block_size - 1) / s->block_size;
+    uint64_t live = by_groups ? size[0] * s->block_size : size[0];
+    if (live > 0xFFFFFFFFull || groups_x * s->block_size > 0xFFFFFFFFull)
+      return fail(EAS_HIP_ERR_INVALID, "%s x exceeds 2^32 threads", what);
+    grid[0] = (uint32_t)groups_x;
+    hidden[0] = (uint32_t)live;
+  } else {
+    // SPMD: a Metal thread is a program; the reference dispatches them as threads with
+    // threadgroups of one (eas/runtime/metal.py:284-295), so both forms count programs
+    if (!auto_tg && (tptg[0] != 1 || tptg[1] != 1 || tptg[2] != 1))
+      return fail(EAS_HIP_ERR_INVALID, "threads_per_threadgroup must be (1, 1, 1) for an SPMD kernel (one program per "
+                                       "Metal thread); got (%u, %u, %u)", tptg[0], tptg[1], tptg[2]);
+    if (size[0] > 0xFFFFFFFFull) return fail(EAS_HIP_ERR_INVALID, "%s x exceeds 2^32 programs", what);
+    uint64_t groups_x = (size[0] + s->programs_per_wg - 1) / s->programs_per_wg * s->split;
+    if (groups_x * s->wg_size > 0xFFFFFFFFull) return fail(EAS_HIP_ERR_INVALID, "%s x exceeds 2^32 threads", what);
+    grid[0] = (uint32_t)groups_x;
+    hidden[0] = (uint32_t)size[0];
+  }
+  for (int i = 1; i < 3; ++i) {
+    if (size[i] > 0xFFFFFFFFull) return fail(EAS_HIP_ERR_INVALID, "%s dim %d too large", what, i);
+    grid[i] = (uint32_t)size[i];
+  }
+  block[0] = s->wg_size;
+  block[1] = block[2] = 1;
+  return EAS_HIP_OK;
+}
+
+// Size of the blob a launch of `k` must carry: its own arguments, padded to 4 bytes when
+// hidden u32 extents follow (0 when the shape does not record it).
+static size_t expected_kernarg(const eas_hip_launch_shape& s, bool with_hidden) {
+  if (!s.arg_bytes) return 0;
+  if (!with_hidden || !s.hidden) return s.arg_bytes;
+  return ((size_t)s.arg_bytes + 3) / 4 * 4 + 4 * (size_t)s.hidden;
+}
+
+// A workgroup-level launch carries the kernel's arguments and its hidden extents.
+static int check_group_blob(const eas_hip_kernel* k, size_t kernarg_size) {
+  if (!k) return EAS_HIP_OK;  // launch_n reports it
+  size_t want = expected_kernarg(k->shape, true);
+  if (want && kernarg_size != want)
+    return fail(EAS_HIP_ERR_INVALID, "kernel argument blob of %zu bytes does not match the kernel's parameters "
+                                     "(%u bytes of arguments, then %u hidden u32: %zu bytes)",
+                kernarg_size, k->shape.arg_bytes, k->shape.hidden, want);
+  return EAS_HIP_OK;
+}
+
 int eas_hip_launch(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],
                    const uint32_t block[3], uint32_t dynamic_lds, void* stream, int repeat) {
   if (repeat <= 0) return fail(EAS_HIP_ERR_INVALID, "repeat must be > 0");
+  int rc = check_group_blob(k, kernarg_size);
+  if (rc) return rc;
   return launch_n(k, kernarg, kernarg_size, grid, block, dynamic_lds, stream, repeat);
+}
+
+static int launch_reference(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, int by_groups,
+                            const uint64_t size[3], const uint32_t tptg[3], void* stream, int repeat) {
+  if (!k) return fail(EAS_HIP_ERR_INVALID, "kernel must not be NULL");
+  if (repeat <= 0) return fail(EAS_HIP_ERR_INVALID, "repeat must be > 0");
+  static const uint32_t kAuto[3] = {0, 0, 0};
+  uint32_t grid[3], block[3], hidden[EAS_HIP_MAX_HIDDEN];
+  int rc = eas_hip_plan_dispatch(&k->shape, by_groups, size, tptg ? tptg : kAuto, grid, block, hidden,
+                                 EAS_HIP_MAX_HIDDEN);
+  if (rc) return rc;
+  size_t want = expected_kernarg(k->shape, false);
+  if (want && kernarg_size != want)
+    return fail(EAS_HIP_ERR_INVALID, "kernel argument blob of %zu bytes does not match the kernel's %u bytes of "
+                                     "arguments (the hidden extents are appended by the launch)",
+                kernarg_size, k->shape.arg_bytes);
+  if (kernarg_size && !kernarg) return fail(EAS_HIP_ERR_INVALID, "kernarg is NULL with nonzero size");
+  std::vector<uint8_t> blob((kernarg_size + 3) / 4 * 4 + 4 * k->shape.hidden, 0);
+  if (kernarg_size) memcpy(blob.data(), kernarg, kernarg_size);
+  memcpy(blob.data() + (kernarg_size + 3) / 4 * 4, hidden, 4 * k->shape.hidden);
+  return launch_n(k, blob.data(), blob.size(), grid, block, 0, stream, repeat);
+}
+
+int eas_hip_launch_threads(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
+                           const uint64_t threads_per_grid[3], const uint32_t threads_per_threadgroup[3], void* stream,
+                           int repeat) {
+  return launch_reference(k, kernarg, kernarg_size, 0, threads_per_grid, threads_per_threadgroup, stream, repeat);
+}
+
+int eas_hip_launch_threadgroups(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
+                                const uint64_t threadgroups[3], const uint32_t threads_per_threadgroup[3], void* stream,
+                                int repeat) {
+  return launch_reference(k, kernarg, kernarg_size, 1, threadgroups, threads_per_threadgroup, stream, repeat);
 }
 
 int eas_hip_launch_timed(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],
                          const uint32_t block[3], uint32_t dynamic_lds, void* stream, int warmup, int repeat,
                          float* mean_ms) {
   if (repeat <= 0 || warmup < 0 || !mean_ms) return fail(EAS_HIP_ERR_INVALID, "repeat > 0, warmup >= 0, mean_ms required");
+  int crc = check_group_blob(k, kernarg_size);
+  if (crc) return crc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (warmup) {
     int rc = launch_n(k, kernarg, kernarg_size, grid, block, dynamic_lds, stream, warmup);

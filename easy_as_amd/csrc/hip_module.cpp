@@ -5,16 +5,18 @@
 // module (eas/runtime/metal_ext.py:22-33: is_available, compile, launch,
 // synchronize, alloc_buffer, copy_from_host, copy_to_host, dlpack_import,
 // dlpack_export, queue_synchronize) plus launch_async / launch_tg /
-// launch_tg_async, and the HIP-specific compile_to_code / load / launch_timed
-// / wrap_pointer / device_props / kernel_attrs.
+// launch_tg_async, and the HIP-specific compile_to_code / load / launch_groups
+// / launch_groups_async / launch_timed / wrap_pointer / device_props /
+// kernel_attrs / kernel_shape / launch_shape / plan_dispatch.
 //
 // Objects crossing into Python are PyCapsules:
 //   "eas._hip.kernel"  -> eas_hip_kernel*       (module unloaded on destruction)
 //   "eas._hip.buffer"  -> Buffer                (memory freed / DLPack deleter run)
 //   "eas._hip.pending" -> Pending               (event + keepalives of a launch)
-// Launches take workgroup counts: HIP has no non-uniform dispatchThreads, so the
-// Python runtime converts thread counts and passes the true extents as hidden
-// kernel arguments.
+// launch/launch_tg take the reference's thread and threadgroup counts and plan the
+// workgroups from the kernel's launch shape (the C ABI appends the hidden extents
+// that stand in for Metal's non-uniform dispatchThreads); launch_groups takes HIP
+// workgroups directly, as the Python runtime plans every launch itself.
 
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -341,31 +343,75 @@ PyObject* py_compiler_version(PyObject*, PyObject*) {
   return Py_BuildValue("(iis)", major, minor, path);
 }
 
-// load(code: bytes, name) -> kernel capsule
-PyObject* py_load(PyObject*, PyObject* args) {
+// Attach the launch shape on `src`'s eas-launch line to `k` (a source without one leaves the
+// kernel's shape unknown: it then runs only through launch_groups).
+int attach_shape(eas_hip_kernel* k, const char* src) {
+  if (!src || !strstr(src, "// eas-launch:")) return EAS_HIP_OK;
+  eas_hip_launch_shape s;
+  int rc = eas_hip_launch_shape_parse(src, &s);
+  return rc ? rc : eas_hip_kernel_set_shape(k, &s);
+}
+
+PyObject* new_kernel_capsule(eas_hip_kernel* k, const char* src) {
+  int rc = attach_shape(k, src);
+  if (rc) {
+    eas_hip_kernel_release(k);
+    return raise_status(rc);
+  }
+  PyObject* cap = PyCapsule_New(k, kKernelCap, kernel_destructor);
+  if (!cap) eas_hip_kernel_release(k);
+  return cap;
+}
+
+// load(code: bytes, name, src=None) -> kernel capsule; `src` (the source the code object was
+// compiled from) gives the kernel its launch shape.
+PyObject* py_load(PyObject*, PyObject* args, PyObject* kwargs) {
+  static const char* kw[] = {"code", "name", "src", nullptr};
   Py_buffer code;
   const char* name;
-  if (!PyArg_ParseTuple(args, "y*s", &code, &name)) return nullptr;
+  const char* src = nullptr;
+  if (!PyArg_ParseTupleAndKeywords(args, kwargs, "y*s|z", const_cast<char**>(kw), &code, &name, &src)) return nullptr;
   eas_hip_kernel* k = nullptr;
   int rc = eas_hip_kernel_load(code.buf, (size_t)code.len, name, &k);
   PyBuffer_Release(&code);
   if (rc) return raise_status(rc);
-  return PyCapsule_New(k, kKernelCap, kernel_destructor);
+  return new_kernel_capsule(k, src);
 }
 
 // compile(src, name, options=None) -> kernel capsule (reference: compile(msl, name))
+// The options `compile` uses when given none: gfx950, -O3, FMAs only where the IR has
+// them (no contraction), packed FP32 off.  Exposed as DEFAULT_OPTIONS; the Python
+// runtime's COMPILE_OPTIONS are the same list (checked by the tests).
+const char* const kDefaultOptions[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off",
+                                       "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+
+PyObject* default_options() {
+  const Py_ssize_t n = (Py_ssize_t)(sizeof(kDefaultOptions) / sizeof(kDefaultOptions[0]));
+  PyObject* t = PyTuple_New(n);
+  for (Py_ssize_t i = 0; t && i < n; ++i) PyTuple_SET_ITEM(t, i, PyUnicode_FromString(kDefaultOptions[i]));
+  return t;
+}
+
 PyObject* py_compile(PyObject* self, PyObject* args) {
   const char* src;
   const char* name;
   PyObject* opts = nullptr;
   if (!PyArg_ParseTuple(args, "ss|O", &src, &name, &opts)) return nullptr;
-  PyObject* code = py_compile_to_code(self, args);
+  PyObject* call = nullptr;
+  if (!opts || opts == Py_None) {
+    PyObject* defaults = default_options();
+    if (!defaults) return nullptr;
+    call = Py_BuildValue("(ssN)", src, name, defaults);
+    if (!call) return nullptr;
+  }
+  PyObject* code = py_compile_to_code(self, call ? call : args);
+  Py_XDECREF(call);
   if (!code) return nullptr;
   eas_hip_kernel* k = nullptr;
   int rc = eas_hip_kernel_load(PyBytes_AS_STRING(code), (size_t)PyBytes_GET_SIZE(code), name, &k);
   Py_DECREF(code);
   if (rc) return raise_status(rc);
-  return PyCapsule_New(k, kKernelCap, kernel_destructor);
+  return new_kernel_capsule(k, src);
 }
 
 PyObject* py_kernel_attrs(PyObject*, PyObject* args) {
@@ -506,52 +552,163 @@ PyObject* py_copy_buffer(PyObject*, PyObject* args) {
   Py_RETURN_NONE;
 }
 
+// ---- launches ------------------------------------------------------------------
+//
+// Three argument forms over one implementation:
+//   launch / launch_async (reference: _metal.mm:1013-1222, 1381-1383):
+//       (kernel, argv, writable, threads_per_grid, threads_per_threadgroup=None, repeat=1, *, stream=None)
+//   launch_tg / launch_tg_async (reference: _metal.mm:1232-1379):
+//       (kernel, argv, writable, threadgroups, threads_per_threadgroup, repeat=1, *, stream=None)
+//   launch_groups / launch_groups_async (HIP workgroups; argv ends with the hidden extents):
+//       (kernel, argv, writable, grid, block, repeat=1, lds=0, stream=None)
+// In the first two forms argv holds the kernel's own arguments, as the reference runtime
+// builds it; the C ABI plans the workgroups from the kernel's launch shape and appends
+// the hidden extents.
+
+enum class Form { kThreads, kThreadgroups, kGroups };
+
 struct LaunchArgs {
   PyObject* kernel = nullptr;
   PyObject* argv = nullptr;
   PyObject* writable = nullptr;
-  PyObject* grid = nullptr;
-  PyObject* block = nullptr;
+  PyObject* size = nullptr;
+  PyObject* tptg = nullptr;
   int repeat = 1;
   unsigned int lds = 0;
   PyObject* stream = nullptr;
   uint32_t g[3], b[3];
+  uint64_t sz[3];
+  uint32_t tg[3] = {0, 0, 0};
   eas_hip_kernel* k = nullptr;
 };
 
-bool parse_launch(PyObject* args, PyObject* kwargs, LaunchArgs& a) {
-  static const char* kw[] = {"kernel", "argv", "writable", "grid", "block", "repeat", "lds", "stream", nullptr};
-  if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOOO|iIO", const_cast<char**>(kw), &a.kernel, &a.argv, &a.writable,
-                                   &a.grid, &a.block, &a.repeat, &a.lds, &a.stream))
+// An int (x, 1, 1) or a 1..3 tuple/list of non-negative ints, as the reference's parse_size3
+// (_metal.mm:955-1011).
+bool parse_size3(PyObject* obj, uint64_t out[3], const char* what) {
+  out[0] = out[1] = out[2] = 1;
+  if (PyLong_Check(obj)) {
+    unsigned long long v = PyLong_AsUnsignedLongLong(obj);
+    if (PyErr_Occurred()) return false;
+    out[0] = v;
+    return true;
+  }
+  if (!PyTuple_Check(obj) && !PyList_Check(obj)) {
+    PyErr_Format(PyExc_TypeError, "%s must be int or tuple/list of ints", what);
     return false;
+  }
+  PyObject* seq = PySequence_Fast(obj, "expected a tuple/list");
+  if (!seq) return false;
+  Py_ssize_t n = PySequence_Fast_GET_SIZE(seq);
+  if (n < 1 || n > 3) {
+    Py_DECREF(seq);
+    PyErr_Format(PyExc_ValueError, "%s must have 1..3 dims", what);
+    return false;
+  }
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject* it = PySequence_Fast_GET_ITEM(seq, i);
+    if (!PyLong_Check(it)) {
+      Py_DECREF(seq);
+      PyErr_Format(PyExc_TypeError, "%s dim %zd must be int", what, i);
+      return false;
+    }
+    unsigned long long v = PyLong_AsUnsignedLongLong(it);
+    if (PyErr_Occurred()) {
+      Py_DECREF(seq);
+      return false;
+    }
+    out[i] = v;
+  }
+  Py_DECREF(seq);
+  return true;
+}
+
+// threads_per_threadgroup: None or 0 means the kernel's own (all zeros for the C ABI).
+bool parse_tptg(PyObject* obj, uint32_t out[3]) {
+  out[0] = out[1] = out[2] = 0;
+  if (!obj || obj == Py_None) return true;
+  uint64_t v[3];
+  if (!parse_size3(obj, v, "threads_per_threadgroup")) return false;
+  if (PyLong_Check(obj) && v[0] == 0) return true;
+  for (int i = 0; i < 3; ++i) {
+    if (v[i] == 0) {
+      PyErr_SetString(PyExc_ValueError, "threads_per_threadgroup dims must be > 0");
+      return false;
+    }
+    if (v[i] > 1024) {
+      PyErr_Format(PyExc_ValueError, "threads_per_threadgroup too large: %llu", (unsigned long long)v[i]);
+      return false;
+    }
+    out[i] = (uint32_t)v[i];
+  }
+  return true;
+}
+
+bool parse_launch(PyObject* args, PyObject* kwargs, Form form, LaunchArgs& a) {
+  if (form == Form::kGroups) {
+    static const char* kw[] = {"kernel", "argv", "writable", "grid", "block", "repeat", "lds", "stream", nullptr};
+    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOOO|iIO", const_cast<char**>(kw), &a.kernel, &a.argv,
+                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.lds, &a.stream))
+      return false;
+  } else if (form == Form::kThreads) {
+    static const char* kw[] = {"kernel", "argv", "writable", "threads_per_grid", "threads_per_threadgroup", "repeat",
+                               "stream", nullptr};
+    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOO|Oi$O", const_cast<char**>(kw), &a.kernel, &a.argv,
+                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.stream))
+      return false;
+  } else {
+    static const char* kw[] = {"kernel", "argv", "writable", "threadgroups", "threads_per_threadgroup", "repeat",
+                               "stream", nullptr};
+    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOOO|i$O", const_cast<char**>(kw), &a.kernel, &a.argv,
+                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.stream))
+      return false;
+  }
   if (a.repeat <= 0) {
     PyErr_SetString(PyExc_ValueError, "repeat must be > 0");
     return false;
   }
   a.k = as_kernel(a.kernel);
   if (!a.k) return false;
-  if (!parse_dim3(a.grid, a.g, "grid") || !parse_dim3(a.block, a.b, "block")) return false;
-  if (a.g[0] == 0 || a.g[1] == 0 || a.g[2] == 0) {
-    PyErr_SetString(PyExc_ValueError, "grid dims must be > 0");
+  if (form == Form::kGroups) {
+    if (!parse_dim3(a.size, a.g, "grid") || !parse_dim3(a.tptg, a.b, "block")) return false;
+    if (a.g[0] == 0 || a.g[1] == 0 || a.g[2] == 0) {
+      PyErr_SetString(PyExc_ValueError, "grid dims must be > 0");
+      return false;
+    }
+    if (a.b[0] == 0 || a.b[1] == 0 || a.b[2] == 0) {
+      PyErr_SetString(PyExc_ValueError, "block dims must be > 0");
+      return false;
+    }
+    if ((uint64_t)a.b[0] * a.b[1] * a.b[2] > 1024) {
+      PyErr_Format(PyExc_ValueError, "threads_per_threadgroup too large: %llu",
+                   (unsigned long long)a.b[0] * a.b[1] * a.b[2]);
+      return false;
+    }
+    return true;
+  }
+  const char* what = form == Form::kThreads ? "threads_per_grid" : "threadgroups";
+  if (!parse_size3(a.size, a.sz, what)) return false;
+  if (a.sz[0] == 0 || a.sz[1] == 0 || a.sz[2] == 0) {
+    PyErr_Format(PyExc_ValueError, "%s dims must be > 0", what);
     return false;
   }
-  if (a.b[0] == 0 || a.b[1] == 0 || a.b[2] == 0) {
-    PyErr_SetString(PyExc_ValueError, "block dims must be > 0");
-    return false;
-  }
-  if ((uint64_t)a.b[0] * a.b[1] * a.b[2] > 1024) {
-    PyErr_Format(PyExc_ValueError, "threads_per_threadgroup too large: %llu",
-                 (unsigned long long)a.b[0] * a.b[1] * a.b[2]);
-    return false;
-  }
-  return true;
+  return parse_tptg(a.tptg, a.tg);
 }
 
-// launch(kernel, argv, writable, grid, block, repeat=1, lds=0, stream=None):
-// enqueue and wait (GIL released while waiting), like the reference's sync launch.
-PyObject* launch_impl(PyObject* args, PyObject* kwargs, bool async) {
+int dispatch(const LaunchArgs& a, Form form, const std::vector<uint8_t>& blob, void* stream) {
+  switch (form) {
+    case Form::kGroups:
+      return eas_hip_launch(a.k, blob.data(), blob.size(), a.g, a.b, a.lds, stream, a.repeat);
+    case Form::kThreads:
+      return eas_hip_launch_threads(a.k, blob.data(), blob.size(), a.sz, a.tg, stream, a.repeat);
+    default:
+      return eas_hip_launch_threadgroups(a.k, blob.data(), blob.size(), a.sz, a.tg, stream, a.repeat);
+  }
+}
+
+// Enqueue; the synchronous forms then wait with the GIL released, like the reference's.
+PyObject* launch_impl(PyObject* args, PyObject* kwargs, Form form, bool async) {
   LaunchArgs a;
-  if (!parse_launch(args, kwargs, a)) return nullptr;
+  if (!parse_launch(args, kwargs, form, a)) return nullptr;
   std::vector<uint8_t> blob;
   auto* pending = async ? new Pending{nullptr, {}} : nullptr;
   if (!pack_args(a.argv, a.writable, blob, pending ? &pending->keepalive : nullptr)) {
@@ -564,7 +721,7 @@ PyObject* launch_impl(PyObject* args, PyObject* kwargs, bool async) {
     delete pending;
     return nullptr;
   }
-  int rc = eas_hip_launch(a.k, blob.data(), blob.size(), a.g, a.b, a.lds, stream, a.repeat);
+  int rc = dispatch(a, form, blob, stream);
   if (rc) {
     if (pending) release_pending(pending);
     delete pending;
@@ -594,10 +751,21 @@ PyObject* launch_impl(PyObject* args, PyObject* kwargs, bool async) {
   return cap;
 }
 
-PyObject* py_launch(PyObject*, PyObject* args, PyObject* kw) { return launch_impl(args, kw, false); }
-PyObject* py_launch_async(PyObject*, PyObject* args, PyObject* kw) { return launch_impl(args, kw, true); }
+PyObject* py_launch(PyObject*, PyObject* args, PyObject* kw) { return launch_impl(args, kw, Form::kThreads, false); }
+PyObject* py_launch_async(PyObject*, PyObject* args, PyObject* kw) { return launch_impl(args, kw, Form::kThreads, true); }
+PyObject* py_launch_tg(PyObject*, PyObject* args, PyObject* kw) {
+  return launch_impl(args, kw, Form::kThreadgroups, false);
+}
+PyObject* py_launch_tg_async(PyObject*, PyObject* args, PyObject* kw) {
+  return launch_impl(args, kw, Form::kThreadgroups, true);
+}
+PyObject* py_launch_groups(PyObject*, PyObject* args, PyObject* kw) { return launch_impl(args, kw, Form::kGroups, false); }
+PyObject* py_launch_groups_async(PyObject*, PyObject* args, PyObject* kw) {
+  return launch_impl(args, kw, Form::kGroups, true);
+}
 
 // launch_timed(kernel, argv, writable, grid, block, repeat=1, lds=0, stream=None, warmup=0) -> mean ms per launch
+// (workgroup form, argv ending with the hidden extents)
 PyObject* py_launch_timed(PyObject*, PyObject* args, PyObject* kwargs) {
   PyObject* warm_obj = kwargs ? PyDict_GetItemString(kwargs, "warmup") : nullptr;
   long warmup = 0;
@@ -610,7 +778,7 @@ PyObject* py_launch_timed(PyObject*, PyObject* args, PyObject* kwargs) {
     PyDict_DelItemString(kw2, "warmup");
   }
   LaunchArgs a;
-  bool ok = parse_launch(args, kw2 ? kw2 : kwargs, a);
+  bool ok = parse_launch(args, kw2 ? kw2 : kwargs, Form::kGroups, a);
   Py_XDECREF(kw2);
   if (!ok) return nullptr;
   if (warmup < 0) {
@@ -628,6 +796,71 @@ PyObject* py_launch_timed(PyObject*, PyObject* args, PyObject* kwargs) {
   Py_END_ALLOW_THREADS
   if (rc) return raise_status(rc);
   return PyFloat_FromDouble((double)ms);
+}
+
+const char* kind_name(int kind) {
+  switch (kind) {
+    case EAS_HIP_KIND_SPMD: return "spmd";
+    case EAS_HIP_KIND_THREAD: return "thread";
+    case EAS_HIP_KIND_GEMM: return "gemm";
+    default: return "raw";
+  }
+}
+
+PyObject* shape_dict(const eas_hip_launch_shape& s) {
+  return Py_BuildValue("{s:s,s:I,s:I,s:I,s:I,s:I,s:I}", "kind", kind_name(s.kind), "block_size", s.block_size,
+                       "wg_size", s.wg_size, "programs_per_wg", s.programs_per_wg, "split", s.split, "arg_bytes",
+                       s.arg_bytes, "hidden", s.hidden);
+}
+
+// kernel_shape(kernel) -> dict: the launch shape attached to a loaded kernel.
+PyObject* py_kernel_shape(PyObject*, PyObject* args) {
+  PyObject* cap;
+  if (!PyArg_ParseTuple(args, "O", &cap)) return nullptr;
+  eas_hip_kernel* k = as_kernel(cap);
+  if (!k) return nullptr;
+  eas_hip_launch_shape s;
+  int rc = eas_hip_kernel_get_shape(k, &s);
+  if (rc) return raise_status(rc);
+  return shape_dict(s);
+}
+
+// launch_shape(src) -> dict: the shape on a generated source's eas-launch line (no GPU needed).
+PyObject* py_launch_shape(PyObject*, PyObject* args) {
+  const char* src;
+  if (!PyArg_ParseTuple(args, "s", &src)) return nullptr;
+  eas_hip_launch_shape s;
+  int rc = eas_hip_launch_shape_parse(src, &s);
+  if (rc) return raise_status(rc);
+  return shape_dict(s);
+}
+
+// plan_dispatch(src, size, threads_per_threadgroup=None, by_groups=False) -> (grid, block, hidden):
+// the HIP dispatch that launch (by_groups False) or launch_tg (True) makes for a kernel compiled
+// from `src`, without a GPU.
+PyObject* py_plan_dispatch(PyObject*, PyObject* args, PyObject* kwargs) {
+  static const char* kw[] = {"src", "size", "threads_per_threadgroup", "by_groups", nullptr};
+  const char* src;
+  PyObject* size_obj;
+  PyObject* tptg_obj = nullptr;
+  int by_groups = 0;
+  if (!PyArg_ParseTupleAndKeywords(args, kwargs, "sO|Op", const_cast<char**>(kw), &src, &size_obj, &tptg_obj,
+                                   &by_groups))
+    return nullptr;
+  eas_hip_launch_shape s;
+  int rc = eas_hip_launch_shape_parse(src, &s);
+  if (rc) return raise_status(rc);
+  uint64_t sz[3];
+  uint32_t tg[3];
+  if (!parse_size3(size_obj, sz, by_groups ? "threadgroups" : "threads_per_grid") || !parse_tptg(tptg_obj, tg))
+    return nullptr;
+  uint32_t grid[3], block[3], hidden[EAS_HIP_MAX_HIDDEN];
+  rc = eas_hip_plan_dispatch(&s, by_groups, sz, tg, grid, block, hidden, EAS_HIP_MAX_HIDDEN);
+  if (rc) return raise_status(rc);
+  PyObject* h = PyTuple_New(s.hidden);
+  for (uint32_t i = 0; h && i < s.hidden; ++i) PyTuple_SET_ITEM(h, i, PyLong_FromUnsignedLong(hidden[i]));
+  if (!h) return nullptr;
+  return Py_BuildValue("((III)(III)N)", grid[0], grid[1], grid[2], block[0], block[1], block[2], h);
 }
 
 PyObject* py_synchronize(PyObject*, PyObject* args) {
@@ -782,8 +1015,14 @@ PyMethodDef kMethods[] = {
     {"device_props", py_device_props, METH_VARARGS, "Properties of a device (default: current)."},
     {"compile_to_code", py_compile_to_code, METH_VARARGS, "hiprtc: source -> code object bytes (no GPU needed)."},
     {"compiler_version", py_compiler_version, METH_NOARGS, "(major, minor, path) of the hiprtc in use."},
-    {"load", py_load, METH_VARARGS, "Load a code object and look up a kernel."},
-    {"compile", py_compile, METH_VARARGS, "compile_to_code + load."},
+    {"load", (PyCFunction)(void (*)(void))py_load, METH_VARARGS | METH_KEYWORDS,
+     "Load a code object and look up a kernel (src= gives it its launch shape)."},
+    {"kernel_shape", py_kernel_shape, METH_VARARGS, "Launch shape attached to a loaded kernel."},
+    {"launch_shape", py_launch_shape, METH_VARARGS, "Launch shape on a generated source's eas-launch line."},
+    {"plan_dispatch", (PyCFunction)(void (*)(void))py_plan_dispatch, METH_VARARGS | METH_KEYWORDS,
+     "HIP dispatch (grid, block, hidden) of a reference-convention launch, without a GPU."},
+    {"compile", py_compile, METH_VARARGS,
+     "compile(src, name, options=None): compile_to_code (DEFAULT_OPTIONS when none are given) + load."},
     {"kernel_attrs", py_kernel_attrs, METH_VARARGS, "Static resources of a loaded kernel."},
     {"alloc_buffer", py_alloc_buffer, METH_VARARGS, "Allocate device ('private') or pinned ('shared') memory."},
     {"wrap_pointer", py_wrap_pointer, METH_VARARGS, "Non-owning buffer capsule over existing device memory."},
@@ -791,13 +1030,21 @@ PyMethodDef kMethods[] = {
     {"copy_from_host", py_copy_from_host, METH_VARARGS, "Synchronous host -> buffer copy."},
     {"copy_to_host", py_copy_to_host, METH_VARARGS, "Synchronous buffer -> host copy."},
     {"copy_buffer", py_copy_buffer, METH_VARARGS, "Synchronous buffer -> buffer copy."},
-    {"launch", (PyCFunction)(void (*)(void))py_launch, METH_VARARGS | METH_KEYWORDS, "Launch and wait."},
+    {"launch", (PyCFunction)(void (*)(void))py_launch, METH_VARARGS | METH_KEYWORDS,
+     "launch(kernel, argv, writable, threads_per_grid, threads_per_threadgroup=None, repeat=1): dispatch by "
+     "threads and wait."},
     {"launch_async", (PyCFunction)(void (*)(void))py_launch_async, METH_VARARGS | METH_KEYWORDS,
-     "Launch; returns a pending capsule."},
-    {"launch_tg", (PyCFunction)(void (*)(void))py_launch, METH_VARARGS | METH_KEYWORDS,
-     "Alias of launch (HIP always dispatches workgroups)."},
-    {"launch_tg_async", (PyCFunction)(void (*)(void))py_launch_async, METH_VARARGS | METH_KEYWORDS,
-     "Alias of launch_async."},
+     "As launch; returns a pending capsule."},
+    {"launch_tg", (PyCFunction)(void (*)(void))py_launch_tg, METH_VARARGS | METH_KEYWORDS,
+     "launch_tg(kernel, argv, writable, threadgroups, threads_per_threadgroup, repeat=1): dispatch by "
+     "threadgroups and wait."},
+    {"launch_tg_async", (PyCFunction)(void (*)(void))py_launch_tg_async, METH_VARARGS | METH_KEYWORDS,
+     "As launch_tg; returns a pending capsule."},
+    {"launch_groups", (PyCFunction)(void (*)(void))py_launch_groups, METH_VARARGS | METH_KEYWORDS,
+     "launch_groups(kernel, argv, writable, grid, block, repeat=1, lds=0, stream=None): HIP workgroups, argv "
+     "ending with the hidden extents; waits."},
+    {"launch_groups_async", (PyCFunction)(void (*)(void))py_launch_groups_async, METH_VARARGS | METH_KEYWORDS,
+     "As launch_groups; returns a pending capsule."},
     {"launch_timed", (PyCFunction)(void (*)(void))py_launch_timed, METH_VARARGS | METH_KEYWORDS,
      "Event-timed repeat launches; mean ms per launch."},
     {"synchronize", py_synchronize, METH_VARARGS, "Wait for a pending launch and drop its keepalives."},
@@ -814,5 +1061,9 @@ PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_hip", "MI355X (gfx950) HIP backe
 PyMODINIT_FUNC PyInit__hip(void) {
   PyObject* m = PyModule_Create(&kModule);
   if (m) PyModule_AddIntConstant(m, "ABI_VERSION", eas_hip_abi_version());
+  if (m && PyModule_AddObject(m, "DEFAULT_OPTIONS", default_options()) != 0) {
+    Py_DECREF(m);
+    return nullptr;
+  }
   return m;
 }

@@ -238,7 +238,8 @@ class HipRuntime:
         if k is None:
             mod = self._mod()
             if callable(getattr(mod, "compile_to_code", None)) and callable(getattr(mod, "load", None)):
-                k = mod.load(compile_code(mod, ck.src, main), entry)
+                # the source's eas-launch line gives the kernel its launch shape and argument size
+                k = mod.load(compile_code(mod, ck.src, main), entry, src=ck.src)
             else:
                 k = mod.compile(ck.src, entry)
             self._kernels[key] = k
@@ -362,11 +363,11 @@ class HipRuntime:
         mod = self._mod()
         kernel = self.kernel_handle(ck, plan.entry)
         if sync or copy_back:
-            mod.launch(kernel, argv, writable, plan.grid, plan.block, stream=stream)
+            mod.launch_groups(kernel, argv, writable, plan.grid, plan.block, stream=stream)
             for buf, arr in copy_back:
                 mod.copy_to_host(buf, arr)
             return
-        self._pending.append(mod.launch_async(kernel, argv, writable, plan.grid, plan.block, stream=stream))
+        self._pending.append(mod.launch_groups_async(kernel, argv, writable, plan.grid, plan.block, stream=stream))
         limit = self._max_pending()
         while limit and len(self._pending) > limit:
             mod.synchronize(self._pending.popleft())

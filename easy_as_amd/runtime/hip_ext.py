@@ -21,6 +21,10 @@ REQUIRED_API = (
     "compile_to_code",
     "load",
     "launch_async",
+    "launch_tg",
+    "launch_tg_async",
+    "launch_groups",
+    "launch_groups_async",
     "launch_timed",
     "wrap_pointer",
     "device_props",

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define EAS_HIP_ABI_VERSION 2
+#define EAS_HIP_ABI_VERSION 3
 
 typedef enum eas_hip_status {
   EAS_HIP_OK = 0,
@@ -111,15 +111,74 @@ int eas_hip_copy_h2d(void* dst, const void* src, size_t nbytes);
 int eas_hip_copy_d2h(void* dst, const void* src, size_t nbytes);
 int eas_hip_copy_d2d(void* dst, const void* src, size_t nbytes);
 
-/* Fill `nbytes` of device memory with a byte value on `stream` (async). */
-int eas_hip_memset(void* dst, int value, size_t nbytes, void* stream);
+/* ---- launch shapes --------------------------------------------------------
+ * How the reference's dispatch sizes map onto HIP workgroups for one compiled
+ * eas kernel.  The reference dispatches Metal threads (`launch`: threads per
+ * grid, non-uniform last threadgroup) or threadgroups (`launch_tg`).  Here an
+ * SPMD program (one Metal thread) is spread over HIP threads, and a thread-mode
+ * kernel's threadgroup is one workgroup; the kernels take their true extent as
+ * hidden u32 arguments after their own, because HIP has no non-uniform
+ * dispatch.  Every generated source carries its shape on a marker line
+ * (`// eas-launch: kind=... block=... wg=... ppw=... split=... args=... hidden=...`). */
+typedef enum eas_hip_launch_kind {
+  EAS_HIP_KIND_RAW = 0,    /* shape unknown: only eas_hip_launch (workgroups) runs it      */
+  EAS_HIP_KIND_SPMD = 1,   /* a Metal thread is a program of block_size lanes (mk.arange)   */
+  EAS_HIP_KIND_THREAD = 2, /* a Metal thread is a HIP thread, a threadgroup a workgroup     */
+  EAS_HIP_KIND_GEMM = 3    /* lifted MFMA GEMM: its plan needs M, N, K (eas_hip_launch only) */
+} eas_hip_launch_kind;
+
+typedef struct eas_hip_launch_shape {
+  int kind;                 /* eas_hip_launch_kind                                        */
+  uint32_t block_size;      /* the kernel's BLOCK (lanes per program, threads per group)   */
+  uint32_t wg_size;         /* HIP threads per workgroup                                   */
+  uint32_t programs_per_wg; /* SPMD: programs each group of `split` workgroups runs         */
+  uint32_t split;           /* SPMD: workgroups a program's lanes are spread over (>= 1)   */
+  uint32_t arg_bytes;       /* packed bytes of the kernel's own arguments (0: not checked) */
+  uint32_t hidden;          /* u32 extents that follow them (<= EAS_HIP_MAX_HIDDEN)        */
+} eas_hip_launch_shape;
+
+#define EAS_HIP_MAX_HIDDEN 8
+
+/* Parse the `// eas-launch:` marker line of a generated source into *out.
+ * EAS_HIP_ERR_INVALID if the source has none or it is malformed.  No GPU needed. */
+int eas_hip_launch_shape_parse(const char* src, eas_hip_launch_shape* out);
+
+/* Attach a launch shape to a loaded kernel (validated), or read it back. */
+int eas_hip_kernel_set_shape(eas_hip_kernel* k, const eas_hip_launch_shape* shape);
+int eas_hip_kernel_get_shape(const eas_hip_kernel* k, eas_hip_launch_shape* out);
+
+/* The HIP dispatch of a reference-convention launch, without launching (no GPU
+ * needed).  by_groups = 0: `size` is threads per grid, as `launch(pipeline, argv,
+ * writable, threads_per_grid, threads_per_threadgroup)` passes it
+ * (_metal.mm:1013-1222, 1381-1383); by_groups = 1: `size` is threadgroups, as
+ * `launch_tg` passes it (_metal.mm:1232-1379).  `tptg` is the threads per
+ * threadgroup the reference runtime passes ((BLOCK,1,1) for thread-mode kernels,
+ * (1,1,1) for SPMD ones, eas/runtime/metal.py:259-326); all zeros means the kernel's
+ * own.  Writes the workgroup grid, the workgroup shape and the shape->hidden
+ * extents.  A zero size dimension is EAS_HIP_ERR_INVALID, as in the reference. */
+int eas_hip_plan_dispatch(const eas_hip_launch_shape* shape, int by_groups, const uint64_t size[3],
+                          const uint32_t tptg[3], uint32_t grid[3], uint32_t block[3], uint32_t* hidden,
+                          int max_hidden);
+
+/* Enqueue `repeat` >= 1 launches by the reference's conventions: `kernarg` holds the
+ * kernel's own arguments only (shape->arg_bytes when known); the hidden extents are
+ * appended here.  Asynchronous.  Replaces `launch` / `launch_async`
+ * (_metal.mm:1013-1222, 1381-1383) and `launch_tg` / `launch_tg_async`
+ * (_metal.mm:1232-1379).  Needs a kernel with an SPMD or thread-mode shape. */
+int eas_hip_launch_threads(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
+                           const uint64_t threads_per_grid[3], const uint32_t threads_per_threadgroup[3],
+                           void* stream, int repeat);
+int eas_hip_launch_threadgroups(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
+                                const uint64_t threadgroups[3], const uint32_t threads_per_threadgroup[3],
+                                void* stream, int repeat);
 
 /* Enqueue `repeat` >= 1 launches of `k` on `stream` with a packed kernel-argument
- * blob (arguments at natural alignment, in the kernel's parameter order).
- * grid = workgroup counts, block = threads per workgroup.  Asynchronous.
- * Replaces `launch` / `launch_tg` (_metal.mm:1013-1222, 1232-1379); the
- * threads->workgroups conversion and the hidden extent arguments that emulate
- * Metal's non-uniform dispatchThreads are done by the caller. */
+ * blob (arguments at natural alignment, in the kernel's parameter order, then the
+ * hidden u32 extents).  grid = workgroup counts, block = threads per workgroup.
+ * Asynchronous.  The HIP-level dispatch under both reference launch forms: the
+ * Python runtime plans every launch itself (a lifted GEMM's plan needs its
+ * matrix sizes) and uses this one.  When the kernel's shape knows its argument
+ * bytes, a blob of any other size is EAS_HIP_ERR_INVALID. */
 int eas_hip_launch(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],
                    const uint32_t block[3], uint32_t dynamic_lds, void* stream, int repeat);
 

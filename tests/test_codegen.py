@@ -202,17 +202,15 @@ def test_mma_kernel_lowers_to_mfma():
     assert "eas_gemm_pp<CT, K, 16>" in ck.src
 
 
-def test_pp_mfma_switch_is_validated():
-    import subprocess
-    import sys
-
-    code = "import easy_as_amd.codegen.gemm_kernels as g; print(g.PP_MFMA)"
-    env = {**__import__("os").environ, "EAS_HIP_GEMM_MFMA": "32"}
-    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
-    assert r.returncode == 0 and r.stdout.strip() == "32"
-    env["EAS_HIP_GEMM_MFMA"] = "8"
-    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, timeout=120)
-    assert r.returncode != 0 and "EAS_HIP_GEMM_MFMA must be 16 or 32" in r.stderr
+def test_pp_mfma_switch_is_validated(monkeypatch):
+    # read when a GEMM source is emitted: a fresh kernel object picks it up
+    h, f = np.zeros(8, np.float16), np.zeros(8, np.float32)
+    monkeypatch.setenv("EAS_HIP_GEMM_MFMA", "32")
+    ck = eas.kernel(K.matmul_mma_kernel.fn).compile(h, h, f, 4096, 4096, BM=32, BN=32, BK=8, K=4096, NT=512)
+    assert "eas_gemm_pp<CT, K, 32>" in ck.src
+    monkeypatch.setenv("EAS_HIP_GEMM_MFMA", "8")
+    with pytest.raises(ValueError, match="EAS_HIP_GEMM_MFMA must be 16 or 32"):
+        eas.kernel(K.matmul_mma_kernel.fn).compile(h, h, f, 4096, 4096, BM=32, BN=32, BK=8, K=4096, NT=512)
 
 
 def _sources() -> list[tuple[str, str]]:

@@ -230,6 +230,42 @@ def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
         assert plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args)).entry == "matmul_mma_kernel__t128"
 
 
+@pytest.mark.parametrize("mnk", [(300, 520, 200), (257, 264, 72), (520, 256, 1000), (130, 260, 4100),
+                                 (1024, 1024, 1024)])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_8wave_entry_with_32x32x16_mfma(gpu_runtime, monkeypatch, mnk, dtype):
+    """EAS_HIP_GEMM_MFMA=32: the 8-wave entry's 4 x 2 tiles of v_mfma_f32_32x32x16 per wave, against
+    float64 and against the default 16 x 16 x 32 body on the same launch (same products, other
+    summation order inside an MFMA: equal to f32 rounding)."""
+    import torch
+
+    import eas
+
+    m, n, k = mnk
+    a, b = _inputs(m, n, k, seed=6)
+    if dtype == "bf16":
+        a32, b32 = (torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16) for x in (a, b))
+        a, b = (t.float().numpy() for t in (a32, b32))
+        da, db = a32.cuda(), b32.cuda()
+        src_kernel = K.matmul_mma_bf16_kernel
+    else:
+        da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+        src_kernel = K.matmul_mma_kernel
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "8wave")
+    outs = {}
+    for mi in ("32", "16"):
+        monkeypatch.setenv("EAS_HIP_GEMM_MFMA", mi)
+        kern = eas.kernel(src_kernel.fn)
+        ck = kern.compile(da, db, torch.zeros(1, device="cuda"), m, n, BM=32, BN=32, BK=8, K=k, NT=512)
+        assert f"eas_gemm_pp<CT, K, {mi}>" in ck.src
+        tc = torch.full((m * n,), float("nan"), device="cuda", dtype=torch.float32)
+        _mma(kern, da, db, tc, m, n, k)
+        torch.cuda.synchronize()
+        outs[mi] = tc.cpu().numpy()
+        _check(outs[mi], a, b, m, n, k)
+    assert ops.rel_err(outs["32"].reshape(m, n).astype(np.float64), outs["16"].reshape(m, n).astype(np.float64)) <= 1e-6
+
+
 @pytest.mark.parametrize("choice,entry", [("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128")])
 def test_dma_entry_guard_for_an_operand_it_cannot_see(gpu_runtime, monkeypatch, choice, entry):
     """An eas.Tensor viewing torch memory at a 2-byte offset: the plan cannot see the address,

@@ -321,7 +321,7 @@ def test_plan_dma_entries_only_for_operands_the_dma_takes(monkeypatch):
 # ---- kernel-argument packing through a recording extension ------------------------
 
 class _RecordingExt:
-    ABI_VERSION = 2
+    ABI_VERSION = 3
 
     def __init__(self):
         self.launches, self.h2d, self.d2h, self.allocs = [], [], [], []
@@ -339,14 +339,14 @@ class _RecordingExt:
     def compile_to_code(self, src, name, options):
         return b"\x7fELF-recorded"
 
-    def load(self, code, entry):
+    def load(self, code, entry, src=None):
         return ("kernel", entry)
 
-    def launch(self, kernel, argv, writable, grid, block, stream=None):
+    def launch_groups(self, kernel, argv, writable, grid, block, stream=None):
         self.launches.append((kernel, list(argv), list(writable), grid, block))
 
-    def launch_async(self, kernel, argv, writable, grid, block, stream=None):
-        self.launch(kernel, argv, writable, grid, block, stream)
+    def launch_groups_async(self, kernel, argv, writable, grid, block, stream=None):
+        self.launch_groups(kernel, argv, writable, grid, block, stream)
         return ("pending", len(self.launches))
 
     def synchronize(self, pending):
