@@ -719,7 +719,12 @@ def analyze(ir: IRModule, block: int) -> GemmSpec:
     seen = np.zeros((S, 8, 8), np.int64)
     frag_rid = recs.index(frag_recs[0])
     c_rnd = None
+    # a bound the operand loads apply must guard every output store too: the lifted kernel
+    # writes only rows < M (cols < N), while a store without that mask would also write
+    # the rows (cols) past it
+    m_from_loads, n_from_loads = m_sym, n_sym
     for name, off, cond, rid in ex.stores:
+        row_masked = col_masked = False
         r = recs[rid]
         if r.kind != "lds":
             raise Unsupported("output is not read back from the fragment tile")
@@ -752,10 +757,15 @@ def analyze(ir: IRModule, block: int) -> GemmSpec:
             is_col = _same(rest, want_col)
             if is_row and (m_sym is None or m_sym == sym):
                 m_sym = sym
+                row_masked = True
             elif is_col and sym == ldb_sym:
-                pass
+                col_masked = True
             else:
                 raise Unsupported("output mask is not row < M / col < N")
+        if m_from_loads is not None and not row_masked:
+            raise Unsupported("row bound applied inconsistently (the loads have it, an output store does not)")
+        if n_from_loads is not None and not col_masked:
+            raise Unsupported("column bound applied inconsistently (the loads have it, an output store does not)")
     if np.any(seen != 1):
         raise Unsupported("the tile is not stored exactly once")
     # the tile is the full rectangle [0,TM) x [0,TN)

@@ -543,6 +543,8 @@ def matmul_mma_variant_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexp
       4 output stored transposed    5 B row stride is M           6 half the tile stored
       7 A fragment stride off       8 one output element stored twice
       9 k blocks in reverse order  10 rows on program_id(0), cols on program_id(1)
+     11 output stored without its row mask (rows past M written, as zeros)
+     12 output stored without its column mask
     """
     V = VARIANT
     pid_n = mk.program_id(1 if V == 10 else 0)
@@ -602,6 +604,10 @@ def matmul_mma_variant_kernel(a, b, c, M, N, BM: eas.constexpr, BN: eas.constexp
         col = base_n + cc
         col_bound = M if V == 3 else N
         mask = mk.where(row < M, col < col_bound, False)
+        if V == 11:
+            mask = col < col_bound
+        if V == 12:
+            mask = row < M
         off = col * N + row if V == 4 else row * N + col
         mk.store(c, off, mk.load(Cs, r * ldc + cc, True), mask)
     if V == 8:

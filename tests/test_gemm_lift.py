@@ -42,7 +42,7 @@ def test_f16_output_and_f32_inputs_are_lifted():
     assert spec.a_dtype == DType.F32 and spec.b_dtype == DType.F32
 
 
-@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("variant", [1, 2, 3, 4, 5, 6, 7, 8, 11, 12])
 def test_non_gemm_variants_are_not_lifted(variant):
     ir, nt = _variant(variant)
     with pytest.raises(Unsupported):

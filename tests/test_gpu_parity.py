@@ -491,6 +491,34 @@ def test_async_launches_and_synchronize(gpu_runtime):
         assert _bits_equal(o.numpy(), ops.add_f32(a, b))
 
 
+@pytest.mark.parametrize("limit", [2, 0])
+def test_in_flight_limit_bounds_pending_launches(monkeypatch, limit):
+    """EAS_MAX_IN_FLIGHT (eas/runtime/metal.py:52-67, 340-352): at most that many async launches
+    stay pending; the oldest is waited on first.  0 means no bound."""
+    from easy_as_amd.runtime.hip import HipRuntime
+
+    monkeypatch.setenv("EAS_MAX_IN_FLIGHT", str(limit))
+    rt = HipRuntime()
+    n = 1 << 20
+    a, b = seeded_normal(0, n), seeded_normal(1, n)
+    ta, tb = eas.tensor(a, device="hip"), eas.tensor(b, device="hip")
+    outs = [eas.empty(n, device="hip") for _ in range(16)]
+    ck = K.add_kernel.compile(ta, tb, outs[0], n, BLOCK=256)
+    seen = []
+    for o in outs:
+        rt.run(ck, {"a": ta, "b": tb, "c": o, "N": n}, {"BLOCK": 256}, sync=False)
+        seen.append(len(rt._pending))
+    if limit:
+        assert max(seen) == limit and seen[:limit] == list(range(1, limit + 1))
+    else:
+        assert seen == list(range(1, 17))
+    rt.synchronize()
+    assert len(rt._pending) == 0
+    want = ops.add_f32(a, b)
+    for o in outs:
+        assert _bits_equal(o.numpy(), want)
+
+
 def test_launches_follow_torch_current_stream(gpu_runtime):
     """An eas launch with torch GPU tensors goes on torch's current stream: inputs that torch
     writes on a side stream (after a long matmul, so they land late) are seen by the kernel,

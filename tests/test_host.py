@@ -513,3 +513,81 @@ def test_fast_binding_matches_inspect():
 
     assert not eas_kernel.Kernel(kwonly)._plain
     assert eas_kernel.Kernel(kwonly)._bind_and_split(x, N=3) == ({}, {"a": x, "N": 3})
+
+
+# ---- code-object cache (reference: the pipeline cache, eas/runtime/metal.py:122-132) ----------
+
+class _CountingCompiler:
+    """compile_to_code that counts its calls; compiler_version and ABI_VERSION are settable."""
+
+    def __init__(self, tag=("7", "2"), abi=3):
+        self.calls, self.tag, self.ABI_VERSION = [], tag, abi
+
+    def compile_to_code(self, src, name, options):
+        self.calls.append((name, tuple(options)))
+        return b"\x7fELF" + str(len(self.calls)).encode()
+
+    def compiler_version(self):
+        return (int(self.tag[0]), int(self.tag[1]), "/opt/rocm/lib/libhiprtc.so.7")
+
+
+def test_code_object_cache_hits_and_misses(monkeypatch, tmp_path):
+    from easy_as_amd.runtime.hip import COMPILE_OPTIONS, compile_code
+
+    monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
+    src = K.add_kernel.compile(np.zeros(1, np.float32), np.zeros(1, np.float32), np.zeros(1, np.float32), 8,
+                               BLOCK=256).src
+    cc = _CountingCompiler()
+    first = compile_code(cc, src, "add_kernel")
+    assert len(cc.calls) == 1 and len(list(tmp_path.glob("*.co"))) == 1
+    assert compile_code(cc, src, "add_kernel") == first and len(cc.calls) == 1  # hit
+    # each part of the key misses: options, entry, source, compiler version, ABI version
+    compile_code(cc, src, "add_kernel", COMPILE_OPTIONS[:-1])
+    compile_code(cc, src, "other_entry")
+    compile_code(cc, src + "\n", "add_kernel")
+    assert len(cc.calls) == 4
+    for other in (_CountingCompiler(tag=("7", "3")), _CountingCompiler(abi=4)):
+        compile_code(other, src, "add_kernel")
+        assert len(other.calls) == 1  # a miss: compiled, not read back
+    assert len(list(tmp_path.glob("*.co"))) == 6
+    # and EAS_HIP_DISABLE_CACHE=1 recompiles
+    monkeypatch.setenv("EAS_HIP_DISABLE_CACHE", "1")
+    compile_code(cc, src, "add_kernel")
+    assert len(cc.calls) == 5
+
+
+def test_second_process_loads_the_cached_code_object(tmp_path):
+    # a first process compiles with the real hiprtc; a second one, whose compiler would fail,
+    # gets the identical code object from EAS_HIP_CACHE_DIR
+    import os
+    import subprocess
+    import sys
+
+    script = (
+        "import sys, hashlib\n"
+        "sys.path[:0] = ['.', 'tests']\n"
+        "import numpy as np, kernels as K\n"
+        "from easy_as_amd.runtime.hip import compile_code\n"
+        "from easy_as_amd.runtime.hip_ext import load_hip_ext\n"
+        "mod = load_hip_ext(require=True)\n"
+        "z = np.zeros(1, np.float32)\n"
+        "src = K.add_kernel.compile(z, z, z, 8, BLOCK=256).src\n"
+        "if sys.argv[1] == 'second':\n"
+        "    class NoCompiler:\n"
+        "        ABI_VERSION = mod.ABI_VERSION\n"
+        "        compiler_version = staticmethod(mod.compiler_version)\n"
+        "        def compile_to_code(self, *a):\n"
+        "            raise AssertionError('compiled again')\n"
+        "    mod = NoCompiler()\n"
+        "code = compile_code(mod, src, 'add_kernel')\n"
+        "assert code[:4] == b'\\x7fELF'\n"
+        "print(hashlib.sha256(code).hexdigest())\n"
+    )
+    env = {**os.environ, "EAS_HIP_CACHE_DIR": str(tmp_path), "PYTHONPATH": str(ROOT)}
+    out = []
+    for which in ("first", "second"):
+        r = subprocess.run([sys.executable, "-c", script, which], cwd=ROOT, env=env, capture_output=True, text=True,
+                           timeout=300)
+        assert r.returncode == 0, r.stderr[-2000:]
+        out.append(r.stdout.strip().splitlines()[-1])
+    assert out[0] == out[1]
