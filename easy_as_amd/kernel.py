@@ -16,7 +16,7 @@ import inspect
 from typing import Any, Callable, Mapping
 
 from .autotune import AutotuneSpec, Config
-from .compiler import CompiledKernel, compile as _compile, runtime_arg_signature
+from .compiler import CompiledKernel, _arg_key, compile as _compile
 from .meta import constexpr
 from .runtime import get_runtime
 
@@ -142,7 +142,9 @@ class Kernel:
         return bound
 
     def _compile_from_split(self, meta: dict[str, Any], runtime_args: dict[str, Any]) -> CompiledKernel:
-        key = (tuple(sorted(meta.items())), runtime_arg_signature(runtime_args))
+        # runtime_args come from the binding in parameter order, so the per-argument keys need no
+        # sorting here (runtime_arg_signature sorts by name for callers with other orders)
+        key = (tuple(sorted(meta.items())), tuple(map(_arg_key, runtime_args.values())))
         ck = self._cache.get(key)
         if ck is None:
             ck = _compile(self.fn, runtime_args, meta)

@@ -40,6 +40,24 @@ def infer_1d_grid(runtime_args: Mapping[str, Any], threadgroup_size: int, *, nth
     return _cdiv(n, threadgroup_size)
 
 
+_NDIM: dict[int, tuple[IRModule, int]] = {}
+
+
+def grid_ndim(ir: IRModule) -> int:
+    """Highest axis used by ``program_id``/``thread_id`` plus one.  An IR never changes
+    after tracing, so the scan runs once per IR (the entry holds the IR, keeping its id
+    unique); an unrolled matmul has tens of thousands of instructions."""
+    hit = _NDIM.get(id(ir))
+    if hit is not None and hit[0] is ir:
+        return hit[1]
+    axes = [int(i.args[0]) for i in ir.insts if i.op in ("program_id", "thread_id")]
+    ndim = max(axes, default=-1) + 1
+    if len(_NDIM) >= 4096:
+        _NDIM.clear()
+    _NDIM[id(ir)] = (ir, ndim)
+    return ndim
+
+
 def infer_grid(
     ir: IRModule,
     runtime_args: Mapping[str, Any],
@@ -53,8 +71,7 @@ def infer_grid(
     plus one.  Sources, in priority order: the trailing 2/3 dims of ``shape``,
     then scalar runtime args ``H``, ``W`` (and ``D``).
     """
-    axes = [int(i.args[0]) for i in ir.insts if i.op in ("program_id", "thread_id")]
-    ndim = max(axes, default=-1) + 1
+    ndim = grid_ndim(ir)
     if ndim <= 1:
         return None
     if ndim > 3:

@@ -186,6 +186,7 @@ class HipRuntime:
         self._arg_specs: dict[int, tuple[IRModule, frozenset[str], tuple[tuple[str, bool, DType, bool], ...]]] = {}
         self._arch_checked = ext is not None
         self._cus = 256
+        self._plans: dict[tuple[Any, ...], tuple[Any, LaunchPlan | None, list[bytes]]] = {}
 
     # -- plumbing ------------------------------------------------------------
     def is_available(self) -> bool:
@@ -352,15 +353,13 @@ class HipRuntime:
         shape: tuple[int, ...] | None = None,
     ) -> None:
         _ = meta
-        self._mod()
-        plan = plan_launch(ck, runtime_args, nthreads=nthreads, grid=grid, tptg=tptg, shape=shape,
-                           compute_units=self._cus)
+        mod = self._mod()
+        plan, hidden = self._plan(ck, runtime_args, nthreads, grid, tptg, shape)
         if plan is None:
             return
         argv, writable, copy_back, stream = self.build_argv(ck.ir, runtime_args, ck.writes)
-        argv += [struct.pack("<I", h) for h in plan.hidden]
-        writable += [False] * len(plan.hidden)
-        mod = self._mod()
+        argv += hidden
+        writable += [False] * len(hidden)
         kernel = self.kernel_handle(ck, plan.entry)
         if sync or copy_back:
             mod.launch_groups(kernel, argv, writable, plan.grid, plan.block, stream=stream)
@@ -371,6 +370,32 @@ class HipRuntime:
         limit = self._max_pending()
         while limit and len(self._pending) > limit:
             mod.synchronize(self._pending.popleft())
+
+    def _plan(self, ck: Any, runtime_args: Mapping[str, Any], nthreads: int | None, grid: Any, tptg: Any,
+              shape: Any) -> tuple[LaunchPlan | None, list[bytes]]:
+        """The launch plan and its packed hidden arguments.  An SPMD or thread-mode plan
+        depends only on the kernel, the launch options and the scalars that size the grid
+        (``N``, ``H``, ``W``, ``D``), so it is cached on those; a lifted GEMM's plan also
+        checks its buffers' sizes and addresses and is made afresh each time."""
+        geo = ck.geometry
+        key = None
+        if geo is not None and geo.kind != "gemm":
+            key = (id(ck), nthreads, grid, tptg, shape, runtime_args.get("N"), runtime_args.get("H"),
+                   runtime_args.get("W"), runtime_args.get("D"))
+            try:
+                hit = self._plans.get(key)
+            except TypeError:  # an unhashable value: plan without the cache
+                key, hit = None, None
+            if hit is not None and hit[0] is ck:
+                return hit[1], hit[2]
+        plan = plan_launch(ck, runtime_args, nthreads=nthreads, grid=grid, tptg=tptg, shape=shape,
+                           compute_units=self._cus)
+        hidden = [] if plan is None else [struct.pack("<I", h) for h in plan.hidden]
+        if key is not None:
+            if len(self._plans) >= 4096:
+                self._plans.clear()
+            self._plans[key] = (ck, plan, hidden)  # holding ck keeps its id unique
+        return plan, hidden
 
     def synchronize(self) -> None:
         mod = self._hip
