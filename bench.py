@@ -173,9 +173,23 @@ def _torch_event_ms(fn, steps: int, warmup: int, torch) -> float:
     return sorted(trials)[EVENT_TRIALS // 2]
 
 
+# --shape M,N,K: the same kernel and input distributions at another shape (for scaling
+# studies such as the K sweep behind a GEMM's time budget; not a metric configuration)
+SHAPE_OVERRIDE: dict[str, tuple[int, int, int]] = {}
+
+
+def _config(name: str) -> tuple:
+    """(kernel, M, N, K, A distribution, B distribution, description) of a matmul workload."""
+    kname, m, n, k, da, db, desc = MATMULS[name]
+    if name in SHAPE_OVERRIDE:
+        m, n, k = SHAPE_OVERRIDE[name]
+        desc = f"{desc.split(',')[0]}, shape override M={m} N={n} K={k} (not the configuration's shape)"
+    return kname, m, n, k, da, db, desc
+
+
 def _matmul_inputs(name: str, torch) -> tuple[object, object]:
     """Host inputs: NumPy arrays, or torch bfloat16 CPU tensors (NumPy has no bfloat16)."""
-    _, m, n, k, da, db, _ = MATMULS[name]
+    _, m, n, k, da, db, _ = _config(name)
     rng_a, rng_b = np.random.default_rng(10), np.random.default_rng(11)
 
     def draw(rng, dist, size):
@@ -202,7 +216,7 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded",
     with ``cpu_baseline``, also time the reference's CPU expression on the same operands."""
     import kernels as K
 
-    kname, m, n, k, _, _, desc = MATMULS[name]
+    kname, m, n, k, _, _, desc = _config(name)
     kern = getattr(K, kname)
     dev = torch.device("cuda:0")
     ha, hb = _matmul_inputs(name, torch)
@@ -289,6 +303,122 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded",
     del a, b, c
     torch.cuda.empty_cache()
     return res
+
+
+# --phases: in-kernel timestamps of the 8-wave GEMM entry.  s_memrealtime counts a constant
+# 100 MHz clock; hardware register XCC_ID (id 20, bits 0-3) names the XCD a workgroup runs on.
+_PHASE_SLOTS = 8  # per wave group: entry, loop start, loop end, stores issued, stores done, XCD id
+_PHASE_STAMP = (
+    "#define EAS_STAMP(slot) do { if (threadIdx.x == 0 || threadIdx.x == 256) "
+    "__eas_stamps[(blockIdx.x * 2u + (threadIdx.x >> 8)) * 8u + (slot)] = __builtin_amdgcn_s_memrealtime(); "
+    "} while (0)\n"
+    "#define EAS_STAMP_XCD() do { if (threadIdx.x == 0 || threadIdx.x == 256) "
+    "__eas_stamps[(blockIdx.x * 2u + (threadIdx.x >> 8)) * 8u + 5u] = "
+    "(unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u); } while (0)\n")
+
+
+def _stamped_pp_source(src: str, entry: str) -> str:
+    """The generated GEMM source with a stamp buffer appended to the 8-wave entry's arguments and
+    stamps written (lane 0 of waves 0 and 4) at five points of ``eas_gemm_pp``: entry, start of the
+    K loop (prologue DMA landed), end of the K loop, C stores issued, C stores complete.  Raises if
+    the source does not have the expected shape (16 x 16 x 32 MFMA body, one 8-wave entry)."""
+    src = src.split("\n", 1)[1]  # the eas-launch line describes the unstamped argument list
+    body = ("eas_op_t* smem) {\n  constexpr int BM = 256, BN = 256, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;\n"
+            "  constexpr int STAGE_H = BM * BK;\n  eas_op_t* As = smem;\n  eas_op_t* Bs = smem + NSTAGE * STAGE_H;\n"
+            "  const int tid = threadIdx.x, lane = tid & 63;\n"
+            "  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n  const int g = wave >> 2, p = wave & 3;\n")
+    edits = [
+        (body, body.replace("eas_op_t* smem) {", "eas_op_t* smem, unsigned long long* __eas_stamps) {")
+         + "  EAS_STAMP(0);\n  EAS_STAMP_XCD();\n"),
+        ("  if (g == 1) __syncthreads();\n  for (int kt = 0; kt < KT; ++kt) {",
+         "  if (g == 1) __syncthreads();\n  EAS_STAMP(1);\n  for (int kt = 0; kt < KT; ++kt) {"),
+        ("  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier\n",
+         "  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier\n  EAS_STAMP(2);\n"),
+        ("(CT)acc16[i][j][r];\n        }\n  }\n}",
+         "(CT)acc16[i][j][r];\n        }\n  }\n  EAS_STAMP(3);\n  __builtin_amdgcn_s_waitcnt(0);\n"
+         "  EAS_STAMP(4);\n}"),
+        ("eas_gemm_pp<CT, K, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);",
+         "eas_gemm_pp<CT, K, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem, __eas_stamps);"),
+    ]
+    for old, new in edits:
+        if src.count(old) != 1:
+            raise RuntimeError(f"--phases: unexpected GEMM source shape at {old[:48]!r}")
+        src = src.replace(old, new)
+    head = src.index(f"void {entry}(")
+    close = src.index(") {", head)
+    src = src[:close] + ",\n    unsigned long long* __restrict__ __eas_stamps" + src[close:]
+    return _PHASE_STAMP + src
+
+
+def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
+    """Per-phase time budget of one launch of the 8-wave GEMM entry on the configuration's seeded
+    inputs: after settling, ``trials`` times run ``lead`` launches back to back and one more, and
+    read the last launch's stamps.  Medians over the trials of: spread of workgroup starts,
+    prologue, K loop (median, min, max over wave groups, median per XCD), C store issue, store
+    completion, median and last end; all in microseconds from the first workgroup's start."""
+    import kernels as K
+    from easy_as_amd.runtime.hip import compile_code, plan_launch, struct
+
+    kname, m, n, k, _, _, _ = _config(name)
+    dev = torch.device("cuda:0")
+    ha, hb = _matmul_inputs(name, torch)
+    a, b = (x.to(dev) if isinstance(x, torch.Tensor) else torch.from_numpy(x).to(dev) for x in (ha, hb))
+    out_dt = torch.float32 if kname in ("matmul_mma_kernel", "matmul_mma_bf16_kernel") else torch.float16
+    c = torch.zeros(m * n, dtype=out_dt, device=dev)
+    ck = getattr(K, kname).compile(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512)
+    args = {"a": a, "b": b, "c": c, "M": m, "N": n}
+    mod = rt._mod()
+    plan = plan_launch(ck, args, grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), compute_units=rt._cus)
+    if plan is None or not plan.entry.endswith("__pp"):
+        raise RuntimeError(f"--phases needs the 8-wave GEMM entry; {name} launches {plan and plan.entry}")
+    kern = mod.load(compile_code(mod, _stamped_pp_source(ck.src, plan.entry), ck.ir.name), plan.entry)
+    groups = plan.grid[0] * plan.grid[1] * plan.grid[2]
+    stamps = torch.zeros(groups * 2 * _PHASE_SLOTS, dtype=torch.int64, device=dev)
+    argv, writable, _, stream = rt.build_argv(ck.ir, args, ck.writes)
+    argv += [struct.pack("<I", h) for h in plan.hidden] + [mod.wrap_pointer(stamps.data_ptr(), stamps.nbytes,
+                                                                            stamps)]
+    writable += [False] * len(plan.hidden) + [True]
+
+    def launches(count: int) -> None:
+        for _ in range(count):
+            mod.launch_groups_async(kern, argv, writable, plan.grid, plan.block, stream=stream)
+
+    def batch() -> float:
+        t0 = time.perf_counter()
+        launches(SETTLE_BATCH)
+        rt.synchronize()
+        return time.perf_counter() - t0
+
+    _settle_until_stable(batch, plan.entry + " (stamped)")
+    runs = []
+    for _ in range(trials):
+        launches(lead + 1)
+        rt.synchronize()
+        s = stamps.cpu().numpy().reshape(groups, 2, _PHASE_SLOTS)
+        xcd = s[:, 0, 5].astype(np.int64)
+        t = s[:, :, :5].astype(np.float64) * 0.01  # 100 MHz ticks -> us
+        t -= t[:, :, 0].min()
+        loop = t[:, :, 2] - t[:, :, 1]
+        runs.append({
+            "start_spread": t[:, :, 0].max(), "prologue": np.median(t[:, :, 1] - t[:, :, 0]),
+            "loop_median": np.median(loop), "loop_min": loop.min(), "loop_max": loop.max(),
+            "store_issue": np.median(t[:, :, 3] - t[:, :, 2]), "store_complete": np.median(t[:, :, 4] - t[:, :, 3]),
+            "end_median": np.median(t[:, :, 4]), "end_last": t[:, :, 4].max(),
+            "loop_median_per_xcd": [float(np.median(loop[xcd == x])) if (xcd == x).any() else None
+                                    for x in range(8)],
+            "workgroup_to_xcd_is_modulo_8": bool((xcd == np.arange(groups) % 8).all()),
+        })
+    out = {key: round(float(np.median([r[key] for r in runs])), 2) for key in runs[0]
+           if not isinstance(runs[0][key], (list, bool))}
+    out["loop_median_per_xcd"] = [round(float(np.median([r["loop_median_per_xcd"][x] for r in runs])), 2)
+                                  for x in range(8) if runs[0]["loop_median_per_xcd"][x] is not None]
+    out["workgroup_to_xcd_is_modulo_8"] = all(r["workgroup_to_xcd_is_modulo_8"] for r in runs)
+    out.update({"unit": "us", "entry": plan.entry, "workgroups": groups, "trials": trials,
+                "method": f"median over {trials} trials of the last of {lead + 1} back-to-back launches; "
+                          "s_memrealtime stamps by lane 0 of each wave group"})
+    del a, b, c, stamps
+    torch.cuda.empty_cache()
+    return out
 
 
 def _host_info() -> dict:
@@ -438,12 +568,30 @@ def main() -> int:
     p.add_argument("--block", type=int, default=PRIMARY_BLOCK)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
+    p.add_argument("--shape", default=None,
+                   help="matmul workloads only: M,N,K instead of the configuration's shape (a scaling study, "
+                        "not the metric)")
+    p.add_argument("--phases", action="store_true",
+                   help="matmul workloads on the 8-wave GEMM entry: add an in-kernel per-phase time budget "
+                        "of one launch (a stamped copy of the kernel, timed after the measurement)")
     p.add_argument("--data", choices=MATMUL_DATA, default="seeded",
                    help="matmul workloads only: input data (anything but 'seeded' is not the metric's data)")
     args = p.parse_args()
     if args.data != "seeded" and args.workload not in MATMULS:
         print("--data applies to the matmul workloads only", file=sys.stderr)
         return 2
+    if args.phases and args.workload not in MATMULS:
+        print("--phases applies to the matmul workloads only", file=sys.stderr)
+        return 2
+    if args.shape is not None:
+        if args.workload not in MATMULS:
+            print("--shape applies to the matmul workloads only", file=sys.stderr)
+            return 2
+        dims = tuple(int(x) for x in args.shape.split(","))
+        if len(dims) != 3 or min(dims) <= 0:
+            print("--shape takes M,N,K (positive)", file=sys.stderr)
+            return 2
+        SHAPE_OVERRIDE[args.workload] = dims
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
               "(the elementwise path would shard N contiguously per GPU with no exchange).", file=sys.stderr)
@@ -607,10 +755,10 @@ def main() -> int:
 def _matmul_main(args, rt, torch) -> int:
     res = _matmul(args.workload, rt, torch, args.steps, args.warmup, args.data,
                   cpu_baseline=not args.no_cpu_baseline)
-    _, m, n, k, _, _, desc = MATMULS[args.workload]
+    _, m, n, k, _, _, desc = _config(args.workload)
     traffic = None
     pmc = ROOT / "profiles" / f"{MATMUL_PROFILES.get(args.workload, args.workload)}.pmc.json"
-    if pmc.exists():
+    if pmc.exists() and args.workload not in SHAPE_OVERRIDE:
         traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
     tiled = args.workload.startswith("tiled")
     in_dt = "f32" if tiled else ("bf16" if args.workload.endswith("bf16") else "f16")
@@ -642,6 +790,9 @@ def _matmul_main(args, rt, torch) -> int:
                    "rule": f"batches of {SETTLE_BATCH} until two agree within 2%"},
         "extra": {},
     }
+    if args.phases:
+        line["phases"] = _gemm_phases(args.workload, rt, torch)
+        _log(f"{args.workload}: phases {json.dumps(line['phases'])}")
     print(json.dumps(line), flush=True)
     return 0 if res["parity_ok"] else 1
 

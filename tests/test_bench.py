@@ -1,0 +1,108 @@
+"""bench.py's command line and its GEMM phase-stamp instrumentation.
+
+The CPU tests check argument handling and that the stamped copy of each 8-wave GEMM source is
+built (the edits find their anchors in the generated source, and hiprtc compiles the result);
+the GPU test runs the stamped kernel once at a short K and checks the phases it reports."""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT))
+
+import bench  # noqa: E402
+import kernels as K  # noqa: E402
+
+
+def _main(monkeypatch, *argv: str) -> int:
+    monkeypatch.setattr(sys, "argv", ["bench.py", *argv])
+    return bench.main()
+
+
+@pytest.mark.parametrize("argv", [
+    ("--gpus", "2"),
+    ("--workload", "add", "--shape", "64,64,64"),
+    ("--workload", "mma", "--shape", "64,64"),
+    ("--workload", "mma", "--shape", "64,0,64"),
+    ("--workload", "add", "--phases"),
+    ("--workload", "add", "--data", "ones"),
+])
+def test_refused_arguments_exit_2(monkeypatch, argv):
+    assert _main(monkeypatch, *argv) == 2
+
+
+def test_shape_override_changes_only_the_shape(monkeypatch):
+    monkeypatch.setitem(bench.SHAPE_OVERRIDE, "mma", (4096, 4096, 512))
+    kname, m, n, k, da, db, desc = bench._config("mma")
+    assert (kname, m, n, k, da, db) == ("matmul_mma_kernel", 4096, 4096, 512, "u", "u")
+    assert "shape override" in desc and "K=512" in desc
+    assert bench._config("prefill")[1:4] == (8192, 8192, 8192)
+
+
+def _pp_source(name: str):
+    import torch
+
+    from easy_as_amd.runtime.hip import plan_launch
+
+    kname, m, n, k, *_ = bench._config(name)
+    dt = torch.bfloat16 if name.endswith("bf16") else torch.float16
+    a, b = torch.empty(m * k, dtype=dt), torch.empty(k * n, dtype=dt)
+    c = torch.empty(m * n, dtype=torch.float16 if name == "prefill" else torch.float32)
+    ck = getattr(K, kname).compile(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512)
+    plan = plan_launch(ck, {"a": a, "b": b, "c": c, "M": m, "N": n},
+                       grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), compute_units=256)
+    return ck, plan
+
+
+@pytest.mark.parametrize("name", ["mma", "prefill", "mma_bf16"])
+def test_stamped_source_finds_every_anchor(name):
+    ck, plan = _pp_source(name)
+    assert plan.entry.endswith("__pp")
+    src = bench._stamped_pp_source(ck.src, plan.entry)
+    for slot in range(5):
+        assert f"EAS_STAMP({slot});" in src
+    assert "EAS_STAMP_XCD();" in src and "__eas_stamps) {" in src
+    assert not src.startswith("// eas-launch")  # the stamped copy has one more argument
+
+
+def test_stamped_source_compiles():
+    from easy_as_amd.runtime.hip import compile_code
+    from easy_as_amd.runtime.hip_ext import load_hip_ext
+
+    mod = load_hip_ext(require=False)
+    if mod is None:
+        pytest.skip("the _hip extension is not built")
+    ck, plan = _pp_source("mma")
+    code = compile_code(mod, bench._stamped_pp_source(ck.src, plan.entry), ck.ir.name)
+    assert code[:4] == b"\x7fELF"
+
+
+def test_stamped_source_rejects_an_unexpected_shape():
+    ck, plan = _pp_source("mma")
+    with pytest.raises(RuntimeError, match="unexpected GEMM source shape"):
+        bench._stamped_pp_source(ck.src.replace("  if (g == 1) __syncthreads();\n  for (int kt", "  for (int kt"),
+                                 plan.entry)
+
+
+@pytest.mark.gpu
+def test_phases_of_a_short_k_launch(monkeypatch):
+    import torch
+
+    from easy_as_amd.runtime import get_runtime
+
+    monkeypatch.setitem(bench.SHAPE_OVERRIDE, "mma", (4096, 4096, 512))
+    print("phases: mma 4096 x 4096 x 512", flush=True)
+    ph = bench._gemm_phases("mma", get_runtime("hip"), torch, trials=2, lead=3)
+    assert ph["entry"] == "matmul_mma_kernel__pp" and ph["workgroups"] == 256
+    assert ph["workgroup_to_xcd_is_modulo_8"] is True
+    assert len(ph["loop_median_per_xcd"]) == 8
+    assert 0 < ph["prologue"] < ph["loop_median"] < ph["end_median"] <= ph["end_last"]
+    assert ph["loop_min"] <= ph["loop_median"] <= ph["loop_max"]
+    assert ph["store_issue"] > 0 and ph["store_complete"] >= 0
+    # 16 stages of BK = 32: a few microseconds of loop, well under a millisecond
+    assert np.isfinite(ph["end_last"]) and ph["end_last"] < 1000
