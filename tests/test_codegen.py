@@ -271,6 +271,44 @@ def test_f16_fma_keeps_two_roundings_in_the_code_object(tmp_path, spmd):
     assert "v_fma_mixlo_f16" not in asm and "v_fma_mixhi_f16" not in asm
     assert "v_cvt_f16_f32" in asm
 
+
+@pytest.mark.parametrize("spmd", [False, True])
+def test_f16_conversion_of_an_f32_product_rounds_twice_in_the_code_object(tmp_path, spmd):
+    # to_f16(a * b) with f32 a, b: the product rounds to binary32, then to binary16.  Without the
+    # conversion helper LLVM folds the multiply into v_fma_mixlo_f16 / v_mad_mixlo_f16 (one
+    # rounding of the exact product), which a random-program test found differing on the GPU.
+    import os
+    import subprocess
+
+    from easy_as_amd.runtime.hip import COMPILE_OPTIONS
+    from easy_as_amd.runtime.hip_ext import load_hip_ext
+
+    if not os.path.exists(_OBJDUMP):
+        pytest.skip("llvm-objdump not installed")
+
+    @eas.kernel
+    def spmd_narrow(a, b, d, N, BLOCK: eas.constexpr):
+        offs = mk.program_id(0) * BLOCK + mk.arange(0, BLOCK)
+        m = offs < N
+        mk.store(d, offs, mk.to_f16(mk.load(a, offs, m) * mk.load(b, offs, m)), m)
+
+    @eas.kernel
+    def thread_narrow(a, b, d, N, BLOCK: eas.constexpr):
+        i = mk.tid(0, BLOCK)
+        m = i < N
+        mk.store(d, i, mk.to_f16(mk.load(a, i, m) * mk.load(b, i, m)), m)
+
+    f = np.zeros(256, np.float32)
+    ck = (spmd_narrow if spmd else thread_narrow).compile(f, f, _h(256), 256, BLOCK=256)
+    assert "eas_f32_to_f16(" in ck.src
+    code = load_hip_ext(require=True).compile_to_code(ck.src, "narrow.hip", list(COMPILE_OPTIONS))
+    path = tmp_path / "k.co"
+    path.write_bytes(code)
+    asm = subprocess.run([_OBJDUMP, "-d", "--mcpu=gfx950", str(path)], capture_output=True, text=True,
+                         check=True).stdout
+    assert not re.search(r"v_(fma|mad)_mix(lo|hi)_f16", asm)
+    assert "v_cvt_f16_f32" in asm and "v_mul_f32" in asm
+
 # ---- bfloat16 (an addition to the reference's dtypes) ---------------------------
 
 def test_bf16_buffers_lower_to_bf16_pointers_and_f32_arithmetic():
@@ -284,7 +322,7 @@ def test_bf16_buffers_lower_to_bf16_pointers_and_f32_arithmetic():
     assert "eas_bf16x8" in ck.src
     ck = K.bf16_convert_kernel.compile(np.zeros(64, np.float32), torch.zeros(64, dtype=torch.bfloat16),
                                        np.zeros(64, np.float32), 64, BLOCK=64)
-    assert "((__bf16)(v" in ck.src and "((float)(v" in ck.src
+    assert "eas_f32_to_bf16(v" in ck.src and "((float)(v" in ck.src
 
 
 def test_bf16_mma_lifts_to_bf16_mfma():

@@ -11,6 +11,7 @@ test_dot_dynamic_k.py, test_kernel_cache.py, test_tensor.py, test_torch_interop.
 from __future__ import annotations
 
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -114,6 +115,31 @@ def test_unfused_mul_add_rounds_twice(gpu_runtime):
     prod = (a * b).astype(np.float32)
     assert _bits_equal(d, (prod + c).astype(np.float32))
     assert _bits_equal(e, prod)
+
+
+def test_subnormal_results_are_not_flushed(gpu_runtime):
+    """f32 subnormals are kept (the HIP build uses no fast-math and no flush to zero): products
+    below 2^-126 and sums with subnormal addends equal NumPy's IEEE binary32 results bit for bit,
+    and the fma corner fixture (subnormal inputs and outputs, signed zeros, NaN) matches on the
+    GPU, NaN for NaN."""
+    rng = np.random.default_rng(21)
+    n = 4099
+
+    def scaled(lo: int, hi: int) -> np.ndarray:
+        return (rng.uniform(1, 2, n) * np.exp2(rng.integers(lo, hi, n)) * rng.choice([-1.0, 1.0], n)).astype(np.float32)
+
+    a, b, c = scaled(-75, -55), scaled(-75, -55), scaled(-149, -126)
+    prod = a * b
+    assert np.count_nonzero((prod != 0) & (np.abs(prod) < np.finfo(np.float32).tiny)) > n // 4
+    d, e = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    K.multi_use_mul_kernel(a, b, c, d, e, n, BLOCK=128)
+    assert _bits_equal(e, prod)
+    assert _bits_equal(d, prod + c)
+    g = np.load(Path(__file__).parent / "golden" / "fma_f32_corners.npz")
+    out = np.zeros_like(g["d"])
+    K.fma_kernel(g["a"], g["b"], g["c"], out, len(out), BLOCK=256)
+    nan = np.isnan(g["d"])
+    assert np.array_equal(np.isnan(out), nan) and _bits_equal(out[~nan], g["d"][~nan])
 
 
 def test_axpy_scalar_runtime_arg_and_cache(gpu_runtime):
