@@ -4,10 +4,12 @@
 over the public DSL (the ops of ``eas/mk.py`` the reference defines: ``+``, ``*``, ``//``, ``%``,
 ``<``, ``&``, ``|``, ``~``, ``where``, ``fma``, ``to_f16``, ``to_f32``, masked ``load`` /
 ``store``, and in thread mode ``tid``, ``local_id``, ``lane_id``, ``sg_id``, ``alloc_tg`` and
-``barrier``).  ``build(src)`` turns it into a kernel and ``inputs(seed, mode)`` gives matching
-host arguments.  Every index a kernel computes stays inside its buffers (gathers are reduced
-``% N``; threadgroup slots ``% BLOCK``), every divisor is a literal >= 1, and the f32 values
-come from N(0,1) inputs, so each program has one defined result for the oracle to give.
+``barrier`` and ``dot``), with runtime f32 and u32 scalars and, for some SPMD kernels, a 2-D
+grid.  ``case(seed)`` gives a kernel source and its launch, ``build(src)`` the kernel and
+``inputs(seed, n)`` the arguments.  Every index a kernel computes stays inside its buffers
+(gathers are reduced ``% N``, threadgroup slots ``% BLOCK``, dot windows ``% 1800`` with N >=
+2048), every divisor is a literal >= 1, and the f32 values come from N(0,1) inputs, so each
+program has one defined result for the oracle to give.
 """
 
 from __future__ import annotations
@@ -140,6 +142,8 @@ class _Gen:
 
 
 def _loads(g: _Gen, index: str, mask: str, nvar: str) -> None:
+    g.f.append("alpha")  # runtime f32 scalar
+    g.u.append("S")  # runtime u32 scalar
     g.lines += [
         f"    a = mk.load(x, {index}, {mask})",
         f"    b = mk.load(y, {index}, {mask})",
@@ -169,16 +173,31 @@ def _stores(g: _Gen, index: str, mask: str) -> None:
     g.lines.append(f"    mk.store(out16, {index}, {h_out}, {mask})")
 
 
-def spmd_source(seed: int, n_stmts: int = 20) -> str:
-    """An SPMD (``mk.arange``) kernel ``fuzz(x, y, z, h, out, out16, N, BLOCK)``."""
+SIGNATURE = "def fuzz(x, y, z, h, out, out16, N, alpha, S, BLOCK: eas.constexpr):"
+
+
+def spmd_source(seed: int, n_stmts: int = 20, grid_x: int = 0) -> str:
+    """An SPMD (``mk.arange``) kernel ``fuzz(x, y, z, h, out, out16, N, alpha, S, BLOCK)``.  With
+    ``grid_x`` > 0 the programs form a 2-D grid of ``grid_x`` columns (launch with ``_grid``) and
+    program (px, py) covers block py * grid_x + px."""
     g = _Gen(random.Random(seed))
-    g.lines = ["def fuzz(x, y, z, h, out, out16, N, BLOCK: eas.constexpr):",
-               "    pid = mk.program_id(0)",
+    pid = "mk.program_id(0)" if grid_x <= 0 else f"mk.program_id(1) * {grid_x} + mk.program_id(0)"
+    g.lines = [SIGNATURE,
+               f"    pid = {pid}",
                "    offs = pid * BLOCK + mk.arange(0, BLOCK)",
                "    m = offs < N"]
     g.u.append("pid")
     _loads(g, "offs", "m", "N")
-    g.body(n_stmts)
+    g.body(n_stmts // 2)
+    if g.r.random() < 0.3:
+        # lanes of one program exchange a value through threadgroup memory
+        g.lines += ["    lanes = mk.arange(0, BLOCK)",
+                    "    tgs = mk.alloc_tg(BLOCK)",
+                    f"    mk.store(tgs, lanes, {g.pick(g.f)})",
+                    "    mk.barrier()",
+                    f"    xs = mk.load(tgs, (lanes * {g.r.choice((1, 3, 5, 7, 33))} + {g.r.randrange(64)}) % BLOCK)"]
+        g.f.append("xs")
+    g.body(n_stmts - n_stmts // 2)
     _stores(g, "offs", "m")
     return "\n".join(g.lines) + "\n"
 
@@ -189,7 +208,7 @@ def thread_source(seed: int, n_stmts: int = 20, exchange: bool | None = None) ->
     of the group (``(lid * p + q) % BLOCK``) between two barriers."""
     r = random.Random(seed)
     g = _Gen(r)
-    g.lines = ["def fuzz(x, y, z, h, out, out16, N, BLOCK: eas.constexpr):",
+    g.lines = [SIGNATURE,
                "    i = mk.tid(0, BLOCK)",
                "    m = i < N",
                "    lid = mk.local_id(0)",
@@ -206,6 +225,14 @@ def thread_source(seed: int, n_stmts: int = 20, exchange: bool | None = None) ->
                     "    mk.barrier()",
                     f"    xr = mk.load(tg, (lid * {mult} + {r.randrange(64)}) % BLOCK)"]
         g.f.append("xr")
+    for _ in range(r.randrange(3)):
+        # a per-thread dot product over a strided window of two buffers (f32 or f16 operands);
+        # bases are reduced % 1800 and spans stay < 200, so every index is < N (N >= 2048)
+        ka, kb = r.choice(("x", "y", "z", "h")), r.choice(("x", "y", "z", "h"))
+        base_a = f"({g.pick(g.u)} * {r.choice(_U_LITS)}) % 1800"
+        base_b = f"({g.pick(g.u)} + {r.randrange(100)}) % 1800"
+        kd = r.randrange(1, 40)
+        g.emit(g.f, f"mk.dot({ka}, {base_a}, {r.randrange(1, 5)}, {kb}, {base_b}, {r.randrange(0, 5)}, {kd})")
     g.body(n_stmts - n_stmts // 2)
     _stores(g, "i", "m")
     return "\n".join(g.lines) + "\n"
@@ -218,24 +245,38 @@ def build(src: str):
     return eas.kernel(ns["fuzz"])
 
 
-def inputs(seed: int, n: int) -> tuple[np.ndarray, ...]:
-    """x, y, z ~ N(0,1) f32, h ~ N(0,1) f16, out and out16 zero."""
+def inputs(seed: int, n: int) -> tuple:
+    """x, y, z ~ N(0,1) f32, h ~ N(0,1) f16, out and out16 zero, then N, alpha (an f32 scalar)
+    and S (a u32 scalar)."""
     rng = np.random.default_rng(seed)
     x, y, z = (rng.standard_normal(n, dtype=np.float32) for _ in range(3))
     h = rng.standard_normal(n, dtype=np.float32).astype(np.float16)
-    return x, y, z, h, np.zeros(n, np.float32), np.zeros(n, np.float16)
+    alpha = float(np.float32(rng.uniform(0.25, 4.0)))
+    return x, y, z, h, np.zeros(n, np.float32), np.zeros(n, np.float16), n, alpha, int(rng.integers(0, 5000))
 
 
-def case(seed: int) -> tuple[str, int, int]:
-    """(mode, N, BLOCK) of fuzz case ``seed``: thread-mode kernels with threadgroup exchange get
-    N a multiple of BLOCK (a partial last group would read slots no thread wrote)."""
+def case(seed: int) -> dict:
+    """Launch of fuzz case ``seed``: ``mode``, ``N``, ``BLOCK``, the kernel ``src`` and the call's
+    ``options`` (``_grid`` for a 2-D SPMD grid).  Thread-mode kernels get N a multiple of BLOCK
+    (a partial last group would read threadgroup slots no thread wrote) and N >= 2048 (the dot
+    windows)."""
     r = random.Random(10_000 + seed)
     mode = "spmd" if seed % 2 == 0 else "thread"
     block = r.choice((64, 128, 256))
     n = r.randrange(1, 9000)
+    options: dict = {}
     if mode == "thread":
-        n = max(block, n - n % block)
-    return mode, n, block
+        n = max(2048, n - n % block)
+        src = thread_source(seed)
+    elif seed % 4 == 2:
+        # 2-D grid: enough programs for N, laid out grid_x wide
+        grid_x = r.choice((1, 2, 3, 5))
+        programs = -(-n // block)
+        options["_grid"] = (grid_x, -(-programs // grid_x), 1)
+        src = spmd_source(seed, grid_x=grid_x)
+    else:
+        src = spmd_source(seed)
+    return {"mode": mode, "N": n, "BLOCK": block, "src": src, "options": options}
 
 
 def same_values(got: np.ndarray, want: np.ndarray) -> bool:

@@ -19,20 +19,22 @@ CPU_SEEDS = range(24)
 GPU_SEEDS = range(200)
 
 
-def _args(seed: int):
-    mode, n, block = F.case(seed)
-    src = F.spmd_source(seed) if mode == "spmd" else F.thread_source(seed)
-    return mode, n, block, src
 
 
 def test_generator_is_deterministic_and_varied():
-    assert F.spmd_source(3) == F.spmd_source(3) and F.thread_source(4) == F.thread_source(4)
-    srcs = {F.spmd_source(s) for s in range(20)}
-    assert len(srcs) == 20
-    joined = "".join(srcs) + "".join(F.thread_source(s) for s in range(20))
+    assert F.case(3) == F.case(3) and F.case(4) == F.case(4)
+    cases = [F.case(s) for s in range(40)]
+    assert len({c["src"] for c in cases}) == 40
+    joined = "".join(c["src"] for c in cases)
     for op in ("mk.fma(", "mk.where(", "mk.to_f16(", "mk.to_f32(", " // ", " % ", " < ", " & ", " | ", "~",
-               "mk.barrier()", "mk.alloc_tg(", "mk.lane_id()", "mk.sg_id()"):
+               "mk.barrier()", "mk.alloc_tg(", "mk.lane_id()", "mk.sg_id()", "mk.dot(", "mk.program_id(1)",
+               "alpha", " S", "tgs = mk.alloc_tg(BLOCK)"):
         assert op in joined, op
+    assert any(c["options"].get("_grid") for c in cases)
+
+
+def _run_oracle(c: dict, args: tuple) -> dict:
+    return interp.run_kernel(F.build(c["src"]), *args, BLOCK=c["BLOCK"], **c["options"])
 
 
 @pytest.mark.parametrize("seed", CPU_SEEDS)
@@ -40,13 +42,13 @@ def test_random_program_compiles_and_runs_in_the_oracle(seed):
     from easy_as_amd.runtime.hip import compile_code
     from easy_as_amd.runtime.hip_ext import load_hip_ext
 
-    mode, n, block, src = _args(seed)
-    k = F.build(src)
-    x, y, z, h, out, out16 = F.inputs(seed, n)
-    ck = k.compile(x, y, z, h, out, out16, n, BLOCK=block)
-    assert ck.launch_mode == mode
-    ref = interp.run_kernel(k, x, y, z, h, out, out16, n, BLOCK=block)
-    assert ref["out"].shape == (n,) and ref["out16"].shape == (n,)
+    c = F.case(seed)
+    k = F.build(c["src"])
+    args = F.inputs(seed, c["N"])
+    ck = k.compile(*args, BLOCK=c["BLOCK"])
+    assert ck.launch_mode == c["mode"]
+    ref = _run_oracle(c, args)
+    assert ref["out"].shape == (c["N"],) and ref["out16"].shape == (c["N"],)
     mod = load_hip_ext(require=False)
     if mod is None:
         pytest.skip("the _hip extension is not built")
@@ -63,16 +65,16 @@ def test_same_values_treats_nans_alike_and_nothing_else():
 @pytest.mark.gpu
 @pytest.mark.parametrize("seed", GPU_SEEDS)
 def test_random_program_matches_the_oracle_on_the_gpu(seed, gpu_runtime):
-    mode, n, block, src = _args(seed)
-    print(f"fuzz seed {seed}: {mode} N={n} BLOCK={block}", flush=True)
-    k = F.build(src)
-    x, y, z, h, out, out16 = F.inputs(seed, n)
-    ref = interp.run_kernel(k, x, y, z, h, out, out16, n, BLOCK=block)
-    k(x, y, z, h, out, out16, n, BLOCK=block)
-    for name, got in (("out", out), ("out16", out16)):
+    c = F.case(seed)
+    print(f"fuzz seed {seed}: {c['mode']} N={c['N']} BLOCK={c['BLOCK']} {c['options']}", flush=True)
+    k = F.build(c["src"])
+    args = F.inputs(seed, c["N"])
+    ref = _run_oracle(c, args)
+    k(*args, BLOCK=c["BLOCK"], **c["options"])
+    for name, got in (("out", args[4]), ("out16", args[5])):
         if not F.same_values(got, ref[name]):
-            bad = np.flatnonzero(got.view(np.uint32 if got.dtype == np.float32 else np.uint16)
-                                 != ref[name].view(np.uint32 if got.dtype == np.float32 else np.uint16))
+            bits = np.uint32 if got.dtype == np.float32 else np.uint16
+            bad = np.flatnonzero(got.view(bits) != ref[name].view(bits))
             i = int(bad[0])
-            pytest.fail(f"seed {seed} ({mode}, N={n}, BLOCK={block}): {name}[{i}] = {got[i]!r}, oracle "
-                        f"{ref[name][i]!r}; {bad.size} elements differ\n{src}")
+            pytest.fail(f"seed {seed} ({c['mode']}, N={c['N']}, BLOCK={c['BLOCK']}, {c['options']}): {name}[{i}] = "
+                        f"{got[i]!r}, oracle {ref[name][i]!r}; {bad.size} elements differ\n{c['src']}")

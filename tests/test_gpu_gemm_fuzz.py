@@ -1,0 +1,89 @@
+"""Seeded random shapes through the lifted GEMMs, against float64.
+
+32 cases.  Each draws a kernel from the reference's workloads (f16-input simdgroup MMA with f32
+or f16 output, the bf16 variant, the fp32 threadgroup-tile kernel) and M, N, K from 1 to ~800 on a
+log scale, so the cases cover:
+* skinny and full-tile launches;
+* odd K (A rows not 4-byte aligned) and K below one stage;
+* N not a multiple of 4, and every entry the launch plan picks by itself.
+
+Every output is checked with the tolerances the parity bars state.  The output buffer is
+longer than M x N, and its tail must keep its sentinel (no write past C)."""
+
+from __future__ import annotations
+
+import math
+import random
+
+import numpy as np
+import pytest
+
+import kernels as K
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+CASES = range(32)
+KINDS = ("f16_f32", "f16_f16", "bf16_f32", "tiled_f32")
+PAD = 1031
+
+
+def _shape(seed: int) -> tuple[str, int, int, int]:
+    r = random.Random(50_000 + seed)
+    kind = KINDS[seed % len(KINDS)]
+
+    def dim(hi: int) -> int:
+        return max(1, int(round(math.exp(r.uniform(0.0, math.log(hi))))))
+
+    return kind, dim(800), dim(900), dim(700)
+
+
+def test_shapes_cover_the_edges():
+    shapes = [_shape(s) for s in CASES]
+    assert any(k % 2 for _, _, _, k in shapes) and any(n % 4 for _, _, n, _ in shapes)
+    assert any(m <= 16 for _, m, _, _ in shapes) and any(m > 256 for _, m, _, _ in shapes)
+    assert any(k < 32 for _, _, _, k in shapes) and {s[0] for s in shapes} == set(KINDS)
+
+
+@pytest.mark.parametrize("seed", CASES)
+def test_random_shape_matches_float64(gpu_runtime, seed):
+    torch = pytest.importorskip("torch")
+    kind, m, n, k = _shape(seed)
+    print(f"gemm fuzz {seed}: {kind} M={m} N={n} K={k}", flush=True)
+    rng = np.random.default_rng(seed)
+    if kind == "tiled_f32":
+        a = (rng.standard_normal(m * k, dtype=np.float32) / np.float32(math.sqrt(k))).astype(np.float32)
+        b = (rng.standard_normal(k * n, dtype=np.float32) / np.float32(math.sqrt(k))).astype(np.float32)
+        c = np.full(m * n + PAD, np.nan, np.float32)
+        bm, bn, bk, nt = (32, 32, 32, 256) if seed % 8 < 4 else (16, 64, 16, 256)
+        K.matmul_tiled_kernel(a, b, c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
+                              _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
+        ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
+        got, tail = c[:m * n], c[m * n:]
+        bar = 1e-5 * math.sqrt(k)
+    elif kind == "bf16_f32":
+        a_bits = ops.f32_to_bf16(rng.uniform(-1, 1, m * k).astype(np.float32))
+        b_bits = ops.f32_to_bf16(rng.uniform(-1, 1, k * n).astype(np.float32))
+        ta = torch.from_numpy(a_bits.view(np.int16)).view(torch.bfloat16)
+        tb = torch.from_numpy(b_bits.view(np.int16)).view(torch.bfloat16)
+        tc = torch.full((m * n + PAD,), float("nan"), dtype=torch.float32)
+        K.matmul_mma_bf16_kernel(ta, tb, tc, m, n, BM=32, BN=32, BK=8, K=k, NT=512, OUT16=False,
+                                 _grid=K.mma_grid, _tptg=(512, 1, 1))
+        ref = ops.matmul_ref(ops.bf16_to_f32(a_bits).reshape(m, k), ops.bf16_to_f32(b_bits).reshape(k, n))
+        c = tc.numpy()
+        got, tail = c[:m * n], c[m * n:]
+        bar = 1e-5 * math.sqrt(k)
+    else:
+        a = rng.uniform(-1, 1, m * k).astype(np.float16)
+        b = rng.uniform(-1, 1, k * n).astype(np.float16)
+        out16 = kind == "f16_f16"
+        c = np.full(m * n + PAD, np.nan, np.float16 if out16 else np.float32)
+        kern = K.matmul_mma_f16out_kernel if out16 else K.matmul_mma_kernel
+        kern(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512, _grid=K.mma_grid, _tptg=(512, 1, 1))
+        ref = ops.matmul_ref(a.reshape(m, k).astype(np.float32), b.reshape(k, n).astype(np.float32))
+        got, tail = c[:m * n], c[m * n:]
+        bar = 2e-3 if out16 else 1e-5 * math.sqrt(k)
+    assert np.isnan(tail).all(), f"{kind} M={m} N={n} K={k}: wrote past C"
+    assert np.isfinite(got).all(), f"{kind} M={m} N={n} K={k}: an output was not written"
+    err = ops.rel_err(np.asarray(got, np.float64).reshape(m, n), ref)
+    assert err <= min(2e-2, bar), f"{kind} M={m} N={n} K={k}: rel err {err:.3e} > {bar:.3e}"
