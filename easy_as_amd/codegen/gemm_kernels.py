@@ -1326,24 +1326,33 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
     __syncthreads();
     if (kt + NSTAGE - 1 < KT) dma(kt + NSTAGE - 1);
     const float* st = smem + (kt % NSTAGE) * STF;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {  // the stage's 16 steps in two halves of 8
-      eas_f32x4 a[2][2];
-      float b[2][8];
+    // the stage's 16 steps in four groups of four; the fragments of group u + 1 are read before
+    // the 16 MFMAs of group u issue, so that one wave per SIMD does not wait on LDS latency
+    // between groups (sched_barrier keeps the compiler from moving the reads back)
+    eas_f32x4 a[2][2];
+    float b[2][2][4];
+    auto read_group = [&](int u, int buf) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
+        a[buf][i] = *(const eas_f32x4*)(st + fa[i][u]);
 #pragma unroll
-        for (int u = 0; u < 2; ++u) a[i][u] = *(const eas_f32x4*)(st + fa[i][2 * h + u]);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) b[i][s] = st[fb[i][8 * h + s]];
+        for (int e = 0; e < 4; ++e) b[buf][i][e] = st[fb[i][4 * u + e]];
       }
+    };
+    read_group(0, 0);
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
+    for (int u = 0; u < 4; ++u) {
+      const int cur = u & 1;
+      if (u + 1 < 4) read_group(u + 1, cur ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s >> 2][s & 3], b[j][s], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][i][e], b[cur][j][e], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
