@@ -15,12 +15,31 @@ from __future__ import annotations
 import inspect
 from typing import Any, Callable, Mapping
 
+import numpy as np
+
 from .autotune import AutotuneSpec, Config
-from .compiler import CompiledKernel, _arg_key, compile as _compile
+from .compiler import CompiledKernel, _arg_key, _torch, compile as _compile
 from .meta import constexpr
 from .runtime import get_runtime
 
 _OPTION_NAMES = ("_sync", "_shape", "_grid", "_tptg", "_nthreads")
+_MEMO_LIMIT = 64
+
+
+def _light_key(v: Any) -> Any:
+    """A call-memo key of one positional argument: its exact type, and for arrays and tensors
+    their dtype (and whether a tensor is on the GPU).  Finer than the compile key of
+    ``_arg_key``, so equal light keys imply the same specialisation.  Other types raise
+    TypeError (the call then takes the full path)."""
+    t = type(v)
+    if t is int or t is float or t is bool:
+        return t
+    if t is np.ndarray:
+        return (t, v.dtype)
+    torch = _torch()
+    if torch is not None and t is torch.Tensor:
+        return (t, v.dtype, v.is_cuda)
+    raise TypeError("no light key")
 
 
 def _dims(value: Any, what: str, *, lo: int, max_dims: int, pad: bool) -> tuple[int, ...]:
@@ -58,6 +77,15 @@ class Kernel:
         self._cache: dict[tuple[Any, Any], CompiledKernel] = {}
         self._autotune_spec: AutotuneSpec | None = None
         self._tuned_cache: dict[tuple[Any, ...], Config] = {}
+        # call memo for repeated launches: runtime parameters first and passed positionally,
+        # keyword arguments only meta parameters and _sync (their values are part of the key)
+        lead = 0
+        while lead < len(params) and params[lead].name not in self.meta_params:
+            lead += 1
+        self._memo_ok = self._plain and lead == len(params) - len(self.meta_params)
+        self._n_lead = lead
+        self._memo_kw = frozenset(self.meta_params) | {"_sync"}
+        self._memo: dict[Any, tuple[CompiledKernel, dict[str, Any], bool]] = {}
 
     def _set_autotune_spec(self, spec: AutotuneSpec) -> None:
         self._autotune_spec = spec
@@ -224,8 +252,24 @@ class Kernel:
         return self._prepare(args, dict(kwargs))[0]
 
     def __call__(self, /, *args: Any, **kwargs: Any) -> None:
-        ck, meta, runtime_args, opts, _ = self._prepare(args, dict(kwargs))
+        key = None
+        if self._memo_ok and len(args) == self._n_lead and self._autotune_spec is None:
+            try:
+                key = (tuple(kwargs.items()), tuple(map(_light_key, args)))
+                hit = self._memo.get(key)
+            except TypeError:  # an argument or keyword value the memo does not key
+                key = hit = None
+            if hit is not None:
+                ck, meta, sync = hit
+                get_runtime().run(ck, dict(zip(self._names, args)), meta, sync=sync)
+                return
+        ck, meta, runtime_args, opts, raw = self._prepare(args, dict(kwargs))
         get_runtime().run(ck, runtime_args, meta, **opts)
+        if key is not None and kwargs.keys() <= self._memo_kw and all(
+                raw[o] is None for o in ("nthreads", "grid", "shape", "tptg")):
+            if len(self._memo) >= _MEMO_LIMIT:
+                self._memo.clear()
+            self._memo[key] = (ck, meta, opts["sync"])
 
     def to_hip(self, /, *args: Any, **kwargs: Any) -> str:
         """The generated gfx950 HIP C++ source for this specialisation (reference: ``to_msl``)."""

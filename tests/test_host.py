@@ -378,6 +378,66 @@ def test_numpy_add_argv_contract(monkeypatch, tmp_path):
     assert ext.d2h == [(("buf", 3), 4 * n)]
 
 
+def _recording_runtime(monkeypatch, tmp_path):
+    monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
+    ext = _RecordingExt()
+    rt = HipRuntime(ext=ext)
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    return ext
+
+
+def test_call_memo_launches_what_the_full_path_launches(monkeypatch, tmp_path):
+    """Repeated calls of one argument shape skip binding and specialisation (the call memo); the
+    launch they make is the one the full path makes, scalar values included."""
+    ext = _recording_runtime(monkeypatch, tmp_path)
+    k = eas.kernel(K.axpy_kernel.fn)
+    a, b, c = np.ones(1031, np.float32), np.ones(1031, np.float32), np.zeros(1031, np.float32)
+    k(a, b, c, 1031, 2.0, BLOCK=256, _sync=True)
+    assert len(k._memo) == 1
+    k(a, b, c, 1000, 3.5, BLOCK=256, _sync=True)  # memo hit: new scalar values, same kernel
+    monkeypatch.setattr(k, "_memo", {})  # the same call through the full path
+    k(a, b, c, 1000, 3.5, BLOCK=256, _sync=True)
+    assert len(ext.launches) == 3
+
+    def shape(launch):  # NumPy arguments are staged afresh on every call: compare buffer slots
+        kern, argv, writable, grid, block = launch
+        return kern, [x[0] if isinstance(x, tuple) else x for x in argv], writable, grid, block
+
+    assert shape(ext.launches[1]) == shape(ext.launches[2])
+    assert ext.launches[1][1][3] == struct.pack("<I", 1000) and ext.launches[1][1][4] == struct.pack("<f", 3.5)
+    assert ext.launches[0][1][3] == struct.pack("<I", 1031)
+
+
+def test_call_memo_keys_everything_that_selects_a_kernel(monkeypatch, tmp_path):
+    ext = _recording_runtime(monkeypatch, tmp_path)
+    k = eas.kernel(K.add_kernel.fn)
+    f32 = [np.ones(64, np.float32) for _ in range(3)]
+    f16 = [np.ones(64, np.float16) for _ in range(3)]
+    k(*f32, 64, BLOCK=64)
+    k(*f32, 64, BLOCK=128)  # another meta value
+    k(*f16, 64, BLOCK=64)  # another dtype
+    k(*f32, 64, BLOCK=64, _sync=False)  # another option value
+    assert len(k._memo) == 4 and len(k._cache) == 3
+    k(*f32, 64, BLOCK=64)
+    assert len(k._memo) == 4 and len(ext.launches) == 5
+    # launch options other than _sync, keyword runtime arguments and unkeyed types bypass the memo
+    k(*f32, 64, BLOCK=64, _grid=(1, 1, 1))
+    k(*f32, N=64, BLOCK=64)
+    k(*f32, np.uint32(64), BLOCK=64)
+    assert len(k._memo) == 4 and len(ext.launches) == 8
+
+
+def test_call_memo_still_rejects_bad_arguments(monkeypatch, tmp_path):
+    _recording_runtime(monkeypatch, tmp_path)
+    k = eas.kernel(K.add_kernel.fn)
+    a = np.ones(64, np.float32)
+    k(a, a, a.copy(), 64, BLOCK=64)
+    with pytest.raises(TypeError):
+        k(a, a, a.astype(np.float64), 64, BLOCK=64)  # another light key: the full path checks it
+    with pytest.raises(ValueError):
+        k(a, a, np.ones(128, np.float32)[::2], 64, BLOCK=64)  # same light key, not contiguous
+
+
 class _FillingExt(_RecordingExt):
     """Copies back a fixed byte pattern, so a test sees which host memory a result reaches."""
 
