@@ -5,8 +5,8 @@
  * extension `eas._metal` (eas/runtime/_metal.mm).  Everything here is plain C:
  * opaque handles, raw pointers, sizes and int status codes; no Python, torch
  * or HIP types cross the boundary.  The CPython module `easy_as_amd._hip`
- * (easy_as_amd/csrc/hip_module.cpp) is one binding of it; INTEGRATION.md shows
- * how a ctypes binding would call it.
+ * (easy_as_amd/csrc/hip_module.cpp) is one binding of it; a ctypes binding
+ * needs only the functions below and their status codes.
  *
  * Conventions
  *   - Every function returns EAS_HIP_OK (0) or a negative eas_hip_status.

@@ -1,4 +1,5 @@
-"""The ctypes binding shown in INTEGRATION.md, executed as written.
+"""The ctypes binding of the repository's integration guide (its one fenced block that starts
+with ``# integration-stub``), executed as written.
 
 CPU: the stub binds every symbol it names and compiles an eas kernel's HIP
 source.  GPU: it runs the reference's add kernel end to end through the bare C
@@ -19,7 +20,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def _stub() -> dict:
     text = (ROOT / "INTEGRATION.md").read_text()
     blocks = re.findall(r"```python\n(# integration-stub.*?)```", text, flags=re.S)
-    assert len(blocks) == 1, "INTEGRATION.md must hold exactly one integration-stub block"
+    assert len(blocks) == 1, "the integration guide must hold exactly one integration-stub block"
     ns: dict = {"__name__": "integration_stub"}
     exec(compile(blocks[0], "INTEGRATION.md:integration-stub", "exec", dont_inherit=True), ns)
     return ns
