@@ -53,7 +53,7 @@ class _Gen:
 
     def f_expr(self) -> str:
         r, p = self.r, self.pick
-        kind = r.randrange(12)
+        kind = r.randrange(13)
         if kind == 0:
             return f"{p(self.f)} + {p(self.f)}"
         if kind == 1:
@@ -75,6 +75,8 @@ class _Gen:
             return f"mk.to_f32(mk.to_f16({p(self.f)}))"
         if kind == 9 and self.u:
             return f"mk.to_f32({p(self.u)} % {r.choice((1000, 4096, 65536))})"
+        if kind == 11 and self.b:
+            return f"mk.to_f32({p(self.b)}) * {p(self.f)}"
         if kind == 10 and len(self.f) >= 2:
             # a product used twice: neither add may fuse it
             prod = self.emit(self.f, f"{p(self.f)} * {p(self.f)}")
@@ -84,7 +86,7 @@ class _Gen:
 
     def h_expr(self) -> str:
         r, p = self.r, self.pick
-        kind = r.randrange(6)
+        kind = r.randrange(8)
         if kind == 0:
             return f"{p(self.h)} + {p(self.h)}"
         if kind == 1:
@@ -96,6 +98,10 @@ class _Gen:
         if kind == 4:
             # f32 values can be large (products of products): scale before narrowing
             return f"mk.to_f16({p(self.f)} * 0.001)"
+        if kind == 6 and self.u:
+            return f"mk.to_f16({p(self.u)} % 70000)"
+        if kind == 7 and self.b:
+            return f"mk.to_f16({p(self.b)}) + {p(self.h)}"
         return f"{p(self.h)} * {p(self.h)} + {p(self.h)}"  # f16: never fused, two roundings
 
     def b_expr(self) -> str:
@@ -117,7 +123,7 @@ class _Gen:
 
     def u_expr(self) -> str:
         r, p = self.r, self.pick
-        kind = r.randrange(5)
+        kind = r.randrange(7)
         if kind == 0:
             return f"{p(self.u)} % {r.choice(_U_LITS)}"
         if kind == 1:
@@ -126,6 +132,10 @@ class _Gen:
             return f"{p(self.u)} * {r.choice(_U_LITS)} + {r.choice(_U_LITS)}"
         if kind == 3:
             return f"{p(self.u)} + {p(self.u)}"
+        if kind == 4:
+            return f"mk.to_u32({p(self.f)} * 100.0)"  # negative and NaN saturate to 0
+        if kind == 5 and self.b:
+            return f"mk.where({p(self.b)}, {p(self.u)}, {p(self.u)})"
         return f"({p(self.u)} * {r.choice(_U_LITS)}) % 4099"
 
     def body(self, n_stmts: int) -> None:
@@ -257,15 +267,19 @@ def inputs(seed: int, n: int) -> tuple:
 
 def case(seed: int) -> dict:
     """Launch of fuzz case ``seed``: ``mode``, ``N``, ``BLOCK``, the kernel ``src`` and the call's
-    ``options`` (``_grid`` for a 2-D SPMD grid).  Thread-mode kernels get N a multiple of BLOCK
-    (a partial last group would read threadgroup slots no thread wrote) and N >= 2048 (the dot
-    windows)."""
+    ``options`` (``_grid`` for a 2-D SPMD grid).  Thread-mode kernels get N >= 2048 (the dot
+    windows); those with a threadgroup exchange get N a multiple of BLOCK (a partial last group
+    would read slots no thread wrote), the others often a partial last group."""
     r = random.Random(10_000 + seed)
     mode = "spmd" if seed % 2 == 0 else "thread"
     block = r.choice((64, 128, 256))
     n = r.randrange(1, 9000)
     options: dict = {}
-    if mode == "thread":
+    if mode == "thread" and r.random() < 0.4:
+        # a partial last threadgroup: exactly N threads exist, so no threadgroup exchange
+        n = max(2048, n)
+        src = thread_source(seed, exchange=False)
+    elif mode == "thread":
         n = max(2048, n - n % block)
         src = thread_source(seed)
     elif seed % 4 == 2:

@@ -28,7 +28,7 @@ def test_generator_is_deterministic_and_varied():
     joined = "".join(c["src"] for c in cases)
     for op in ("mk.fma(", "mk.where(", "mk.to_f16(", "mk.to_f32(", " // ", " % ", " < ", " & ", " | ", "~",
                "mk.barrier()", "mk.alloc_tg(", "mk.lane_id()", "mk.sg_id()", "mk.dot(", "mk.program_id(1)",
-               "alpha", " S", "tgs = mk.alloc_tg(BLOCK)"):
+               "alpha", " S", "tgs = mk.alloc_tg(BLOCK)", "mk.to_u32("):
         assert op in joined, op
     assert any(c["options"].get("_grid") for c in cases)
 
