@@ -78,3 +78,26 @@ def test_random_program_matches_the_oracle_on_the_gpu(seed, gpu_runtime):
             i = int(bad[0])
             pytest.fail(f"seed {seed} ({c['mode']}, N={c['N']}, BLOCK={c['BLOCK']}, {c['options']}): {name}[{i}] = "
                         f"{got[i]!r}, oracle {ref[name][i]!r}; {bad.size} elements differ\n{c['src']}")
+
+
+_MAPPINGS = [{"EAS_HIP_SPMD_WG": "64"}, {"EAS_HIP_SPMD_WG": "256"}, {"EAS_HIP_SPMD_LPT": "16"},
+             {"EAS_HIP_SPMD_UNROLL": "2", "EAS_HIP_SPMD_WG": "32"}]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("env", _MAPPINGS, ids=lambda e: ",".join(f"{k[13:]}={v}" for k, v in e.items()))
+@pytest.mark.parametrize("seed", range(0, 80, 2))  # the SPMD cases
+def test_random_spmd_program_under_every_mapping(seed, env, gpu_runtime, monkeypatch):
+    """The SPMD emitter's other workgroup mappings (threads per workgroup, lanes per thread,
+    programs per workgroup, split programs) give the same bits as the oracle."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    c = F.case(seed)
+    assert c["mode"] == "spmd"
+    print(f"fuzz seed {seed} {env}: N={c['N']} BLOCK={c['BLOCK']} {c['options']}", flush=True)
+    k = F.build(c["src"])
+    args = F.inputs(seed, c["N"])
+    ref = _run_oracle(c, args)
+    k(*args, BLOCK=c["BLOCK"], **c["options"])
+    for name, got in (("out", args[4]), ("out16", args[5])):
+        assert F.same_values(got, ref[name]), f"seed {seed} {env}: {name} differs\n{c['src']}"
