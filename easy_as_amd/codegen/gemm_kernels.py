@@ -1166,18 +1166,18 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
     b_off[i] = ((uint32_t)rr * (uint32_t)ldb + (uint32_t)(n0 + lcb * 4)) * 4u;
     b_r[i] = rr;
   }
-  auto dma = [&](int kt) {
+  auto dma = [&](int kt) {  // a stage past K (kt >= KT) loads zeros into a slot nobody reads
     const uint32_t st = lds0 + (uint32_t)((kt % NSTAGE) * STF) * 4u;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       uint32_t off = a_off[i] + (uint32_t)(kt * BK) * 4u;
-      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: zeros
+      if ((K % BK != 0 && kt * BK + a_k[i] >= K) || kt >= KT) off = 0x80000000u;  // K tail: zeros
       eas_dma16(ra, off, st + (wave * 2 + i) * 1024);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       uint32_t off = b_off[i] + (uint32_t)(kt * BK) * (uint32_t)ldb * 4u;
-      if (K % BK != 0 && kt * BK + b_r[i] >= K) off = 0x80000000u;
+      if ((K % BK != 0 && kt * BK + b_r[i] >= K) || kt >= KT) off = 0x80000000u;
       eas_dma16(rb, off, st + AST * 4 + (wave * 2 + i) * 1024);
     }
   };
@@ -1193,28 +1193,66 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
     fb[s] = AST + row * BN + (((bj >> 2) ^ (8 * ((row >> 4) & 1))) * 4) + (bj & 3);
   }
   eas_f32x16 acc = {};
-#pragma unroll
-  for (int p = 0; p < NSTAGE - 1; ++p)
-    if (p < KT) dma(p);
-  for (int kt = 0; kt < KT; ++kt) {
-    // this wave's loads of stage kt landed (newer stages, 4 loads each, may stay in flight);
-    // the barrier makes every wave's part visible and frees stage kt-1 for the next DMA
-    const int later = min(NSTAGE - 2, KT - 1 - kt);
-    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
-    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));
-    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
-    __syncthreads();
-    if (kt + NSTAGE - 1 < KT) dma(kt + NSTAGE - 1);
+  // Fragments are read one stage ahead and interleaved with the MFMAs.  At the barrier of stage
+  // kt every wave has its own DMA of stage kt+1 landed; after it the wave issues stage kt's 16
+  // MFMAs (a dependent chain, 64 clocks each) from the register set read one stage earlier, and
+  // between them the DMA of stage kt+3 and the reads of stage kt+1 into the other set, one per
+  // MFMA (sched_group_barrier), so that with one wave per SIMD they use the chain's idle issue
+  // slots.  The DMA of stage kt+3 refills the slot of stage kt-1, whose fragments every wave read
+  // (and waited for) before its MFMAs of stage kt-1.  4 loads per wave and stage.
+  auto read_stage = [&](int kt, eas_f32x4 (&a)[4], float (&b)[16]) {
     const float* st = smem + (kt % NSTAGE) * STF;
-    eas_f32x4 a[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) a[u] = *(const eas_f32x4*)(st + fa[u]);
-    float b[16];
 #pragma unroll
     for (int s = 0; s < 16; ++s) b[s] = st[fb[s]];
+  };
+  auto mfmas = [&](const eas_f32x4 (&a)[4], const float (&b)[16]) {
 #pragma unroll
     for (int s = 0; s < 16; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s >> 2][s & 3], b[s], acc, 0, 0, 0);
+  };
+  // a stage that is followed by another: every stage from 2 on is DMA'd (zeros past K), so
+  // stage kt+2's 4 loads are always the ones that may stay in flight here
+  auto step = [&](int kt, const eas_f32x4 (&a)[4], const float (&b)[16], eas_f32x4 (&na)[4], float (&nb)[16]) {
+    __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    dma(kt + NSTAGE - 1);
+    read_stage(kt + 1, na, nb);
+    mfmas(a, b);
+    // schedule: the 4 DMA loads after the first 4 MFMAs, then one LDS read after each MFMA
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+#pragma unroll
+    for (int s = 0; s < 12; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p) dma(p);
+  // stage 0 landed (stages 1 and 2 may be in flight)
+  __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
+  __syncthreads();
+  eas_f32x4 a0[4], a1[4];
+  float b0[16], b1[16];
+  read_stage(0, a0, b0);
+  int kt = 0;
+  for (; kt + 2 < KT; kt += 2) {  // two stages per iteration: the register sets alternate
+    step(kt, a0, b0, a1, b1);
+    step(kt + 1, a1, b1, a0, b0);
   }
+  if constexpr (KT % 2 == 0) {
+    step(KT - 2, a0, b0, a1, b1);
+    mfmas(a1, b1);
+  } else {
+    mfmas(a0, b0);
+  }
+  __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));  // the zero-filling DMAs past K
   // lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
