@@ -1264,13 +1264,13 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
 """
 
 # The fp32 128 x 128 tile entry: four waves of 64 x 64 (2 x 2 accumulators of
-# v_mfma_f32_32x32x2_f32), a 3-stage ring of 32 KB stages.  A quarter of the
+# v_mfma_f32_32x32x2_f32), a 4-stage ring of 32 KB stages.  A quarter of the
 # 64-tile kernel's DMA bytes per flop and four independent MFMA chains per wave;
 # the launch plan picks it when 128 x 128 tiles still give every CU one.
 _TEMPLATE_F32_T128 = r"""
 extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
     @PARAMS@) {
-  constexpr int BM = 128, BN = 128, BK = 32, NSTAGE = 3, K = @K@, KT = (K + BK - 1) / BK;
+  constexpr int BM = 128, BN = 128, BK = 32, NSTAGE = 4, K = @K@, KT = (K + BK - 1) / BK;
   constexpr int AST = BM * BK, BST = BK * BN, STF = AST + BST;  // floats per stage (32 KB)
   const int ldb = (int)@LDB@;
   // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
@@ -1321,15 +1321,15 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
     b_off[i] = ((uint32_t)rr * (uint32_t)ldb + (uint32_t)(n0 + lcb * 4)) * 4u;
     b_r[i] = rr;
   }
-  auto dma = [&](int kt) {
+  auto dma = [&](int kt) {  // a stage past K (kt >= KT) loads zeros into a slot nobody reads
     const uint32_t st = lds0 + (uint32_t)((kt % NSTAGE) * STF) * 4u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t off = a_off[i] + (uint32_t)(kt * BK) * 4u;
-      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: zeros
+      if ((K % BK != 0 && kt * BK + a_k[i] >= K) || kt >= KT) off = 0x80000000u;  // K tail: zeros
       eas_dma16(ra, off, st + (wave * 4 + i) * 1024);
       uint32_t offb = b_off[i] + (uint32_t)(kt * BK) * (uint32_t)ldb * 4u;
-      if (K % BK != 0 && kt * BK + b_r[i] >= K) offb = 0x80000000u;
+      if ((K % BK != 0 && kt * BK + b_r[i] >= K) || kt >= KT) offb = 0x80000000u;
       eas_dma16(rb, offb, st + AST * 4 + (wave * 4 + i) * 1024);
     }
   };
@@ -1353,46 +1353,74 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
-#pragma unroll
-  for (int p = 0; p < NSTAGE - 1; ++p)
-    if (p < KT) dma(p);
-  for (int kt = 0; kt < KT; ++kt) {
-    // this wave's loads of stage kt landed (a newer stage, 8 loads, may stay in flight); the barrier
-    // makes every wave's part visible and frees stage kt-1 for the next DMA
-    if (kt + 1 < KT) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
-    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
-    __syncthreads();
-    if (kt + NSTAGE - 1 < KT) dma(kt + NSTAGE - 1);
+  // Fragments are read one stage ahead, interleaved with the MFMAs: at the barrier of stage kt
+  // every wave has its own DMA of stage kt+1 landed; after it the wave issues stage kt's 64
+  // MFMAs from the register set read one stage earlier and, between them (sched_group_barrier),
+  // the DMA of stage kt+3 and every fragment read of stage kt+1 into the other set.  The DMA
+  // refills the slot of stage kt-1, whose fragments every wave read (and waited for) before its
+  // MFMAs of stage kt-1.  Every stage from 3 on is DMA'd (zeros past K), so stage kt+2's 8 loads
+  // are always the ones that may stay in flight at the barrier.
+  auto read_stage = [&](int kt, eas_f32x4 (&a)[2][4], float (&b)[2][16]) {
     const float* st = smem + (kt % NSTAGE) * STF;
-    // the stage's 16 steps in four groups of four; the fragments of group u + 1 are read before
-    // the 16 MFMAs of group u issue, so that one wave per SIMD does not wait on LDS latency
-    // between groups (sched_barrier keeps the compiler from moving the reads back)
-    eas_f32x4 a[2][2];
-    float b[2][2][4];
-    auto read_group = [&](int u, int buf) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        a[buf][i] = *(const eas_f32x4*)(st + fa[i][u]);
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) b[buf][i][e] = st[fb[i][4 * u + e]];
-      }
-    };
-    read_group(0, 0);
+      for (int u = 0; u < 4; ++u) a[i][u] = *(const eas_f32x4*)(st + fa[i][u]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int cur = u & 1;
-      if (u + 1 < 4) read_group(u + 1, cur ^ 1);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cur][i][e], b[cur][j][e], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int s = 0; s < 16; ++s) b[i][s] = st[fb[i][s]];
     }
+  };
+  auto mfmas = [&](const eas_f32x4 (&a)[2][4], const float (&b)[2][16]) {
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s >> 2][s & 3], b[j][s], acc[i][j], 0, 0, 0);
+  };
+  auto step = [&](int kt, const eas_f32x4 (&a)[2][4], const float (&b)[2][16], eas_f32x4 (&na)[2][4],
+                  float (&nb)[2][16]) {
+    __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    dma(kt + NSTAGE - 1);
+    read_stage(kt + 1, na, nb);
+    mfmas(a, b);
+    // schedule: the 8 DMA loads after the first 8 MFMAs, then one LDS read after each MFMA
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+#pragma unroll
+    for (int s = 0; s < 40; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#pragma unroll
+  for (int p = 0; p < NSTAGE - 1; ++p) dma(p);
+  // stage 0 landed (stages 1 and 2 may be in flight, 8 loads each)
+  __builtin_amdgcn_s_waitcnt(EAS_WAITVM(16));
+  __syncthreads();
+  eas_f32x4 a0[2][4], a1[2][4];
+  float b0[2][16], b1[2][16];
+  read_stage(0, a0, b0);
+  int kt = 0;
+  for (; kt + 2 < KT; kt += 2) {  // two stages per iteration: the register sets alternate
+    step(kt, a0, b0, a1, b1);
+    step(kt + 1, a1, b1, a0, b0);
   }
+  if constexpr (KT % 2 == 0) {
+    step(KT - 2, a0, b0, a1, b1);
+    mfmas(a1, b1);
+  } else {
+    mfmas(a0, b0);
+  }
+  __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));  // the zero-filling DMAs past K
   // lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
 #pragma unroll
   for (int i = 0; i < 2; ++i)
