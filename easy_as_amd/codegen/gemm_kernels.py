@@ -90,6 +90,13 @@ static __device__ __forceinline__ eas_rsrc eas_make_rsrc(const void* base, uint3
 static __device__ __forceinline__ void eas_dma16(eas_rsrc r, uint32_t voff, uint32_t lds) {
   asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
+// The same with the stage part of the offset in an SGPR (soffset): the lane part stays fixed in
+// one VGPR per load, so a wave that only issues these runs no VALU.  Every caller keeps
+// voff + soff inside the buffer, or voff at 2^31 or more with soff below 2^31 (zeros), so the
+// result does not depend on whether the range check includes soffset.
+static __device__ __forceinline__ void eas_dma16s(eas_rsrc r, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(lds) : "memory");
+}
 """
 
 # The MFMA operand type of the 16-bit templates: f16 or bf16 (the dtype of the kernel's
@@ -1100,8 +1107,16 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
 }
 """
 
+# The fp32 entries (the tiled threadgroup kernel lifted to v_mfma_f32_32x32x2_f32) run 8 waves
+# (512 threads), specialised.  Waves 0-3 consume: fragment reads one stage ahead, interleaved one
+# per MFMA with the current stage's MFMAs.  Waves 4-7 produce: the HBM -> LDS DMA of a 4-stage
+# ring of BK = 32, three stages ahead, with no VALU.  Measured on MI355X, a wave that issues a
+# 16-byte-per-lane load (to LDS or to VGPRs) costs its SIMD's MFMA pipe ~30 clocks, while loads
+# issued by the other wave of the SIMD cost the MFMA wave nothing as long as that wave runs no
+# VALU: at 1024^3 a stage of the 64 x 64 entry takes 1105 clocks instead of 1232 (1024 for its
+# MFMAs), at 2048^3 one of the 128 x 128 entry 4187 instead of 4418 (4096).
 _TEMPLATE_F32 = r"""
-extern "C" __global__ __launch_bounds__(256) void @NAME@(
+extern "C" __global__ __launch_bounds__(512) void @NAME@(
     @PARAMS@) {
   constexpr int BM = 64, BN = 64, BK = 32, NSTAGE = 4, K = @K@, KT = (K + BK - 1) / BK;
   constexpr int AST = BM * BK, BST = BK * BN, STF = AST + BST;  // floats per stage
@@ -1125,7 +1140,8 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   const bool dma_ok = (K % 4 == 0) && (ldb % 4 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0) &&
                       ((uint64_t)M * K * 4 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 4 < (1ull << 31));
   if (!dma_ok) {
-    // rows not 16-byte aligned: each thread accumulates a 4 x 4 block with plain fmas
+    // rows not 16-byte aligned: each of 256 threads accumulates a 4 x 4 block with plain fmas
+    if (tid >= 256) return;
     const int r0 = m0 + (tid >> 4) * 4, c0 = n0 + (tid & 15) * 4;
     float acc[4][4] = {};
     for (int k = 0; k < K; ++k) {
@@ -1146,41 +1162,69 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
         if (r0 + i < M && c0 + j < N) C[(size_t)(r0 + i) * ldb + c0 + j] = acc[i][j];
     return;
   }
-  // 4 waves of 32 x 32; v_mfma_f32_32x32x2_f32: A lane l holds A[l%32][k], B lane l holds B[k][l%32]
-  const int wm = wave >> 1, wn = wave & 1;
-  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 4u);
-  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 4u);
-  const uint32_t lds0 = (uint32_t)(size_t)(EAS_LDS float*)smem;
-  // DMA (1 KB per instruction, 2 A + 2 B per wave per stage):
-  //   A stage [64 rows][32 k]: rows 8q + lane/8, 16-byte chunk lane%8 stored at chunk ^ ((row/2)%8)
-  //   B stage [32 k][64 n]:    rows 4q + lane/16, chunk lane%16 stored at chunk ^ 8((row/16)%2)
-  uint32_t a_off[2], b_off[2];
-  int a_k[2], b_r[2];
+  if (wave >= 4) {
+    // producer: the DMA (1 KB per instruction, 2 A + 2 B per wave per stage, q = 2 pw + i)
+    //   A stage [64 rows][32 k]: rows 8q + lane/8, 16-byte chunk lane%8 stored at chunk ^ ((row/2)%8)
+    //   B stage [32 k][64 n]:    rows 4q + lane/16, chunk lane%16 stored at chunk ^ 8((row/16)%2)
+    // Rows past M and columns past N load zeros (they are never stored), so every address a load
+    // reads, lane offset plus stage offset, lies inside A or B.  The last stage of a K that is not
+    // a multiple of BK loads zeros past K; stages past K load zeros into a slot nobody reads, so
+    // every stage issues 4 loads and the count at each barrier is the same.
+    const int pw = wave - 4;
+    const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 4u);
+    const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 4u);
+    const uint32_t lds0 = (uint32_t)(size_t)(EAS_LDS float*)smem;
+    constexpr int KLAST = K - (KT - 1) * BK;  // k extent of the last stage
+    uint32_t a_off[2], b_off[2], a_tail[2], b_tail[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = wave * 2 + i;
-    const int r = 8 * q + (lane >> 3), lc = (lane & 7) ^ ((r >> 1) & 7);
-    a_off[i] = ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)(lc * 4)) * 4u;
-    a_k[i] = lc * 4;
-    const int rr = 4 * q + (lane >> 4), lcb = (lane & 15) ^ (8 * ((rr >> 4) & 1));
-    b_off[i] = ((uint32_t)rr * (uint32_t)ldb + (uint32_t)(n0 + lcb * 4)) * 4u;
-    b_r[i] = rr;
+    for (int i = 0; i < 2; ++i) {
+      const int q = pw * 2 + i;
+      const int r = 8 * q + (lane >> 3), lc = (lane & 7) ^ ((r >> 1) & 7);
+      a_off[i] = m0 + r < M ? ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)(lc * 4)) * 4u : 0x80000000u;
+      a_tail[i] = lc * 4 >= KLAST ? 0x80000000u : a_off[i];
+      const int rr = 4 * q + (lane >> 4), lcb = (lane & 15) ^ (8 * ((rr >> 4) & 1));
+      b_off[i] = n0 + lcb * 4 < N ? (uint32_t)(n0 + lcb * 4) * 4u + (uint32_t)rr * (uint32_t)ldb * 4u : 0x80000000u;
+      b_tail[i] = rr >= KLAST ? 0x80000000u : b_off[i];
+    }
+    auto dma = [&](int kt) {
+      const uint32_t st = lds0 + (uint32_t)((kt % NSTAGE) * STF) * 4u;
+      const uint32_t sa = (uint32_t)(kt * BK) * 4u, sb = (uint32_t)(kt * BK) * (uint32_t)ldb * 4u;
+      if (kt >= KT) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          eas_dma16s(ra, 0x80000000u, 0u, st + (pw * 2 + i) * 1024);
+          eas_dma16s(rb, 0x80000000u, 0u, st + AST * 4 + (pw * 2 + i) * 1024);
+        }
+      } else if (K % BK != 0 && kt == KT - 1) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          eas_dma16s(ra, a_tail[i], sa, st + (pw * 2 + i) * 1024);
+          eas_dma16s(rb, b_tail[i], sb, st + AST * 4 + (pw * 2 + i) * 1024);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          eas_dma16s(ra, a_off[i], sa, st + (pw * 2 + i) * 1024);
+          eas_dma16s(rb, b_off[i], sb, st + AST * 4 + (pw * 2 + i) * 1024);
+        }
+      }
+    };
+    // one barrier per stage, as many as the consumers
+#pragma unroll
+    for (int p = 0; p < NSTAGE - 1; ++p) dma(p);
+    __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));  // stage 0 landed (stages 1 and 2 may be in flight)
+    __syncthreads();
+    for (int kt = 0; kt + 1 < KT; ++kt) {
+      __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));  // stage kt+1 landed (stage kt+2 may be in flight)
+      __syncthreads();
+      dma(kt + NSTAGE - 1);  // the slot of stage kt-1, whose fragments every consumer has read
+    }
+    __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+    return;
   }
-  auto dma = [&](int kt) {  // a stage past K (kt >= KT) loads zeros into a slot nobody reads
-    const uint32_t st = lds0 + (uint32_t)((kt % NSTAGE) * STF) * 4u;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t off = a_off[i] + (uint32_t)(kt * BK) * 4u;
-      if ((K % BK != 0 && kt * BK + a_k[i] >= K) || kt >= KT) off = 0x80000000u;  // K tail: zeros
-      eas_dma16(ra, off, st + (wave * 2 + i) * 1024);
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t off = b_off[i] + (uint32_t)(kt * BK) * (uint32_t)ldb * 4u;
-      if ((K % BK != 0 && kt * BK + b_r[i] >= K) || kt >= KT) off = 0x80000000u;
-      eas_dma16(rb, off, st + AST * 4 + (wave * 2 + i) * 1024);
-    }
-  };
+  // consumers: 4 waves of 32 x 32; v_mfma_f32_32x32x2_f32: A lane l holds A[l%32][k], B lane l
+  // holds B[k][l%32]
+  const int wm = wave >> 1, wn = wave & 1;
   // k order within a stage: MFMA step s (0..15) takes k = s + 16 c for lane half c = lane/32, so one
   // ds_read_b128 gives a lane A values for four steps; B is one float of row s + 16 c per step
   const int c = lane >> 5, ai = wm * 32 + (lane & 31), bj = wn * 32 + (lane & 31);
@@ -1194,12 +1238,11 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   }
   eas_f32x16 acc = {};
   // Fragments are read one stage ahead and interleaved with the MFMAs.  At the barrier of stage
-  // kt every wave has its own DMA of stage kt+1 landed; after it the wave issues stage kt's 16
-  // MFMAs (a dependent chain, 64 clocks each) from the register set read one stage earlier, and
-  // between them the DMA of stage kt+3 and the reads of stage kt+1 into the other set, one per
-  // MFMA (sched_group_barrier), so that with one wave per SIMD they use the chain's idle issue
-  // slots.  The DMA of stage kt+3 refills the slot of stage kt-1, whose fragments every wave read
-  // (and waited for) before its MFMAs of stage kt-1.  4 loads per wave and stage.
+  // kt the producers' DMA of stage kt+1 has landed; after it the wave issues stage kt's 16 MFMAs
+  // (a dependent chain, 64 clocks each) from the register set read one stage earlier, and between
+  // them the reads of stage kt+1 into the other set, one per MFMA (sched_group_barrier).  After
+  // this barrier the producers refill the slot of stage kt-1, whose fragments every consumer read
+  // (and waited for, at the barrier of stage kt-1) before it.
   auto read_stage = [&](int kt, eas_f32x4 (&a)[4], float (&b)[16]) {
     const float* st = smem + (kt % NSTAGE) * STF;
 #pragma unroll
@@ -1211,33 +1254,22 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
 #pragma unroll
     for (int s = 0; s < 16; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s >> 2][s & 3], b[s], acc, 0, 0, 0);
   };
-  // a stage that is followed by another: every stage from 2 on is DMA'd (zeros past K), so
-  // stage kt+2's 4 loads are always the ones that may stay in flight here
+  // a stage that is followed by another (KT - 1 of them, each with the barrier the producers match)
   auto step = [&](int kt, const eas_f32x4 (&a)[4], const float (&b)[16], eas_f32x4 (&na)[4], float (&nb)[16]) {
-    __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    dma(kt + NSTAGE - 1);
     read_stage(kt + 1, na, nb);
     mfmas(a, b);
-    // schedule: the 4 DMA loads after the first 4 MFMAs, then one LDS read after each MFMA
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
+    // one LDS read after each of the first 12 MFMAs
 #pragma unroll
     for (int s = 0; s < 12; ++s) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
-#pragma unroll
-  for (int p = 0; p < NSTAGE - 1; ++p) dma(p);
-  // stage 0 landed (stages 1 and 2 may be in flight)
-  __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
-  __syncthreads();
+  __syncthreads();  // stage 0 landed
   eas_f32x4 a0[4], a1[4];
   float b0[16], b1[16];
   read_stage(0, a0, b0);
@@ -1252,7 +1284,6 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   } else {
     mfmas(a0, b0);
   }
-  __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));  // the zero-filling DMAs past K
   // lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -1263,12 +1294,12 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
 }
 """
 
-# The fp32 128 x 128 tile entry: four waves of 64 x 64 (2 x 2 accumulators of
-# v_mfma_f32_32x32x2_f32), a 4-stage ring of 32 KB stages.  A quarter of the
-# 64-tile kernel's DMA bytes per flop and four independent MFMA chains per wave;
-# the launch plan picks it when 128 x 128 tiles still give every CU one.
+# The fp32 128 x 128 tile entry: four consumer waves of 64 x 64 (2 x 2 accumulators of
+# v_mfma_f32_32x32x2_f32) and four producer waves, a 4-stage ring of 32 KB stages.  A quarter of
+# the 64-tile kernel's DMA bytes per flop and four independent MFMA chains per wave; the launch
+# plan picks it when 128 x 128 tiles still give every CU one.
 _TEMPLATE_F32_T128 = r"""
-extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
+extern "C" __global__ __launch_bounds__(512) void @NAME@__t128(
     @PARAMS@) {
   constexpr int BM = 128, BN = 128, BK = 32, NSTAGE = 4, K = @K@, KT = (K + BK - 1) / BK;
   constexpr int AST = BM * BK, BST = BK * BN, STF = AST + BST;  // floats per stage (32 KB)
@@ -1293,7 +1324,7 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
                       ((uint64_t)M * K * 4 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 4 < (1ull << 31));
   if (!dma_ok) {
     // guard for operands the launch plan could not see: one f32 dot product per element
-    for (int e = tid; e < BM * BN; e += 256) {
+    for (int e = tid; e < BM * BN; e += 512) {
       const int row = m0 + e / BN, col = n0 + e % BN;
       if (row >= M || col >= N) continue;
       float acc = 0.0f;
@@ -1302,37 +1333,67 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
     }
     return;
   }
-  const int wm = wave >> 1, wn = wave & 1;
-  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 4u);
-  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 4u);
-  const uint32_t lds0 = (uint32_t)(size_t)(EAS_LDS float*)smem;
-  // DMA (1 KB per instruction, 4 A + 4 B per wave per stage, q = 4 wave + i):
-  //   A stage [128 rows][32 k]: rows 8q + lane/8, chunk lane%8 stored at chunk ^ ((row/2)%8)
-  //   B stage [32 k][128 n]:    rows 2q + lane/32, chunk lane%32 stored at chunk ^ 8((row/16)%2)
-  uint32_t a_off[4], b_off[4];
-  int a_k[4], b_r[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int q = wave * 4 + i;
-    const int r = 8 * q + (lane >> 3), lc = (lane & 7) ^ ((r >> 1) & 7);
-    a_off[i] = ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)(lc * 4)) * 4u;
-    a_k[i] = lc * 4;
-    const int rr = 2 * q + (lane >> 5), lcb = (lane & 31) ^ (8 * ((rr >> 4) & 1));
-    b_off[i] = ((uint32_t)rr * (uint32_t)ldb + (uint32_t)(n0 + lcb * 4)) * 4u;
-    b_r[i] = rr;
-  }
-  auto dma = [&](int kt) {  // a stage past K (kt >= KT) loads zeros into a slot nobody reads
-    const uint32_t st = lds0 + (uint32_t)((kt % NSTAGE) * STF) * 4u;
+  if (wave >= 4) {
+    // producer: the DMA (1 KB per instruction, 4 A + 4 B per wave per stage, q = 4 pw + i)
+    //   A stage [128 rows][32 k]: rows 8q + lane/8, chunk lane%8 stored at chunk ^ ((row/2)%8)
+    //   B stage [32 k][128 n]:    rows 2q + lane/32, chunk lane%32 stored at chunk ^ 8((row/16)%2)
+    // Rows past M and columns past N load zeros (they are never stored), so every address a load
+    // reads, lane offset plus stage offset, lies inside A or B.  The last stage of a K that is not
+    // a multiple of BK loads zeros past K; stages past K load zeros into a slot nobody reads, so
+    // every stage issues 8 loads and the count at each barrier is the same.
+    const int pw = wave - 4;
+    const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 4u);
+    const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 4u);
+    const uint32_t lds0 = (uint32_t)(size_t)(EAS_LDS float*)smem;
+    constexpr int KLAST = K - (KT - 1) * BK;  // k extent of the last stage
+    uint32_t a_off[4], b_off[4], a_tail[4], b_tail[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t off = a_off[i] + (uint32_t)(kt * BK) * 4u;
-      if ((K % BK != 0 && kt * BK + a_k[i] >= K) || kt >= KT) off = 0x80000000u;  // K tail: zeros
-      eas_dma16(ra, off, st + (wave * 4 + i) * 1024);
-      uint32_t offb = b_off[i] + (uint32_t)(kt * BK) * (uint32_t)ldb * 4u;
-      if ((K % BK != 0 && kt * BK + b_r[i] >= K) || kt >= KT) offb = 0x80000000u;
-      eas_dma16(rb, offb, st + AST * 4 + (wave * 4 + i) * 1024);
+      const int q = pw * 4 + i;
+      const int r = 8 * q + (lane >> 3), lc = (lane & 7) ^ ((r >> 1) & 7);
+      a_off[i] = m0 + r < M ? ((uint32_t)(m0 + r) * (uint32_t)K + (uint32_t)(lc * 4)) * 4u : 0x80000000u;
+      a_tail[i] = lc * 4 >= KLAST ? 0x80000000u : a_off[i];
+      const int rr = 2 * q + (lane >> 5), lcb = (lane & 31) ^ (8 * ((rr >> 4) & 1));
+      b_off[i] = n0 + lcb * 4 < N ? (uint32_t)(n0 + lcb * 4) * 4u + (uint32_t)rr * (uint32_t)ldb * 4u : 0x80000000u;
+      b_tail[i] = rr >= KLAST ? 0x80000000u : b_off[i];
     }
-  };
+    auto dma = [&](int kt) {
+      const uint32_t st = lds0 + (uint32_t)((kt % NSTAGE) * STF) * 4u;
+      const uint32_t sa = (uint32_t)(kt * BK) * 4u, sb = (uint32_t)(kt * BK) * (uint32_t)ldb * 4u;
+      if (kt >= KT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          eas_dma16s(ra, 0x80000000u, 0u, st + (pw * 4 + i) * 1024);
+          eas_dma16s(rb, 0x80000000u, 0u, st + AST * 4 + (pw * 4 + i) * 1024);
+        }
+      } else if (K % BK != 0 && kt == KT - 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          eas_dma16s(ra, a_tail[i], sa, st + (pw * 4 + i) * 1024);
+          eas_dma16s(rb, b_tail[i], sb, st + AST * 4 + (pw * 4 + i) * 1024);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          eas_dma16s(ra, a_off[i], sa, st + (pw * 4 + i) * 1024);
+          eas_dma16s(rb, b_off[i], sb, st + AST * 4 + (pw * 4 + i) * 1024);
+        }
+      }
+    };
+    // one barrier per stage, as many as the consumers
+#pragma unroll
+    for (int p = 0; p < NSTAGE - 1; ++p) dma(p);
+    __builtin_amdgcn_s_waitcnt(EAS_WAITVM(16));  // stage 0 landed (stages 1 and 2 may be in flight)
+    __syncthreads();
+    for (int kt = 0; kt + 1 < KT; ++kt) {
+      __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));  // stage kt+1 landed (stage kt+2 may be in flight)
+      __syncthreads();
+      dma(kt + NSTAGE - 1);  // the slot of stage kt-1, whose fragments every consumer has read
+    }
+    __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+    return;
+  }
+  const int wm = wave >> 1, wn = wave & 1;
   // MFMA step s (0..15) of a stage takes k = s + 16 c for lane half c = lane/32
   const int c = lane >> 5;
   int fa[2][4], fb[2][16];
@@ -1354,12 +1415,11 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
   // Fragments are read one stage ahead, interleaved with the MFMAs: at the barrier of stage kt
-  // every wave has its own DMA of stage kt+1 landed; after it the wave issues stage kt's 64
-  // MFMAs from the register set read one stage earlier and, between them (sched_group_barrier),
-  // the DMA of stage kt+3 and every fragment read of stage kt+1 into the other set.  The DMA
-  // refills the slot of stage kt-1, whose fragments every wave read (and waited for) before its
-  // MFMAs of stage kt-1.  Every stage from 3 on is DMA'd (zeros past K), so stage kt+2's 8 loads
-  // are always the ones that may stay in flight at the barrier.
+  // the producers' DMA of stage kt+1 has landed; after it the wave issues stage kt's 64 MFMAs
+  // from the register set read one stage earlier and, between them (sched_group_barrier), every
+  // fragment read of stage kt+1 into the other set.  After this barrier the producers refill the
+  // slot of stage kt-1, whose fragments every consumer read (and waited for, at the barrier of
+  // stage kt-1) before it.
   auto read_stage = [&](int kt, eas_f32x4 (&a)[2][4], float (&b)[2][16]) {
     const float* st = smem + (kt % NSTAGE) * STF;
 #pragma unroll
@@ -1379,33 +1439,23 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][s >> 2][s & 3], b[j][s], acc[i][j], 0, 0, 0);
   };
+  // a stage that is followed by another (KT - 1 of them, each with the barrier the producers match)
   auto step = [&](int kt, const eas_f32x4 (&a)[2][4], const float (&b)[2][16], eas_f32x4 (&na)[2][4],
                   float (&nb)[2][16]) {
-    __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    dma(kt + NSTAGE - 1);
     read_stage(kt + 1, na, nb);
     mfmas(a, b);
-    // schedule: the 8 DMA loads after the first 8 MFMAs, then one LDS read after each MFMA
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
+    // one LDS read after each of the first 40 MFMAs
 #pragma unroll
     for (int s = 0; s < 40; ++s) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 24, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
-#pragma unroll
-  for (int p = 0; p < NSTAGE - 1; ++p) dma(p);
-  // stage 0 landed (stages 1 and 2 may be in flight, 8 loads each)
-  __builtin_amdgcn_s_waitcnt(EAS_WAITVM(16));
-  __syncthreads();
+  __syncthreads();  // stage 0 landed
   eas_f32x4 a0[2][4], a1[2][4];
   float b0[2][16], b1[2][16];
   read_stage(0, a0, b0);
@@ -1420,7 +1470,6 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
   } else {
     mfmas(a0, b0);
   }
-  __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));  // the zero-filling DMAs past K
   // lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -1439,6 +1488,7 @@ TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
 PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
+F32_THREADS = 512  # both fp32 entries: 4 consumer + 4 producer waves
 SKINNY_M = 128  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
 # MFMA shape of the 8-wave entry's body: 16 (v_mfma_f32_16x16x32, the default) or 32
@@ -1497,9 +1547,10 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
     header = (f"// Lifted from eas kernel `{ir.name}`: proven dense GEMM C[M,N] = A[M,{spec.K}] @ B[{spec.K},N]\n"
               f"// (A={spec.a}, B={spec.b}, C={spec.c}, M={spec.m_sym}, N={spec.n_sym}, reference tile "
               f"{spec.TM}x{spec.TN} rows on program_id({spec.row_axis})).\n")
-    geo = Geometry("gemm", ir.name, block, THREADS, params={
+    threads = F32_THREADS if spec.f32 else THREADS
+    geo = Geometry("gemm", ir.name, block, threads, params={
         "m_sym": spec.m_sym, "n_sym": spec.n_sym, "K": spec.K, "TM": spec.TM, "TN": spec.TN,
-        "row_axis": spec.row_axis, "BM": bm, "BN": bn, "threads": THREADS,
+        "row_axis": spec.row_axis, "BM": bm, "BN": bn, "threads": threads,
         "skinny_m": 0 if spec.f32 else SKINNY_M, "skinny_n": SKINNY_N, "row_base": spec.row_base,
         "col_base": spec.col_base,
         "col_masked": spec.col_masked,

@@ -259,13 +259,14 @@ def test_plan_tile_size_follows_the_cu_count(mn, entry, grid):
 
 
 def test_plan_fp32_tile_size(monkeypatch):
-    # fp32: 128 x 128 tiles while they still give every CU one, else 64 x 64
+    # fp32: 128 x 128 tiles while they still give every CU one, else 64 x 64; both entries run
+    # 4 consumer and 4 producer waves
     z = np.zeros(1, np.float32)
     for m, entry, grid in ((2048, "matmul_tiled_kernel__t128", 256), (1024, None, 256), (1536, None, 576)):
         ck = K.matmul_tiled_kernel.compile(z, z, z, m, m, 0, 0, BM=32, BN=32, BK=32, K=64, NT=256)
         args = {"M": m, "N": m, "PID_M_BASE": 0, "PID_N_BASE": 0}
         plan = plan_launch(ck, args, grid=(m // 32, m // 32, 1))
-        assert plan.entry == entry and plan.grid == (grid, 1, 1) and plan.block == (256, 1, 1)
+        assert plan.entry == entry and plan.grid == (grid, 1, 1) and plan.block == (512, 1, 1)
     ck = K.matmul_tiled_kernel.compile(z, z, z, 2048, 2048, 0, 0, BM=32, BN=32, BK=32, K=62, NT=256)
     assert plan_launch(ck, {"M": 2048, "N": 2048, "PID_M_BASE": 0, "PID_N_BASE": 0},
                        grid=(64, 64, 1)).entry is None  # rows of 62 floats are not 16-byte aligned
