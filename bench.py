@@ -12,10 +12,11 @@ of the kernel from HIP events on its launch stream, vs 8 TB/s) and
 expressions its tests compute expected values with: ``np.add(a, b, out=c)``,
 ``a*b+c``, ``A32 @ B32``, ``A16.astype(np.float32) @ B16.astype(np.float32)``)
 timed on this host's cores on the same arrays, with the host described.  ``vendor`` times the same operation through torch (ROCm:
-``torch.add``, hipBLASLt/rocBLAS ``torch.matmul``) on the same device-resident
-inputs, in the same run, with the same event method; each matmul entry under
-``extra`` carries its ``torch_matmul``.  Secondary measurements ride along under
-``extra``.
+``torch.add``, hipBLASLt/rocBLAS ``torch.matmul``, or ``torch.mm(..., out_dtype=torch.float32)``
+where the eas kernel writes f32 from 16-bit inputs) on the same device-resident inputs with the
+eas kernel's output dtype, in the same run, with the same event method; for a matmul the eas and
+vendor event trials alternate.  Each matmul entry under ``extra`` carries its ``torch_matmul``.
+Secondary measurements ride along under ``extra``.
 
 ``--workload copy|fma|read|write`` measures the other elementwise kernels the same way
 (``copy`` is the known-size kernel that calibrates HBM byte counters; ``read`` and
@@ -143,6 +144,25 @@ def _time_kernel(rt, ck, rargs, meta, steps: int, warmup: int, torch, **launch) 
     return wall_ms, trials[EVENT_TRIALS // 2] * 1e3
 
 
+def _interleaved_event_ms(rt, ck, rargs, meta, fn, steps: int, torch, **launch) -> tuple[float, float]:
+    """(eas ms/launch, torch ms/call): EVENT_TRIALS trials of ``steps`` back-to-back launches of
+    each, alternating eas and torch trial by trial, medians of each.  The shader clock keeps
+    ramping for a while after a burst starts, so timing one side's trials after the other's
+    gives the later side a faster clock; alternating gives both the same.  Both are settled
+    before (``_time_kernel``, ``_torch_event_ms``)."""
+    ours, theirs = [], []
+    for _ in range(EVENT_TRIALS):
+        ours.append(rt.benchmark(ck, rargs, meta, repeat=steps, warmup=0, **launch) * 1e3)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            fn()
+        t1.record()
+        t1.synchronize()
+        theirs.append(t0.elapsed_time(t1) / steps)
+    return sorted(ours)[EVENT_TRIALS // 2], sorted(theirs)[EVENT_TRIALS // 2]
+
+
 def _torch_event_ms(fn, steps: int, warmup: int, torch) -> float:
     """ms per call of a torch operation on torch's current stream: the median of EVENT_TRIALS
     trials of ``steps`` back-to-back calls between torch events (the vendor comparison), after
@@ -248,6 +268,24 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded",
     ck = kern.compile(*args, **meta)
     compile_s = time.perf_counter() - t0
     wall_ms, ev_ms = _time_kernel(rt, ck, rargs, meta, steps, warmup, torch, grid=grid, tptg=tptg)
+    tms = vendor_op = None
+    if data == "seeded":
+        # vendor comparison on the same device-resident operands, with the eas kernel's output
+        # dtype: hipBLASLt/rocBLAS through torch.matmul (fp32, and f16 output), or torch.mm with
+        # out_dtype=float32 for 16-bit inputs into an f32 C.  After both are settled, their event
+        # trials alternate and both medians come from them.
+        A2, B2 = a.view(m, k), b.view(k, n)
+        if out_dt == torch.float32 and a.dtype != torch.float32:
+            mm = lambda: torch.mm(A2, B2, out_dtype=torch.float32)  # noqa: E731
+            vendor_op = "torch.mm(A, B, out_dtype=torch.float32)"
+        else:
+            out_t = torch.empty((m, n), dtype=a.dtype, device=dev)
+            mm = lambda: torch.matmul(A2, B2, out=out_t)  # noqa: E731
+            vendor_op = "torch.matmul(A, B, out=C)"
+        _torch_event_ms(mm, steps, warmup, torch)
+        ev_ms, tms = _interleaved_event_ms(rt, ck, rargs, meta, mm, steps, torch, grid=grid, tptg=tptg)
+        del mm
+        out_t = None
     flops = 2.0 * m * n * k
     # parity: rows sampled with a fixed seed, float64 reference of the (rounded) inputs
     c.fill_(float("nan"))
@@ -287,16 +325,11 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded",
     }
     _log(f"{name}: {res['TFLOP/s']} TFLOP/s ({100 * res['frac']:.1f}% of {peak}), {ev_ms:.4f} ms/launch, "
          f"parity {res['parity']}, compile {compile_s:.1f} s")
-    # vendor comparison on the same device-resident operands: torch.matmul (hipBLASLt/rocBLAS),
-    # whose output has the input dtype (the f32-output eas lines write twice its output bytes)
-    if data == "seeded":
-        A2, B2 = a.view(m, k), b.view(k, n)
-        out_t = torch.empty((m, n), dtype=a.dtype, device=dev)
-        tms = _torch_event_ms(lambda: torch.matmul(A2, B2, out=out_t), steps, warmup, torch)
-        res["torch_matmul"] = {"TFLOP/s": round(flops / (tms * 1e-3) / 1e12, 1), "ms_per_launch": round(tms, 5),
-                               "out_dtype": str(a.dtype).replace("torch.", "")}
-        _log(f"{name}: torch.matmul {res['torch_matmul']['TFLOP/s']} TFLOP/s, {tms:.4f} ms/launch")
-        del out_t
+    if tms is not None:
+        res["torch_matmul"] = {"op": vendor_op, "TFLOP/s": round(flops / (tms * 1e-3) / 1e12, 1),
+                               "ms_per_launch": round(tms, 5), "out_dtype": str(out_dt).replace("torch.", ""),
+                               "timing": "event trials alternating with the eas kernel's"}
+        _log(f"{name}: {vendor_op} {res['torch_matmul']['TFLOP/s']} TFLOP/s, {tms:.4f} ms/launch")
     if cpu_baseline and data == "seeded":
         res["cpu_baseline"] = _matmul_cpu_baseline(name, ha, hb, m, n, k)
         _log(f"{name}: cpu baseline {res['cpu_baseline']['value']} TFLOP/s ({res['cpu_baseline']['cores']} threads)")
@@ -785,7 +818,7 @@ def _matmul_main(args, rt, torch) -> int:
                      {"bound": res["bound"], "achieved": res["TFLOP/s"], "peak": res["peak_TFLOP/s"],
                       "unit": "TFLOP/s", "frac": res["frac"], "traffic": traffic}),
         "cpu_baseline": (dict(res["cpu_baseline"], host=_host_info()) if "cpu_baseline" in res else None),
-        "vendor": ({"op": "torch.matmul(A, B, out=C)", **res["torch_matmul"]} if "torch_matmul" in res else None),
+        "vendor": (dict(res["torch_matmul"]) if "torch_matmul" in res else None),
         "settle": {"untimed_launches_before_warmup": list(SETTLE_LOG),
                    "rule": f"batches of {SETTLE_BATCH} until two agree within 2%"},
         "extra": {},
