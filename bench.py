@@ -338,7 +338,7 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded",
     return res
 
 
-# --phases: in-kernel timestamps of the 8-wave GEMM entry.  s_memrealtime counts a constant
+# --phases: in-kernel timestamps of the 8-wave GEMM entry (the fp32 entries: below).  s_memrealtime counts a constant
 # 100 MHz clock; hardware register XCC_ID (id 20, bits 0-3) names the XCD a workgroup runs on.
 _PHASE_SLOTS = 8  # per wave group: entry, loop start, loop end, stores issued, stores done, XCD id
 _PHASE_STAMP = (
@@ -383,12 +383,55 @@ def _stamped_pp_source(src: str, entry: str) -> str:
     return _PHASE_STAMP + src
 
 
+# The fp32 entries: lane 0 of consumer wave 0 of each workgroup stamps slots 0-4 as above and the
+# XCD id (slot 5); slots 6 and 7 take s_memtime, which counts shader clocks, at the start and end
+# of the K loop, so the loop's clocks per BK = 32 stage come out independent of the clock rate.
+_PHASE_STAMP_F32 = (
+    "#define EAS_F32_STAMP(slot) do { if (threadIdx.x == 0) "
+    "__eas_stamps[blockIdx.x * 8u + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)\n"
+    "#define EAS_F32_CLOCK(slot) do { if (threadIdx.x == 0) "
+    "__eas_stamps[blockIdx.x * 8u + (slot)] = __builtin_amdgcn_s_memtime(); } while (0)\n"
+    "#define EAS_F32_XCD() do { if (threadIdx.x == 0) __eas_stamps[blockIdx.x * 8u + 5u] = "
+    "(unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u); } while (0)\n")
+
+
+def _stamped_f32_source(src: str, entry: str) -> str:
+    """The generated fp32 GEMM source with a stamp buffer appended to ``entry``'s arguments (either
+    fp32 entry) and stamps at: entry, start of the K loop (stage 0 landed), end of the K loop (last
+    MFMA issued), C stores issued, C stores complete.  Raises if the entry does not have the
+    expected shape."""
+    src = src.split("\n", 1)[1]  # the eas-launch line describes the unstamped argument list
+    start = src.rindex('extern "C"', 0, src.index(f"void {entry}("))
+    nxt = src.find('extern "C"', start + 10)
+    end = nxt if nxt >= 0 else len(src)
+    body = src[start:end]
+    edits = [
+        ("  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n",
+         "  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n  EAS_F32_STAMP(0);\n  EAS_F32_XCD();\n"),
+        ("  __syncthreads();  // stage 0 landed\n",
+         "  __syncthreads();  // stage 0 landed\n  EAS_F32_STAMP(1);\n  EAS_F32_CLOCK(6);\n"),
+        ("  } else {\n    mfmas(a0, b0);\n  }\n",
+         "  } else {\n    mfmas(a0, b0);\n  }\n  EAS_F32_STAMP(2);\n  EAS_F32_CLOCK(7);\n"),
+    ]
+    for old, new in edits:
+        if body.count(old) != 1:
+            raise RuntimeError(f"--phases: unexpected fp32 GEMM source shape at {old[:48]!r}")
+        body = body.replace(old, new)
+    close = body.index(") {")
+    body = body[:close] + ",\n    unsigned long long* __restrict__ __eas_stamps" + body[close:]
+    last = body.rindex("}")
+    body = body[:last] + "  EAS_F32_STAMP(3);\n  __builtin_amdgcn_s_waitcnt(0);\n  EAS_F32_STAMP(4);\n" + body[last:]
+    return _PHASE_STAMP_F32 + src[:start] + body + src[end:]
+
+
 def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
-    """Per-phase time budget of one launch of the 8-wave GEMM entry on the configuration's seeded
-    inputs: after settling, ``trials`` times run ``lead`` launches back to back and one more, and
-    read the last launch's stamps.  Medians over the trials of: spread of workgroup starts,
-    prologue, K loop (median, min, max over wave groups, median per XCD), C store issue, store
-    completion, median and last end; all in microseconds from the first workgroup's start."""
+    """Per-phase time budget of one launch of the 8-wave GEMM entry, or of either fp32 entry, on
+    the configuration's seeded inputs: after settling, ``trials`` times run ``lead`` launches back
+    to back and one more, and read the last launch's stamps.  Medians over the trials of: spread
+    of workgroup starts, prologue, K loop (median, min, max over wave groups, median per XCD), C
+    store issue, store completion, median and last end; all in microseconds from the first
+    workgroup's start.  The fp32 entries add the K loop's shader clocks per BK = 32 stage and the
+    shader clock they imply."""
     import kernels as K
     from easy_as_amd.runtime.hip import compile_code, plan_launch, struct
 
@@ -396,17 +439,27 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
     dev = torch.device("cuda:0")
     ha, hb = _matmul_inputs(name, torch)
     a, b = (x.to(dev) if isinstance(x, torch.Tensor) else torch.from_numpy(x).to(dev) for x in (ha, hb))
-    out_dt = torch.float32 if kname in ("matmul_mma_kernel", "matmul_mma_bf16_kernel") else torch.float16
+    tiled = kname == "matmul_tiled_kernel"
+    out_dt = torch.float32 if kname in ("matmul_mma_kernel", "matmul_mma_bf16_kernel") or tiled else torch.float16
     c = torch.zeros(m * n, dtype=out_dt, device=dev)
-    ck = getattr(K, kname).compile(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512)
-    args = {"a": a, "b": b, "c": c, "M": m, "N": n}
+    if tiled:
+        ck = K.matmul_tiled_kernel.compile(a, b, c, m, n, 0, 0, BM=32, BN=32, BK=32, K=k, NT=256)
+        args = {"a": a, "b": b, "c": c, "M": m, "N": n, "PID_M_BASE": 0, "PID_N_BASE": 0}
+    else:
+        ck = getattr(K, kname).compile(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512)
+        args = {"a": a, "b": b, "c": c, "M": m, "N": n}
     mod = rt._mod()
     plan = plan_launch(ck, args, grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), compute_units=rt._cus)
-    if plan is None or not plan.entry.endswith("__pp"):
-        raise RuntimeError(f"--phases needs the 8-wave GEMM entry; {name} launches {plan and plan.entry}")
-    kern = mod.load(compile_code(mod, _stamped_pp_source(ck.src, plan.entry), ck.ir.name), plan.entry)
+    entry = plan.entry or ck.geometry.entry if plan is not None else None
+    if tiled:
+        src, per_wg = _stamped_f32_source(ck.src, entry), 1
+    elif entry is None or not entry.endswith("__pp"):
+        raise RuntimeError(f"--phases needs the 8-wave GEMM entry; {name} launches {entry}")
+    else:
+        src, per_wg = _stamped_pp_source(ck.src, entry), 2
+    kern = mod.load(compile_code(mod, src, ck.ir.name), entry)
     groups = plan.grid[0] * plan.grid[1] * plan.grid[2]
-    stamps = torch.zeros(groups * 2 * _PHASE_SLOTS, dtype=torch.int64, device=dev)
+    stamps = torch.zeros(groups * per_wg * _PHASE_SLOTS, dtype=torch.int64, device=dev)
     argv, writable, _, stream = rt.build_argv(ck.ir, args, ck.writes)
     argv += [struct.pack("<I", h) for h in plan.hidden] + [mod.wrap_pointer(stamps.data_ptr(), stamps.nbytes,
                                                                             stamps)]
@@ -422,17 +475,23 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
         rt.synchronize()
         return time.perf_counter() - t0
 
-    _settle_until_stable(batch, plan.entry + " (stamped)")
+    _settle_until_stable(batch, entry + " (stamped)")
     runs = []
     for _ in range(trials):
         launches(lead + 1)
         rt.synchronize()
-        s = stamps.cpu().numpy().reshape(groups, 2, _PHASE_SLOTS)
+        s = stamps.cpu().numpy().reshape(groups, per_wg, _PHASE_SLOTS)
         xcd = s[:, 0, 5].astype(np.int64)
         t = s[:, :, :5].astype(np.float64) * 0.01  # 100 MHz ticks -> us
         t -= t[:, :, 0].min()
         loop = t[:, :, 2] - t[:, :, 1]
-        runs.append({
+        if tiled:  # shader clocks over the K loop (slots 6, 7), per BK = 32 stage
+            clk = (s[:, 0, 7] - s[:, 0, 6]).astype(np.float64)
+            runs.append({"loop_clocks_per_stage": float(np.median(clk)) / -(-k // 32),
+                         "loop_shader_GHz": float(np.median(clk / (loop[:, 0] * 1e3)))})
+        else:
+            runs.append({})
+        runs[-1].update({
             "start_spread": t[:, :, 0].max(), "prologue": np.median(t[:, :, 1] - t[:, :, 0]),
             "loop_median": np.median(loop), "loop_min": loop.min(), "loop_max": loop.max(),
             "store_issue": np.median(t[:, :, 3] - t[:, :, 2]), "store_complete": np.median(t[:, :, 4] - t[:, :, 3]),
@@ -446,9 +505,15 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
     out["loop_median_per_xcd"] = [round(float(np.median([r["loop_median_per_xcd"][x] for r in runs])), 2)
                                   for x in range(8) if runs[0]["loop_median_per_xcd"][x] is not None]
     out["workgroup_to_xcd_is_modulo_8"] = all(r["workgroup_to_xcd_is_modulo_8"] for r in runs)
-    out.update({"unit": "us", "entry": plan.entry, "workgroups": groups, "trials": trials,
+    out.update({"unit": "us", "entry": entry, "workgroups": groups, "trials": trials,
                 "method": f"median over {trials} trials of the last of {lead + 1} back-to-back launches; "
-                          "s_memrealtime stamps by lane 0 of each wave group"})
+                          "s_memrealtime stamps by lane 0 of each wave group"
+                          + (" (consumer wave 0); s_memtime shader clocks over the K loop" if tiled else "")})
+    if tiled:
+        out["loop_clocks_per_stage"] = round(float(np.median([r["loop_clocks_per_stage"] for r in runs])), 1)
+        out["loop_shader_GHz"] = round(float(np.median([r["loop_shader_GHz"] for r in runs])), 3)
+        # v_mfma_f32_32x32x2_f32 keeps a SIMD's MFMA pipe 64 clocks; 16 steps of 2 k per stage
+        out["mfma_clocks_per_stage"] = 64 * 16 * (4 if entry.endswith("__t128") else 1)
     del a, b, c, stamps
     torch.cuda.empty_cache()
     return out
@@ -605,8 +670,9 @@ def main() -> int:
                    help="matmul workloads only: M,N,K instead of the configuration's shape (a scaling study, "
                         "not the metric)")
     p.add_argument("--phases", action="store_true",
-                   help="matmul workloads on the 8-wave GEMM entry: add an in-kernel per-phase time budget "
-                        "of one launch (a stamped copy of the kernel, timed after the measurement)")
+                   help="matmul workloads on the 8-wave GEMM entry or an fp32 entry: add an in-kernel "
+                        "per-phase time budget of one launch (a stamped copy of the kernel, timed after the "
+                        "measurement; the fp32 entries also give shader clocks per K stage)")
     p.add_argument("--data", choices=MATMUL_DATA, default="seeded",
                    help="matmul workloads only: input data (anything but 'seeded' is not the metric's data)")
     args = p.parse_args()

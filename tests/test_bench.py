@@ -89,6 +89,55 @@ def test_stamped_source_rejects_an_unexpected_shape():
                                  plan.entry)
 
 
+def _f32_source(name: str):
+    from easy_as_amd.runtime.hip import plan_launch
+
+    kname, m, n, k, *_ = bench._config(name)
+    z = np.zeros(1, np.float32)
+    ck = K.matmul_tiled_kernel.compile(z, z, z, m, n, 0, 0, BM=32, BN=32, BK=32, K=k, NT=256)
+    plan = plan_launch(ck, {"M": m, "N": n, "PID_M_BASE": 0, "PID_N_BASE": 0},
+                       grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), compute_units=256)
+    return ck, plan.entry or ck.geometry.entry
+
+
+@pytest.mark.parametrize("name, entry", [("tiled1024", "matmul_tiled_kernel"),
+                                         ("tiled2048", "matmul_tiled_kernel__t128")])
+def test_stamped_f32_source_stamps_only_its_entry(name, entry):
+    from easy_as_amd.runtime.hip import compile_code
+    from easy_as_amd.runtime.hip_ext import load_hip_ext
+
+    ck, got = _f32_source(name)
+    assert got == entry
+    src = bench._stamped_f32_source(ck.src, entry)
+    for slot in range(5):
+        assert src.count(f"EAS_F32_STAMP({slot});") == 1
+    assert src.count("EAS_F32_CLOCK(6);") == src.count("EAS_F32_CLOCK(7);") == src.count("EAS_F32_XCD();") == 1
+    assert src.count("unsigned long long* __restrict__ __eas_stamps") == 1
+    mod = load_hip_ext(require=False)
+    if mod is not None:
+        assert compile_code(mod, src, ck.ir.name)[:4] == b"\x7fELF"
+    with pytest.raises(RuntimeError, match="unexpected fp32 GEMM source shape"):
+        bench._stamped_f32_source(ck.src.replace("  __syncthreads();  // stage 0 landed\n", "  __syncthreads();\n"),
+                                  entry)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name, stages, mfma_clocks", [("tiled1024", 32, 1024), ("tiled2048", 64, 4096)])
+def test_phases_of_the_fp32_entries(name, stages, mfma_clocks):
+    import torch
+
+    from easy_as_amd.runtime import get_runtime
+
+    print(f"phases: {name}", flush=True)
+    ph = bench._gemm_phases(name, get_runtime("hip"), torch, trials=2, lead=3)
+    assert ph["workgroups"] == 256 and ph["mfma_clocks_per_stage"] == mfma_clocks
+    assert ph["workgroup_to_xcd_is_modulo_8"] is True and len(ph["loop_median_per_xcd"]) == 8
+    assert 0 < ph["prologue"] < ph["loop_median"] < ph["end_median"] <= ph["end_last"] < 1000
+    # a stage costs at least its MFMAs; the shader clock is a plausible one
+    assert mfma_clocks <= ph["loop_clocks_per_stage"] < 2 * mfma_clocks
+    assert 0.5 < ph["loop_shader_GHz"] < 3.0
+
+
 @pytest.mark.gpu
 def test_phases_of_a_short_k_launch(monkeypatch):
     import torch
