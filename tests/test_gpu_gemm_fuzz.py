@@ -46,7 +46,7 @@ def test_shapes_cover_the_edges():
 
 
 @pytest.mark.parametrize("seed", CASES)
-def test_random_shape_matches_float64(gpu_runtime, seed):
+def test_random_shape_matches_float64(gpu_runtime, monkeypatch, seed):
     torch = pytest.importorskip("torch")
     kind, m, n, k = _shape(seed)
     print(f"gemm fuzz {seed}: {kind} M={m} N={n} K={k}", flush=True)
@@ -54,13 +54,20 @@ def test_random_shape_matches_float64(gpu_runtime, seed):
     if kind == "tiled_f32":
         a = (rng.standard_normal(m * k, dtype=np.float32) / np.float32(math.sqrt(k))).astype(np.float32)
         b = (rng.standard_normal(k * n, dtype=np.float32) / np.float32(math.sqrt(k))).astype(np.float32)
-        c = np.full(m * n + PAD, np.nan, np.float32)
         bm, bn, bk, nt = (32, 32, 32, 256) if seed % 8 < 4 else (16, 64, 16, 256)
-        K.matmul_tiled_kernel(a, b, c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
-                              _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
         ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
-        got, tail = c[:m * n], c[m * n:]
         bar = 1e-5 * math.sqrt(k)
+        # the 128 x 128-tile entry too (its edge tiles, K tail and zero-filled stages)
+        for choice in ("tile128", "auto"):
+            monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
+            c = np.full(m * n + PAD, np.nan, np.float32)
+            K.matmul_tiled_kernel(a, b, c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
+                                  _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
+            got, tail = c[:m * n], c[m * n:]
+            if choice == "tile128":
+                assert np.isnan(tail).all() and np.isfinite(got).all(), f"tile128 M={m} N={n} K={k}"
+                err = ops.rel_err(np.asarray(got, np.float64).reshape(m, n), ref)
+                assert err <= bar, f"tile128 M={m} N={n} K={k}: rel err {err:.3e} > {bar:.3e}"
     elif kind == "bf16_f32":
         a_bits = ops.f32_to_bf16(rng.uniform(-1, 1, m * k).astype(np.float32))
         b_bits = ops.f32_to_bf16(rng.uniform(-1, 1, k * n).astype(np.float32))
