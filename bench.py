@@ -519,6 +519,187 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
     return out
 
 
+# --workload loadcost: what a 16-byte-per-lane LDS-DMA load costs the MFMA pipe of a SIMD, the
+# measurement behind the fp32 GEMM entries' producer waves.  One workgroup per CU; each MFMA wave
+# runs 4 independent v_mfma_f32_32x32x2_f32 chains, 16 MFMAs per iteration (1024 clocks of MFMA
+# pipe), and counts its shader clocks (s_memtime).  Modes: 0 MFMAs only; 1 MFMA waves that also
+# issue LOADS loads per 16 MFMAs (spread one per MFMA slot); 3 waves NW/2.. issue LOADS loads per
+# 16 MFMAs of their sibling with SGPR-only addressing (no VALU); 2 the same with VALU addressing,
+# running until the MFMA waves are done (a flag in LDS, bounded).  Every load reads inside a
+# 256 MiB buffer (offsets masked) and writes its wave's own 1 KB of LDS.
+_LOADCOST_SRC = r"""
+typedef float lc_f32x16 __attribute__((ext_vector_type(16)));
+typedef int lc_rsrc __attribute__((ext_vector_type(4)));
+static __device__ __forceinline__ lc_rsrc lc_make_rsrc(const void* p, unsigned bytes) {
+  const unsigned long long a = (unsigned long long)p;
+  lc_rsrc r;
+  r[0] = (int)(unsigned)a; r[1] = (int)((unsigned)(a >> 32) & 0xffffu); r[2] = (int)bytes; r[3] = 0x00020000;
+  return r;
+}
+static __device__ __forceinline__ void lc_dma(lc_rsrc r, unsigned voff, unsigned lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds) : "memory");
+}
+static __device__ __forceinline__ void lc_dma_s(lc_rsrc r, unsigned voff, unsigned soff, unsigned lds) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(lds) : "memory");
+}
+template <int MODE, int NW, int LOADS>
+static __device__ void lc_body(const float* src, unsigned bytes, float* out, unsigned long long* clk, int iters) {
+  __shared__ __attribute__((aligned(1024))) float lds[8 * 256];
+  __shared__ int done;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (threadIdx.x == 0) done = 0;
+  __syncthreads();
+  const lc_rsrc r = lc_make_rsrc(src, bytes);
+  const unsigned ldsw = (unsigned)(size_t)(__attribute__((address_space(3))) float*)lds + wave * 1024;
+  const unsigned mask = bytes - 1;  // bytes is a power of two
+  unsigned voff = ((blockIdx.x * NW + wave) * 64 + lane) * 16;
+  lc_f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  const float a = lane * 1e-3f, b = 1.0f + wave;
+  const bool mfma_wave = MODE < 2 || wave < NW / 2;
+  int n = 0;
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  if (mfma_wave) {
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        lc_f32x16& c = (m & 3) == 0 ? c0 : (m & 3) == 1 ? c1 : (m & 3) == 2 ? c2 : c3;
+        c = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+        if (MODE == 1 && (m * LOADS) / 16 != ((m + 1) * LOADS) / 16) {
+          lc_dma(r, voff & mask, ldsw);
+          voff += 1u << 20;
+        }
+        if (MODE == 1) __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (MODE == 2 && lane == 0) __hip_atomic_fetch_add(&done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  } else if (MODE == 3) {
+    const unsigned v0 = (((blockIdx.x * NW + wave) * 64 + lane) * 16) & ((1u << 21) - 1);
+    const int total = iters * LOADS / 8;
+    for (int it = 0; it < total; ++it) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) lc_dma_s(r, v0, ((unsigned)(it * 8 + j) & 127u) << 21, ldsw);  // < 2^28
+      n += 8;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  } else {
+    for (int it = 0; it < iters * 64; ++it) {  // bounded; ends when every MFMA wave is done
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        lc_dma(r, voff & mask, ldsw);
+        voff += 1u << 20;
+      }
+      n += 8;
+      if (__hip_atomic_load(&done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= NW / 2) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  if (lane == 0) {
+    // start, end, loads issued, SIMD id (HW_ID bits 5:4)
+    clk[(blockIdx.x * 8 + wave) * 4] = t0;
+    clk[(blockIdx.x * 8 + wave) * 4 + 1] = t1;
+    clk[(blockIdx.x * 8 + wave) * 4 + 2] = (unsigned long long)n;
+    clk[(blockIdx.x * 8 + wave) * 4 + 3] = (unsigned long long)__builtin_amdgcn_s_getreg(4 | (4 << 6) | (1 << 11));
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) s += c0[e] + c1[e] + c2[e] + c3[e];
+  out[blockIdx.x * 512 + threadIdx.x] = s;
+}
+#define LC_ENTRY(NAME, MODE, NW, LOADS) \
+  extern "C" __global__ __launch_bounds__(512) void NAME(const float* src, unsigned bytes, float* out, \
+                                                         unsigned long long* clk, int iters) { \
+    lc_body<MODE, NW, LOADS>(src, bytes, out, clk, iters); \
+  }
+LC_ENTRY(lc_w4_mfma, 0, 4, 0)
+LC_ENTRY(lc_w4_loads1, 1, 4, 1)
+LC_ENTRY(lc_w4_loads2, 1, 4, 2)
+LC_ENTRY(lc_w4_loads4, 1, 4, 4)
+LC_ENTRY(lc_w8_mfma, 0, 8, 0)
+LC_ENTRY(lc_w8_loads1, 1, 8, 1)
+LC_ENTRY(lc_w8_loads2, 1, 8, 2)
+LC_ENTRY(lc_w8_salu_producers1, 3, 8, 1)
+LC_ENTRY(lc_w8_salu_producers2, 3, 8, 2)
+LC_ENTRY(lc_w8_valu_producers, 2, 8, 0)
+"""
+# (entry, waves per workgroup, what it shows)
+_LOADCOST_CASES = (
+    ("lc_w4_mfma", 4, "1 wave per SIMD, MFMAs only"),
+    ("lc_w4_loads1", 4, "1 wave per SIMD, 1 load per 16 MFMAs"),
+    ("lc_w4_loads2", 4, "1 wave per SIMD, 2 loads per 16 MFMAs"),
+    ("lc_w4_loads4", 4, "1 wave per SIMD, 4 loads per 16 MFMAs"),
+    ("lc_w8_mfma", 8, "2 waves per SIMD, MFMAs only"),
+    ("lc_w8_loads1", 8, "2 waves per SIMD, each 1 load per 16 of its MFMAs"),
+    ("lc_w8_loads2", 8, "2 waves per SIMD, each 2 loads per 16 of its MFMAs"),
+    ("lc_w8_salu_producers1", 8, "MFMA wave + sibling issuing 1 load per 16 of its MFMAs, SGPR addressing"),
+    ("lc_w8_salu_producers2", 8, "MFMA wave + sibling issuing 2 loads per 16 of its MFMAs, SGPR addressing"),
+    ("lc_w8_valu_producers", 8, "MFMA wave + sibling issuing loads with VALU addressing"),
+)
+
+
+def _loadcost_main(rt, torch, iters: int = 2000) -> int:
+    """``--workload loadcost``: for each case of ``_LOADCOST_CASES``, the MFMA pipe's clocks per 16
+    MFMAs on each SIMD (median over the 256 workgroups' SIMDs, last of 3 launches; ideal 1024 in
+    every case): one MFMA wave on a SIMD counts its own span, two count from the earlier start to
+    the later end over both waves' MFMAs.  Also the loads the loading waves issued.  Prints a table
+    and one JSON line."""
+    import struct
+
+    from easy_as_amd.runtime.hip import compile_code
+
+    mod = rt._mod()
+    code = compile_code(mod, _LOADCOST_SRC, "loadcost")
+    dev = torch.device("cuda:0")
+    nbytes = 1 << 28
+    src = torch.zeros(nbytes // 4, dtype=torch.float32, device=dev)
+    out = torch.zeros(256 * 512, dtype=torch.float32, device=dev)
+    clk = torch.zeros(256 * 8 * 4, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(0).cuda_stream
+    argv = [mod.wrap_pointer(src.data_ptr(), src.nbytes, src), struct.pack("<I", nbytes),
+            mod.wrap_pointer(out.data_ptr(), out.nbytes, out), mod.wrap_pointer(clk.data_ptr(), clk.nbytes, clk),
+            struct.pack("<i", iters)]
+    writable = [False, False, True, True, False]
+    rows = []
+    for entry, nw, what in _LOADCOST_CASES:
+        kern = mod.load(code, entry)
+        for _ in range(3):
+            clk.zero_()
+            torch.cuda.synchronize()
+            mod.launch_groups(kern, argv, writable, (256, 1, 1), (64 * nw, 1, 1), stream=stream)
+        h = clk.cpu().numpy().reshape(256, 8, 4)[:, :nw].astype(np.float64)
+        mfma_waves = nw if "producers" not in entry else nw // 2
+        per_simd, shared = [], 0
+        for g in range(256):
+            for simd in range(4):
+                on = [w for w in range(mfma_waves) if int(h[g, w, 3]) == simd]
+                if on:
+                    span = h[g, on, 1].max() - h[g, on, 0].min()
+                    per_simd.append(span / (iters * len(on)))
+                    shared += len(on) > 1
+        loads = h[:, mfma_waves:nw, 2].reshape(-1)
+        row = {"case": what, "entry": entry,
+               "simd_clocks_per_16_mfma_median": round(float(np.median(per_simd)), 1),
+               "simd_clocks_per_16_mfma_max": round(float(np.max(per_simd)), 1),
+               "simds_with_two_mfma_waves": shared}
+        if loads.size:
+            row["loads_per_16_sibling_mfma"] = round(float(np.median(loads)) / iters, 2)
+        rows.append(row)
+        _log(f"loadcost: {what}: {row['simd_clocks_per_16_mfma_median']} clocks per 16 MFMAs of a SIMD (ideal 1024)"
+             + (f", loading waves issued {row['loads_per_16_sibling_mfma']} loads per 16 sibling MFMAs"
+                if loads.size else ""))
+    base = rows[0]["simd_clocks_per_16_mfma_median"]
+    per_load = round((rows[2]["simd_clocks_per_16_mfma_median"] - base) / 2, 1)
+    print(json.dumps({"metric": "MFMA pipe clocks lost per 16-byte-per-lane load issued by the MFMA wave",
+                      "value": per_load, "unit": "clocks", "higher_is_better": False, "n_gpus": 1,
+                      "config": {"workload": "loadcost microbenchmark (v_mfma_f32_32x32x2_f32 chains + LDS DMA)",
+                                 "workgroups": 256, "iterations": iters}, "cases": rows}), flush=True)
+    del src, out, clk
+    return 0
+
+
 def _host_info() -> dict:
     """The CPU side of the GPU box: core counts, model, NumPy and its BLAS."""
     import os
@@ -662,7 +843,8 @@ def main() -> int:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(MATMULS), default="add")
+    p.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(MATMULS) + ["loadcost"], default="add",
+                   help="loadcost: the microbenchmark of what a load costs the MFMA pipe (not a config)")
     p.add_argument("--block", type=int, default=PRIMARY_BLOCK)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true")
@@ -703,6 +885,8 @@ def main() -> int:
 
     rt = get_runtime("hip")
     dev = torch.device("cuda:0")
+    if args.workload == "loadcost":
+        return _loadcost_main(rt, torch)
     if args.workload in MATMULS:
         return _matmul_main(args, rt, torch)
     kname, nin, per_elem = WORKLOADS[args.workload]

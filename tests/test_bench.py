@@ -1,11 +1,13 @@
-"""bench.py's command line and its GEMM phase-stamp instrumentation.
+"""bench.py's command line, its GEMM phase-stamp instrumentation and its load-cost microbenchmark.
 
-The CPU tests check argument handling and that the stamped copy of each 8-wave GEMM source is
-built (the edits find their anchors in the generated source, and hiprtc compiles the result);
-the GPU test runs the stamped kernel once at a short K and checks the phases it reports."""
+The CPU tests check argument handling and that the stamped copies of the 8-wave and fp32 GEMM
+sources are built (the edits find their anchors in the generated source, and hiprtc compiles the
+result), and that the microbenchmark source compiles with every case; the GPU tests run the
+stamped kernels and the microbenchmark once and check what they report."""
 
 from __future__ import annotations
 
+import json
 import sys
 from pathlib import Path
 
@@ -155,3 +157,33 @@ def test_phases_of_a_short_k_launch(monkeypatch):
     assert ph["store_issue"] > 0 and ph["store_complete"] >= 0
     # 16 stages of BK = 32: a few microseconds of loop, well under a millisecond
     assert np.isfinite(ph["end_last"]) and ph["end_last"] < 1000
+
+
+def test_loadcost_source_has_every_case():
+    from easy_as_amd.runtime.hip import compile_code
+    from easy_as_amd.runtime.hip_ext import load_hip_ext
+
+    entries = [e for e, _, _ in bench._LOADCOST_CASES]
+    assert len(set(entries)) == len(entries)
+    for e, nw, _ in bench._LOADCOST_CASES:
+        assert f"LC_ENTRY({e}," in bench._LOADCOST_SRC and nw in (4, 8)
+    mod = load_hip_ext(require=False)
+    if mod is None:
+        pytest.skip("the _hip extension is not built")
+    code = compile_code(mod, bench._LOADCOST_SRC, "loadcost")
+    assert code[:4] == b"\x7fELF"
+
+
+@pytest.mark.gpu
+def test_loadcost_runs(capsys):
+    import torch
+
+    from easy_as_amd.runtime import get_runtime
+
+    print("loadcost microbenchmark", flush=True)
+    assert bench._loadcost_main(get_runtime("hip"), torch, iters=200) == 0
+    line = json.loads(capsys.readouterr().out.strip().splitlines()[-1])
+    rows = {r["entry"]: r for r in line["cases"]}
+    # MFMAs alone run at one per 64 clocks; loads a sibling issues with SGPR addressing are free
+    assert 1000 < rows["lc_w4_mfma"]["simd_clocks_per_16_mfma_median"] < 1100
+    assert rows["lc_w8_salu_producers2"]["loads_per_16_sibling_mfma"] == 2.0
