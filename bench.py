@@ -363,8 +363,8 @@ def _stamped_pp_source(src: str, entry: str) -> str:
     edits = [
         (body, body.replace("eas_op_t* smem) {", "eas_op_t* smem, unsigned long long* __eas_stamps) {")
          + "  EAS_STAMP(0);\n  EAS_STAMP_XCD();\n"),
-        ("  if (g == 1) __syncthreads();\n  for (int kt = 0; kt < KT; ++kt) {",
-         "  if (g == 1) __syncthreads();\n  EAS_STAMP(1);\n  for (int kt = 0; kt < KT; ++kt) {"),
+        ("    if (g == 1) __syncthreads();\n    for (int kt = 0; kt < KT; ++kt) stage(kt, kt % NSTAGE, b_fast);",
+         "    if (g == 1) __syncthreads();\n    EAS_STAMP(1);\n    for (int kt = 0; kt < KT; ++kt) stage(kt, kt % NSTAGE, b_fast);"),
         ("  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier\n",
          "  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier\n  EAS_STAMP(2);\n"),
         ("(CT)acc16[i][j][r];\n        }\n  }\n}",

@@ -345,6 +345,10 @@ static __device__ __forceinline__ void eas_gemm_dma(const eas_op_t* __restrict__
 // MI selects the MFMA: 32 (v_mfma_f32_32x32x16: each wave's 128 x 64 as 4 x 2 tiles of 32 x 32,
 // two k-steps of 16 per stage) or 16 (v_mfma_f32_16x16x32: 8 x 4 tiles of 16 x 16, one k-step of
 // 32 per stage; fewer accumulator bytes move through the MFMA per flop).  Same LDS reads per stage.
+template <bool V>
+struct eas_bool_c {  // a compile-time flag passed as a value (to select a loop version)
+  static constexpr bool value = V;
+};
 template <typename CT, int K, int MI = 32>
 static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                    CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
@@ -376,19 +380,38 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
     const int c_b = (lane & 31) ^ bsw(r_b);
     b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
     b_k[i] = r_b;
+    // rows past M read zeros through an offset past the range (a row offset could wrap in 32 bits)
+    if (m0 + r_a >= M) a_off[i] = 0x80000000u;
   }
   const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS eas_op_t*)As, lds_b = (uint32_t)(size_t)(EAS_LDS eas_op_t*)Bs;
-  auto dma_one = [&](int kt, int d) {  // d: 0, 1 A; 2, 3 B
+  // Every stage but a K tail, and for B every stage of a tile whose columns all lie below N, puts
+  // the stage's offset in soffset (an SGPR) and keeps the lane offsets fixed: the load phase then
+  // runs no VALU for its DMA, VALU that the other wave of the SIMD, busy with MFMAs, would hold
+  // back.  Those loads read inside A and B whatever the range check does with soffset.  The K tail
+  // stage and tiles at the right edge keep the whole offset in the VGPR, so the range check covers
+  // every dword.  Which B form a tile uses is a compile-time flag of its loop version (b_fast), so
+  // that the per-lane form's address math is not hoisted into every stage.
+  const bool b_inside = n0 + BN <= N;
+  auto dma_one = [&](int kt, int d, auto b_fast) {  // d: 0, 1 A; 2, 3 B
     const int s = kt % NSTAGE, i = d & 1;
     const uint32_t dst = (uint32_t)((s * STAGE_H + (wave * 2 + i) * 512) * 2);
+    const bool tail = K % BK != 0 && kt == KT - 1;
     if (d < 2) {
-      uint32_t off = a_off[i] + (uint32_t)(kt * BK * 2);
-      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: past the range -> zeros
-      eas_dma16(ra, off, lds_a + dst);
+      if (!tail) {
+        eas_dma16s(ra, a_off[i], (uint32_t)(kt * BK * 2), lds_a + dst);
+      } else {
+        uint32_t off = a_off[i] + (uint32_t)(kt * BK * 2);
+        if (kt * BK + a_k[i] >= K || a_off[i] >= 0x80000000u) off = 0x80000000u;  // past K or M: zeros
+        eas_dma16(ra, off, lds_a + dst);
+      }
     } else {
-      uint32_t off = b_off[i] + (uint32_t)kt * (uint32_t)(BK * 2) * (uint32_t)ldb;
-      if (K % BK != 0 && kt * BK + b_k[i] >= K) off = 0x80000000u;  // B rows past K
-      eas_dma16(rb, off, lds_b + dst);
+      if (decltype(b_fast)::value && !tail) {
+        eas_dma16s(rb, b_off[i], (uint32_t)kt * (uint32_t)(BK * 2) * (uint32_t)ldb, lds_b + dst);
+      } else {
+        uint32_t off = b_off[i] + (uint32_t)kt * (uint32_t)(BK * 2) * (uint32_t)ldb;
+        if (K % BK != 0 && kt * BK + b_k[i] >= K) off = 0x80000000u;  // B rows past K
+        eas_dma16(rb, off, lds_b + dst);
+      }
     }
   };
   int fa_off[2][4], fb_off[2][2][2];
@@ -438,11 +461,14 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
     const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
     return (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
   };
+  // The h = 1 half of a transposing B read is rows 4 further down with the same swizzle (rows r and
+  // r + 4 differ only in bit 2, which the swizzle does not read), i.e. fb*_off[..][1] is
+  // fb*_off[..][0] + 4 BN: written so, the compiler needs one address per read pair, not two.
   auto read_b = [&](int s, int ks, int j) {
-    fb[ks][j] = read_tr(Bs + s * STAGE_H, fb_off[ks][j][0], fb_off[ks][j][1]);
+    fb[ks][j] = read_tr(Bs + s * STAGE_H, fb_off[ks][j][0], fb_off[ks][j][0] + 4 * BN);
   };
   auto read_a16 = [&](int s, int i) { fa16[i] = *(const eas_h8*)(As + s * STAGE_H + fa16_off[i]); };
-  auto read_b16 = [&](int s, int j) { fb16[j] = read_tr(Bs + s * STAGE_H, fb16_off[j][0], fb16_off[j][1]); };
+  auto read_b16 = [&](int s, int j) { fb16[j] = read_tr(Bs + s * STAGE_H, fb16_off[j][0], fb16_off[j][0] + 4 * BN); };
   eas_f32x16 acc[4][2];
   eas_f32x4 acc16[8][4];
   if constexpr (MI == 32) {
@@ -468,23 +494,14 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
   // of stage kt+1 before b(2kt+2): group 0 at the end of its MFMA phase, group 1 at the end of its
   // load phase.  Stage kt+3 refills the buffer of stage kt-1, whose last reader (group 1) passed
   // b(2kt) before any wave issues that DMA.  Both groups execute the same number of barriers.
-#pragma unroll
-  for (int s = 0; s < NSTAGE - 1; ++s)
-    if (s < KT)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) dma_one(s, d);
-  wait_stage(KT - 1 < NSTAGE - 2 ? KT - 1 : NSTAGE - 2);
-  __syncthreads();
-  if (g == 1) __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int s = kt % NSTAGE;
-    const bool issue = kt + NSTAGE - 1 < KT;
+  // one stage of the K loop (s = kt % NSTAGE)
+  auto stage = [&](const int kt, const int s, auto b_fast) {
     const int later = KT - 2 - kt < NSTAGE - 2 ? KT - 2 - kt : NSTAGE - 2;
     // load phase: every fragment of stage kt, and this wave's quarter of stage kt+3
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      if (issue) dma_one(kt + NSTAGE - 1, u);
+      if (kt + NSTAGE - 1 < KT) dma_one(kt + NSTAGE - 1, u, b_fast);
       if constexpr (MI == 32) {
         read_a(s, u >> 1, 2 * (u & 1));
         read_a(s, u >> 1, 2 * (u & 1) + 1);
@@ -536,7 +553,22 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
     if (g == 0 && kt + 1 < KT) wait_stage(later);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-  }
+  };
+  auto k_loop = [&](auto b_fast) {
+#pragma unroll
+    for (int s = 0; s < NSTAGE - 1; ++s)
+      if (s < KT)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) dma_one(s, d, b_fast);
+    wait_stage(KT - 1 < NSTAGE - 2 ? KT - 1 : NSTAGE - 2);
+    __syncthreads();
+    if (g == 1) __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) stage(kt, kt % NSTAGE, b_fast);
+  };
+  if (b_inside)  // uniform over the workgroup
+    k_loop(eas_bool_c<true>{});
+  else
+    k_loop(eas_bool_c<false>{});
   if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier
   const bool full = (m0 + BM <= M) && (n0 + BN <= N);
   if constexpr (MI == 32) {

@@ -87,7 +87,7 @@ def test_stamped_source_compiles():
 def test_stamped_source_rejects_an_unexpected_shape():
     ck, plan = _pp_source("mma")
     with pytest.raises(RuntimeError, match="unexpected GEMM source shape"):
-        bench._stamped_pp_source(ck.src.replace("  if (g == 1) __syncthreads();\n  for (int kt", "  for (int kt"),
+        bench._stamped_pp_source(ck.src.replace("    if (g == 1) __syncthreads();\n    for (int kt", "    for (int kt"),
                                  plan.entry)
 
 
