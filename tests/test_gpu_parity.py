@@ -409,10 +409,12 @@ def test_tiled_matmul_split_launch_like_the_reference(gpu_runtime, monkeypatch, 
     assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
 
 
-@pytest.mark.parametrize("mnk", [(300, 260, 1000), (130, 300, 40), (257, 132, 36), (2048, 2048, 256)])
+@pytest.mark.parametrize("mnk", [(300, 260, 1000), (130, 300, 40), (257, 132, 36), (2048, 2048, 256),
+                                 (2048, 2048, 100), (4096, 3000, 96)])
 def test_tiled_fp32_entries_agree(gpu_runtime, monkeypatch, mnk):
     """The fp32 GEMM's 128 x 128-tile entry and its 64 x 64 default on the same launch (edge
-    tiles, K tails of 8 and 4 elements; 2048² picks the 128 tiles by itself)."""
+    tiles, K tails of 8 and 4 elements; 2048² picks the 128 tiles by itself, also with a K tail;
+    4096 x 3000 runs four 128 x 128 tiles per CU with a partial last column of tiles)."""
     from easy_as_amd.runtime.hip import plan_launch
 
     m, n, k = mnk
@@ -423,7 +425,7 @@ def test_tiled_fp32_entries_agree(gpu_runtime, monkeypatch, mnk):
     ck = K.matmul_tiled_kernel.compile(A, B, np.zeros(1, np.float32), m, n, 0, 0, **meta)
     args = {"a": A, "b": B, "c": np.zeros(m * n, np.float32), "M": m, "N": n, "PID_M_BASE": 0, "PID_N_BASE": 0}
     auto = plan_launch(ck, args, grid=grid).entry
-    assert auto == ("matmul_tiled_kernel__t128" if m == 2048 else None)
+    assert auto == ("matmul_tiled_kernel__t128" if m >= 2048 else None)
     ref = ops.matmul_ref(a2, b2)
     outs = {}
     for choice, entry in (("tile128", "matmul_tiled_kernel__t128"), ("auto", auto), ("4wave", None)):
