@@ -12,8 +12,9 @@ entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
   four waves alternate load phases and MFMA phases one barrier apart, each
   wave holding 128 x 64 of the tile (8 x 4 ``v_mfma_f32_16x16x32_f16``
   accumulators; ``EAS_HIP_GEMM_MFMA=32`` selects 4 x 2 of ``32x32x16``).
-* ``<name>__t128`` (256 threads): the same DMA operands on 128 x 128 tiles (4
-  waves of 64 x 64), for launches whose 256 x 256 grid would leave CUs idle.
+* ``<name>__t128`` (512 threads): the same DMA operands on 128 x 128 tiles, for
+  launches whose 256 x 256 grid would leave CUs idle: 4 waves issue the DMA, 4
+  waves of 64 x 64 read fragments and run the MFMAs.
 * ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
   AGPRs): the skinny path (launches of at most 128 rows), the 4-wave DMA body,
   and the register body; a uniform branch picks one per launch.
@@ -614,54 +615,94 @@ static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict
   }
 }
 
-// 128 x 128 tile body for launches whose 256 x 256 grid would leave CUs idle: 4 waves of 64 x 64
-// (2 x 2 accumulators of 32x32), the same DMA ring, swizzles and range checks as the 256 bodies
-// with 16 KB stages (64 KB of LDS, so two workgroups share a CU and overlap each other's waits).
-// Per stage: wait for this wave's DMA, barrier, issue this wave's quarter of the DMA three stages
-// ahead, read the stage's fragments, 8 MFMAs.
+// 128 x 128 tile body for launches whose 256 x 256 grid would leave CUs idle: 8 waves (512
+// threads), specialised like the fp32 entries, on a ring of 4 stages of 16 KB (64 KB of LDS).
+// Waves 4-7 produce: the DMA of stage kt+3, 2 A + 2 B loads of 1 KB per wave per stage, with the
+// stage offset in soffset, so the loads cost the MFMA waves sharing their SIMDs nothing.  Waves
+// 0-3 consume, 64 x 64 each (2 x 2 accumulators of 32x32x16): the fragments of stage kt+1 are
+// read between stage kt's 8 MFMAs.  A load costs the SIMD that issues it tens of clocks of MFMA
+// issue, which in the 4-wave form of this body (each wave loading its quarter of every stage
+// beside 8 MFMAs) was most of the stage.
 template <typename CT, int K>
 static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
                                                      eas_op_t* smem) {
   constexpr int BM = 128, BN = 128, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
-  constexpr int STAGE_H = BM * BK;  // halves per operand per stage (8 KB)
+  constexpr int STAGE_H = BM * BK;          // halves per operand per stage (8 KB)
+  constexpr int KLAST = K - (KT - 1) * BK;  // k extent of the last stage
   eas_op_t* As = smem;
   eas_op_t* Bs = smem + NSTAGE * STAGE_H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
-  const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
-  // DMA instruction q = 2 wave + i writes 1 KB of a stage.  A: rows 16q + lane/4, chunk lane%4
-  // stored at chunk ^ ((row/4)%4).  B: rows (k) 4q + lane/16, chunk lane%16 stored at chunk ^ 4(row%4).
-  uint32_t a_off[2], b_off[2];
-  int a_k[2], b_k[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = wave * 2 + i;
-    const int r_a = 16 * q + (lane >> 2);
-    const int c_a = (lane & 3) ^ ((r_a >> 2) & 3);
-    a_off[i] = ((uint32_t)(m0 + r_a) * (uint32_t)K + (uint32_t)(c_a * 8)) * 2u;
-    a_k[i] = c_a * 8;
-    const int r_b = 4 * q + (lane >> 4);
-    const int c_b = (lane & 15) ^ (4 * (r_b & 3));
-    b_off[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
-    b_k[i] = r_b;
-  }
-  const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS eas_op_t*)As, lds_b = (uint32_t)(size_t)(EAS_LDS eas_op_t*)Bs;
-  auto dma_stage = [&](int kt) {
-    const int s = kt % NSTAGE;
+  if (wave >= 4) {
+    // DMA instruction q = 2 pw + i writes 1 KB of a stage.  A: rows 16q + lane/4, chunk lane%4
+    // stored at chunk ^ ((row/4)%4).  B: rows (k) 4q + lane/16, chunk lane%16 stored at chunk ^ 4(row%4).
+    // Rows past M load zeros, and so do columns past N when no 8-column chunk straddles N, so
+    // every address a load reads, lane offset plus stage offset, lies inside A or B.  An edge tile
+    // whose chunk straddles N (N % 8 != 0) adds the stage offset to the lane offset instead, where
+    // the range check sees all of it.  The last stage of a K that is not a multiple of BK does the
+    // same (its straddling A chunk may end past A); stages past K load zeros into a slot nobody
+    // reads, so every stage issues 4 loads and the count at each barrier is the same.
+    const int pw = wave - 4;
+    const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
+    const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
+    const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS eas_op_t*)As, lds_b = (uint32_t)(size_t)(EAS_LDS eas_op_t*)Bs;
+    uint32_t a_off[2], a_tail[2], b_raw[2], b_off[2], b_tail[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint32_t dst = (uint32_t)((s * STAGE_H + (wave * 2 + i) * 512) * 2);
-      uint32_t off = a_off[i] + (uint32_t)(kt * BK * 2);
-      if (K % BK != 0 && kt * BK + a_k[i] >= K) off = 0x80000000u;  // K tail: past the range -> zeros
-      eas_dma16(ra, off, lds_a + dst);
-      uint32_t offb = b_off[i] + (uint32_t)kt * (uint32_t)(BK * 2) * (uint32_t)ldb;
-      if (K % BK != 0 && kt * BK + b_k[i] >= K) offb = 0x80000000u;  // B rows past K
-      eas_dma16(rb, offb, lds_b + dst);
+      const int q = pw * 2 + i;
+      const int r_a = 16 * q + (lane >> 2);
+      const int c_a = (lane & 3) ^ ((r_a >> 2) & 3);
+      const uint32_t a_raw = ((uint32_t)(m0 + r_a) * (uint32_t)K + (uint32_t)(c_a * 8)) * 2u;
+      a_off[i] = m0 + r_a < M ? a_raw : 0x80000000u;
+      a_tail[i] = (m0 + r_a < M && c_a * 8 < KLAST) ? a_raw + (uint32_t)((KT - 1) * BK * 2) : 0x80000000u;
+      const int r_b = 4 * q + (lane >> 4);
+      const int c_b = (lane & 15) ^ (4 * (r_b & 3));
+      b_raw[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
+      b_off[i] = n0 + c_b * 8 < N ? b_raw[i] : 0x80000000u;
+      b_tail[i] = r_b < KLAST ? b_raw[i] + (uint32_t)((KT - 1) * BK * 2) * (uint32_t)ldb : 0x80000000u;
     }
-  };
+    auto dma = [&](int kt, auto b_fast) {
+      const uint32_t st = (uint32_t)((kt % NSTAGE) * STAGE_H * 2);
+      const uint32_t sa = (uint32_t)(kt * BK * 2), sb = (uint32_t)(kt * BK * 2) * (uint32_t)ldb;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t dst = st + (uint32_t)((pw * 2 + i) * 1024);
+        if (kt >= KT) {
+          eas_dma16s(ra, 0x80000000u, 0u, lds_a + dst);
+          eas_dma16s(rb, 0x80000000u, 0u, lds_b + dst);
+        } else if (K % BK != 0 && kt == KT - 1) {
+          eas_dma16s(ra, a_tail[i], 0u, lds_a + dst);
+          eas_dma16s(rb, b_tail[i], 0u, lds_b + dst);
+        } else {
+          eas_dma16s(ra, a_off[i], sa, lds_a + dst);
+          if constexpr (decltype(b_fast)::value)
+            eas_dma16s(rb, b_off[i], sb, lds_b + dst);
+          else
+            eas_dma16s(rb, b_raw[i] + sb, 0u, lds_b + dst);
+        }
+      }
+    };
+    // one barrier per stage, as many as the consumers
+    auto produce = [&](auto b_fast) {
+#pragma unroll
+      for (int p = 0; p < NSTAGE - 1; ++p) dma(p, b_fast);
+      __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));  // stage 0 landed (stages 1 and 2 may be in flight)
+      __syncthreads();
+      for (int kt = 0; kt + 1 < KT; ++kt) {
+        __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));  // stage kt+1 landed (stage kt+2 may be in flight)
+        __syncthreads();
+        dma(kt + NSTAGE - 1, b_fast);  // the slot of stage kt-1, whose fragments every consumer has read
+      }
+      __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
+    };
+    if (n0 + BN <= N || N % 8 == 0)
+      produce(eas_bool_c<true>{});
+    else
+      produce(eas_bool_c<false>{});
+    return;
+  }
+  const int wm = wave >> 1, wn = wave & 1;
   int fa_off[2][2], fb_off[2][2][2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
@@ -685,48 +726,74 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
-  auto wait_stage = [&](int later) {  // `later` newer stages (4 loads each) may stay in flight
-    if (later >= 2) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));
-    else if (later == 1) __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));
-    else __builtin_amdgcn_s_waitcnt(EAS_WAITVM(0));
-  };
-#pragma unroll
-  for (int s = 0; s < NSTAGE - 1; ++s)
-    if (s < KT) dma_stage(s);
-  for (int kt = 0; kt < KT; ++kt) {
-    // this wave's loads of stage kt landed; the barrier makes every wave's visible and frees
-    // stage kt-1, which the DMA of stage kt+3 refills
-    wait_stage(KT - 1 - kt < NSTAGE - 2 ? KT - 1 - kt : NSTAGE - 2);
-    __syncthreads();
-    if (kt + NSTAGE - 1 < KT) dma_stage(kt + NSTAGE - 1);
+  typedef eas_h8 frag_t[2][2];  // [ks][i]
+  auto read_stage = [&](int kt, frag_t& fa, frag_t& fb) {
     const eas_op_t* as = As + (kt % NSTAGE) * STAGE_H;
     const eas_op_t* bs = Bs + (kt % NSTAGE) * STAGE_H;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      eas_h8 fa[2], fb[2];
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        fa[i] = *(const eas_h8*)(as + fa_off[ks][i]);
+        fa[ks][i] = *(const eas_h8*)(as + fa_off[ks][i]);
         const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][0]));
         const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][1]));
         const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
-        fb[i] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+        fb[ks][i] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
       }
-      if constexpr (K % 8 != 0) {
-        if (kt == KT - 1) {  // tail stage: halves at k >= K hold the next row of A
+  };
+  auto mfmas = [&](const frag_t& fa, const frag_t& fb) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const bool past = kt * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
-#pragma unroll
-            for (int i = 0; i < 2; ++i) fa[i][e] = past ? (eas_op_t)0.0f : fa[i][e];
-          }
-        }
-      }
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = EAS_MFMA32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) acc[i][j] = EAS_MFMA32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+  };
+  // At the barrier of stage kt the producers' DMA of stage kt+1 has landed; after it the wave
+  // issues stage kt's MFMAs from the fragments read one stage earlier and, between them, every
+  // fragment read of stage kt+1 into the other set.  After this barrier the producers refill the
+  // slot of stage kt-1, whose fragments every consumer read (and used) before it.
+  auto step = [&](int kt, const frag_t& fa, const frag_t& fb, frag_t& na, frag_t& nb) {
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    read_stage(kt + 1, na, nb);
+    mfmas(fa, fb);
+#pragma unroll
+    for (int s = 0; s < 6; ++s) {  // 12 LDS reads: two after each of the first 6 MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // the last stage of a K that is not a multiple of 8: halves at k >= K hold the next row of A
+  auto mask_tail = [&](frag_t& fa) {
+    if constexpr (K % 8 != 0) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool past = (KT - 1) * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
+#pragma unroll
+          for (int i = 0; i < 2; ++i) fa[ks][i][e] = past ? (eas_op_t)0.0f : fa[ks][i][e];
+        }
+    }
+  };
+  __syncthreads();  // stage 0 landed
+  frag_t a0, b0, a1, b1;
+  read_stage(0, a0, b0);
+  int kt = 0;
+  for (; kt + 2 < KT; kt += 2) {  // two stages per iteration: the fragment sets alternate
+    step(kt, a0, b0, a1, b1);
+    step(kt + 1, a1, b1, a0, b0);
+  }
+  if constexpr (KT % 2 == 0) {
+    step(KT - 2, a0, b0, a1, b1);
+    mask_tail(a1);
+    mfmas(a1, b1);
+  } else {
+    mask_tail(a0);
+    mfmas(a0, b0);
   }
   const bool full = (m0 + BM <= M) && (n0 + BN <= N);
   // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
@@ -1115,7 +1182,7 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__pp(
     eas_gemm_elementwise<AT, BT, CT, K>(A, B, C, ldb, M, N, m0, n0);
 }
 
-extern "C" __global__ __launch_bounds__(256) void @NAME@__t128(
+extern "C" __global__ __launch_bounds__(512) void @NAME@__t128(
     @PARAMS@) {
   constexpr int K = @K@;
   typedef @AT@ AT;
@@ -1520,6 +1587,7 @@ TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
 PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
+T128_THREADS = 512  # the 128 x 128 entry of f16 GEMMs: 4 consumer + 4 producer waves
 F32_THREADS = 512  # both fp32 entries: 4 consumer + 4 producer waves
 SKINNY_M = 128  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
@@ -1588,6 +1656,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "col_masked": spec.col_masked,
         "pp_entry": f"{ir.name}__pp" if pingpong else None, "pp_threads": PP_THREADS,
         "t128_entry": f"{ir.name}__t128" if (pingpong or spec.f32) else None, "f32": spec.f32,
+        "t128_threads": F32_THREADS if spec.f32 else T128_THREADS,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value,
         "op_dtype": "f32" if spec.f32 else spec.op_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

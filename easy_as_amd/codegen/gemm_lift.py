@@ -1044,7 +1044,7 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
         other = None
         if m > SKINNY_CUT and p.get("pp_entry") and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
             if choice == "tile128" or (choice == "auto" and groups > compute_units):
-                other = LaunchPlan((tiles128, 1, 1), (p["threads"], 1, 1), hidden, entry=p["t128_entry"])
+                other = LaunchPlan((tiles128, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128_entry"])
             elif choice == "8wave":
                 other = LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
         return other or LaunchPlan((groups, 1, 1), (p["threads"], 1, 1), hidden)
@@ -1052,12 +1052,12 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
         # fp32: 128 x 128 tiles (a quarter of the DMA bytes per flop) while they still give every CU one
         if p.get("t128_entry") and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n, elem=4) and (
                 choice == "tile128" or (choice == "auto" and tiles128 >= compute_units)):
-            return LaunchPlan((tiles128, 1, 1), (p["threads"], 1, 1), hidden, entry=p["t128_entry"])
+            return LaunchPlan((tiles128, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128_entry"])
         return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
     if p.get("pp_entry") and choice != "4wave" and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
         # 128 x 128 tiles when 256 x 256 ones would fill at most half of the CUs
         if choice == "tile128" or (choice == "auto" and 2 * tiles <= compute_units):
-            return LaunchPlan((tiles128, 1, 1), (p["threads"], 1, 1), hidden, entry=p["t128_entry"])
+            return LaunchPlan((tiles128, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128_entry"])
         return LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
     return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
 

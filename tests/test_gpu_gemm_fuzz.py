@@ -5,7 +5,9 @@ or f16 output, the bf16 variant, the fp32 threadgroup-tile kernel) and M, N, K f
 log scale, so the cases cover:
 * skinny and full-tile launches;
 * odd K (A rows not 4-byte aligned) and K below one stage;
-* N not a multiple of 4, and every entry the launch plan picks by itself.
+* N not a multiple of 4, and every entry the launch plan picks by itself;
+* each shape again on the 128 x 128-tile entry (``EAS_HIP_GEMM_ENTRY=tile128``), which the
+  plan picks by itself only for launches of more than 128 rows.
 
 Every output is checked with the tolerances the parity bars state.  The output buffer is
 longer than M x N, and its tail must keep its sentinel (no write past C)."""
@@ -57,40 +59,44 @@ def test_random_shape_matches_float64(gpu_runtime, monkeypatch, seed):
         bm, bn, bk, nt = (32, 32, 32, 256) if seed % 8 < 4 else (16, 64, 16, 256)
         ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
         bar = 1e-5 * math.sqrt(k)
-        # the 128 x 128-tile entry too (its edge tiles, K tail and zero-filled stages)
-        for choice in ("tile128", "auto"):
-            monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
+
+        def run():
             c = np.full(m * n + PAD, np.nan, np.float32)
             K.matmul_tiled_kernel(a, b, c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
                                   _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
-            got, tail = c[:m * n], c[m * n:]
-            if choice == "tile128":
-                assert np.isnan(tail).all() and np.isfinite(got).all(), f"tile128 M={m} N={n} K={k}"
-                err = ops.rel_err(np.asarray(got, np.float64).reshape(m, n), ref)
-                assert err <= bar, f"tile128 M={m} N={n} K={k}: rel err {err:.3e} > {bar:.3e}"
+            return c
     elif kind == "bf16_f32":
         a_bits = ops.f32_to_bf16(rng.uniform(-1, 1, m * k).astype(np.float32))
         b_bits = ops.f32_to_bf16(rng.uniform(-1, 1, k * n).astype(np.float32))
         ta = torch.from_numpy(a_bits.view(np.int16)).view(torch.bfloat16)
         tb = torch.from_numpy(b_bits.view(np.int16)).view(torch.bfloat16)
-        tc = torch.full((m * n + PAD,), float("nan"), dtype=torch.float32)
-        K.matmul_mma_bf16_kernel(ta, tb, tc, m, n, BM=32, BN=32, BK=8, K=k, NT=512, OUT16=False,
-                                 _grid=K.mma_grid, _tptg=(512, 1, 1))
         ref = ops.matmul_ref(ops.bf16_to_f32(a_bits).reshape(m, k), ops.bf16_to_f32(b_bits).reshape(k, n))
-        c = tc.numpy()
-        got, tail = c[:m * n], c[m * n:]
         bar = 1e-5 * math.sqrt(k)
+
+        def run():
+            tc = torch.full((m * n + PAD,), float("nan"), dtype=torch.float32)
+            K.matmul_mma_bf16_kernel(ta, tb, tc, m, n, BM=32, BN=32, BK=8, K=k, NT=512, OUT16=False,
+                                     _grid=K.mma_grid, _tptg=(512, 1, 1))
+            return tc.numpy()
     else:
         a = rng.uniform(-1, 1, m * k).astype(np.float16)
         b = rng.uniform(-1, 1, k * n).astype(np.float16)
         out16 = kind == "f16_f16"
-        c = np.full(m * n + PAD, np.nan, np.float16 if out16 else np.float32)
         kern = K.matmul_mma_f16out_kernel if out16 else K.matmul_mma_kernel
-        kern(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512, _grid=K.mma_grid, _tptg=(512, 1, 1))
         ref = ops.matmul_ref(a.reshape(m, k).astype(np.float32), b.reshape(k, n).astype(np.float32))
-        got, tail = c[:m * n], c[m * n:]
         bar = 2e-3 if out16 else 1e-5 * math.sqrt(k)
-    assert np.isnan(tail).all(), f"{kind} M={m} N={n} K={k}: wrote past C"
-    assert np.isfinite(got).all(), f"{kind} M={m} N={n} K={k}: an output was not written"
-    err = ops.rel_err(np.asarray(got, np.float64).reshape(m, n), ref)
-    assert err <= min(2e-2, bar), f"{kind} M={m} N={n} K={k}: rel err {err:.3e} > {bar:.3e}"
+
+        def run():
+            c = np.full(m * n + PAD, np.nan, np.float16 if out16 else np.float32)
+            kern(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512, _grid=K.mma_grid, _tptg=(512, 1, 1))
+            return c
+    # the entry the launch plan picks, and the 128 x 128-tile entry on every shape (its edge
+    # tiles, K tail and zero-filled stages)
+    for choice in ("auto", "tile128"):
+        monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
+        c = run()
+        got, tail = c[:m * n], c[m * n:]
+        assert np.isnan(tail).all(), f"{kind} {choice} M={m} N={n} K={k}: wrote past C"
+        assert np.isfinite(got).all(), f"{kind} {choice} M={m} N={n} K={k}: an output was not written"
+        err = ops.rel_err(np.asarray(got, np.float64).reshape(m, n), ref)
+        assert err <= min(2e-2, bar), f"{kind} {choice} M={m} N={n} K={k}: rel err {err:.3e} > {bar:.3e}"

@@ -227,7 +227,7 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(17, 10, 1))
     # 6 tiles of 256 x 256 would leave CUs idle: 3 x 5 tiles of 128 x 128 on the 128-tile entry
     assert plan.hidden == (0, 300, 0, 520) and plan.grid == (3 * 5, 1, 1)
-    assert plan.block == (256, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
+    assert plan.block == (512, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(3, 2, 1))  # partial grid: 64 x 96 rectangle
     assert plan.hidden == (0, 64, 0, 96) and plan.grid == (2, 1, 1)  # 64 rows: skinny, 64 columns per workgroup
     # M <= 128 (decode-like): one workgroup per 64 columns, on the 4-wave entry
@@ -237,7 +237,7 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
         assert plan.block == (256, 1, 1) and plan.entry is None
     # 17-128 rows with more column groups than CUs: 128 x 128 tiles instead of two skinny rounds
     plan = plan_launch(ck, {"M": 128, "N": 28672}, grid=(896, 4, 1))
-    assert plan.grid == (224, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
+    assert plan.grid == (224, 1, 1) and plan.entry == "matmul_mma_kernel__t128" and plan.block == (512, 1, 1)
     plan = plan_launch(ck, {"M": 16, "N": 28672}, grid=(896, 1, 1))
     assert plan.grid == (448, 1, 1) and plan.entry is None
     plan = plan_launch(ck, {"M": 129, "N": 14336}, grid=(448, 5, 1))
@@ -255,7 +255,7 @@ def test_plan_tile_size_follows_the_cu_count(mn, entry, grid):
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, m, n, BM=32, BN=32, BK=8, K=64, NT=512)
     plan = plan_launch(ck, {"M": m, "N": n}, grid=(n // 32, m // 32, 1))
     assert plan.entry == "matmul_mma_kernel" + entry and plan.grid == (grid, 1, 1)
-    assert plan.block == ((512 if entry == "__pp" else 256), 1, 1)
+    assert plan.block == (512, 1, 1)
 
 
 def test_plan_fp32_tile_size(monkeypatch):
