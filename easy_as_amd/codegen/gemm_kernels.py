@@ -12,9 +12,10 @@ entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
   four waves alternate load phases and MFMA phases one barrier apart, each
   wave holding 128 x 64 of the tile (8 x 4 ``v_mfma_f32_16x16x32_f16``
   accumulators; ``EAS_HIP_GEMM_MFMA=32`` selects 4 x 2 of ``32x32x16``).
-* ``<name>__t128`` (512 threads): the same DMA operands on 128 x 128 tiles, for
-  launches whose 256 x 256 grid would leave CUs idle: 4 waves issue the DMA, 4
-  waves of 64 x 64 read fragments and run the MFMAs.
+* ``<name>__t128`` and ``<name>__t128x256`` (512 threads): the same DMA operands
+  on 128 x 128 and 128 x 256 tiles, for launches whose 256 x 256 grid would leave
+  CUs idle: 4 waves issue the DMA, 4 waves of 64 x 64 (64 x 128) read fragments
+  and run the MFMAs.
 * ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
   AGPRs): the skinny path (launches of at most 128 rows), the 4-wave DMA body,
   and the register body; a uniform branch picks one per launch.
@@ -599,14 +600,14 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
   }
 }
 
-// Guard body of the 8-wave and 128-tile entries for inputs the DMA cannot take (the launch plan
+// Guard body of the 8-wave and 128-row entries for inputs the DMA cannot take (the launch plan
 // sends those to the 4-wave entry; this path only keeps a mistaken plan correct): one f32 dot
-// product per element of the T x T tile.
-template <typename AT, typename BT, typename CT, int K, int T = 256>
+// product per element of the TM x TN tile.
+template <typename AT, typename BT, typename CT, int K, int TM = 256, int TN = TM>
 static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict__ A, const BT* __restrict__ B,
                                                             CT* __restrict__ C, int ldb, int M, int N, int m0, int n0) {
-  for (int e = threadIdx.x; e < T * T; e += blockDim.x) {
-    const int row = m0 + e / T, col = n0 + e % T;
+  for (int e = threadIdx.x; e < TM * TN; e += blockDim.x) {
+    const int row = m0 + e / TN, col = n0 + e % TN;
     if (row >= M || col >= N) continue;
     float acc = 0.0f;
     for (int k = 0; k < K; ++k)
@@ -615,39 +616,44 @@ static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict
   }
 }
 
-// 128 x 128 tile body for launches whose 256 x 256 grid would leave CUs idle: 8 waves (512
-// threads), specialised like the fp32 entries, on a ring of 4 stages of 16 KB (64 KB of LDS).
-// Waves 4-7 produce: the DMA of stage kt+3, 2 A + 2 B loads of 1 KB per wave per stage, with the
-// stage offset in soffset, so the loads cost the MFMA waves sharing their SIMDs nothing.  Waves
-// 0-3 consume, 64 x 64 each (2 x 2 accumulators of 32x32x16): the fragments of stage kt+1 are
-// read between stage kt's 8 MFMAs.  A load costs the SIMD that issues it tens of clocks of MFMA
-// issue, which in the 4-wave form of this body (each wave loading its quarter of every stage
-// beside 8 MFMAs) was most of the stage.
-template <typename CT, int K>
+// 128 x BN tile body (BN = 128 or 256) for launches whose 256 x 256 grid would leave CUs idle:
+// 8 waves (512 threads), specialised like the fp32 entries, on a ring of 4 stages of 8 KB of A
+// and BN / 16 KB of B.  Waves 4-7 produce: the DMA of stage kt+3, 2 A + BN / 64 B loads of 1 KB
+// per wave per stage, with the stage offset in soffset, so the loads cost the MFMA waves sharing
+// their SIMDs nothing.  Waves 0-3 consume, 64 x BN/2 each (2 x BN/64 accumulators of 32x32x16):
+// the fragments of stage kt+1 are read between stage kt's MFMAs.  A load costs the SIMD that
+// issues it tens of clocks of MFMA issue, which in a 4-wave form of this body (each wave loading
+// its quarter of every stage beside 8 MFMAs) was most of the stage.
+template <typename CT, int K, int BN>
 static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
                                                      eas_op_t* smem) {
-  constexpr int BM = 128, BN = 128, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
-  constexpr int STAGE_H = BM * BK;          // halves per operand per stage (8 KB)
+  static_assert(BN == 128 || BN == 256, "128 x 128 and 128 x 256 tiles");
+  constexpr int BM = 128, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
+  constexpr int NJ = BN / 64;               // 32-column accumulators per consumer wave
+  constexpr int NBI = BN / 64;              // B loads per producer wave per stage
+  constexpr int CH = BN / 8;                // 16-byte chunks per B row
+  constexpr int STAGE_A = BM * BK, STAGE_B = BK * BN;  // halves per stage
   constexpr int KLAST = K - (KT - 1) * BK;  // k extent of the last stage
   eas_op_t* As = smem;
-  eas_op_t* Bs = smem + NSTAGE * STAGE_H;
+  eas_op_t* Bs = smem + NSTAGE * STAGE_A;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   if (wave >= 4) {
-    // DMA instruction q = 2 pw + i writes 1 KB of a stage.  A: rows 16q + lane/4, chunk lane%4
-    // stored at chunk ^ ((row/4)%4).  B: rows (k) 4q + lane/16, chunk lane%16 stored at chunk ^ 4(row%4).
+    // DMA instructions write 1 KB of a stage each.  A instruction q = 2 pw + i: rows 16q + lane/4,
+    // chunk lane%4 stored at chunk ^ ((row/4)%4).  B instruction q = NBI pw + i: rows
+    // (64 / CH) q + lane / CH, chunk lane % CH stored at chunk ^ 4(row%4).
     // Rows past M load zeros, and so do columns past N when no 8-column chunk straddles N, so
     // every address a load reads, lane offset plus stage offset, lies inside A or B.  An edge tile
     // whose chunk straddles N (N % 8 != 0) adds the stage offset to the lane offset instead, where
     // the range check sees all of it.  The last stage of a K that is not a multiple of BK does the
     // same (its straddling A chunk may end past A); stages past K load zeros into a slot nobody
-    // reads, so every stage issues 4 loads and the count at each barrier is the same.
+    // reads, so every stage issues the same loads and the count at each barrier is the same.
     const int pw = wave - 4;
     const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
     const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
     const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS eas_op_t*)As, lds_b = (uint32_t)(size_t)(EAS_LDS eas_op_t*)Bs;
-    uint32_t a_off[2], a_tail[2], b_raw[2], b_off[2], b_tail[2];
+    uint32_t a_off[2], a_tail[2], b_raw[NBI], b_off[NBI], b_tail[NBI];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int q = pw * 2 + i;
@@ -656,41 +662,52 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
       const uint32_t a_raw = ((uint32_t)(m0 + r_a) * (uint32_t)K + (uint32_t)(c_a * 8)) * 2u;
       a_off[i] = m0 + r_a < M ? a_raw : 0x80000000u;
       a_tail[i] = (m0 + r_a < M && c_a * 8 < KLAST) ? a_raw + (uint32_t)((KT - 1) * BK * 2) : 0x80000000u;
-      const int r_b = 4 * q + (lane >> 4);
-      const int c_b = (lane & 15) ^ (4 * (r_b & 3));
+    }
+#pragma unroll
+    for (int i = 0; i < NBI; ++i) {
+      const int q = pw * NBI + i;
+      const int r_b = (64 / CH) * q + lane / CH;
+      const int c_b = (lane % CH) ^ (4 * (r_b & 3));
       b_raw[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
       b_off[i] = n0 + c_b * 8 < N ? b_raw[i] : 0x80000000u;
       b_tail[i] = r_b < KLAST ? b_raw[i] + (uint32_t)((KT - 1) * BK * 2) * (uint32_t)ldb : 0x80000000u;
     }
     auto dma = [&](int kt, auto b_fast) {
-      const uint32_t st = (uint32_t)((kt % NSTAGE) * STAGE_H * 2);
+      const uint32_t st_a = lds_a + (uint32_t)((kt % NSTAGE) * STAGE_A * 2);
+      const uint32_t st_b = lds_b + (uint32_t)((kt % NSTAGE) * STAGE_B * 2);
       const uint32_t sa = (uint32_t)(kt * BK * 2), sb = (uint32_t)(kt * BK * 2) * (uint32_t)ldb;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const uint32_t dst = st + (uint32_t)((pw * 2 + i) * 1024);
-        if (kt >= KT) {
-          eas_dma16s(ra, 0x80000000u, 0u, lds_a + dst);
-          eas_dma16s(rb, 0x80000000u, 0u, lds_b + dst);
-        } else if (K % BK != 0 && kt == KT - 1) {
-          eas_dma16s(ra, a_tail[i], 0u, lds_a + dst);
-          eas_dma16s(rb, b_tail[i], 0u, lds_b + dst);
-        } else {
-          eas_dma16s(ra, a_off[i], sa, lds_a + dst);
-          if constexpr (decltype(b_fast)::value)
-            eas_dma16s(rb, b_off[i], sb, lds_b + dst);
-          else
-            eas_dma16s(rb, b_raw[i] + sb, 0u, lds_b + dst);
-        }
+        const uint32_t dst = st_a + (uint32_t)((pw * 2 + i) * 1024);
+        if (kt >= KT)
+          eas_dma16s(ra, 0x80000000u, 0u, dst);
+        else if (K % BK != 0 && kt == KT - 1)
+          eas_dma16s(ra, a_tail[i], 0u, dst);
+        else
+          eas_dma16s(ra, a_off[i], sa, dst);
+      }
+#pragma unroll
+      for (int i = 0; i < NBI; ++i) {
+        const uint32_t dst = st_b + (uint32_t)((pw * NBI + i) * 1024);
+        if (kt >= KT)
+          eas_dma16s(rb, 0x80000000u, 0u, dst);
+        else if (K % BK != 0 && kt == KT - 1)
+          eas_dma16s(rb, b_tail[i], 0u, dst);
+        else if constexpr (decltype(b_fast)::value)
+          eas_dma16s(rb, b_off[i], sb, dst);
+        else
+          eas_dma16s(rb, b_raw[i] + sb, 0u, dst);
       }
     };
     // one barrier per stage, as many as the consumers
     auto produce = [&](auto b_fast) {
+      constexpr int PER = 2 + NBI;  // loads per stage
 #pragma unroll
       for (int p = 0; p < NSTAGE - 1; ++p) dma(p, b_fast);
-      __builtin_amdgcn_s_waitcnt(EAS_WAITVM(8));  // stage 0 landed (stages 1 and 2 may be in flight)
+      __builtin_amdgcn_s_waitcnt(EAS_WAITVM(2 * PER));  // stage 0 landed (stages 1 and 2 may be in flight)
       __syncthreads();
       for (int kt = 0; kt + 1 < KT; ++kt) {
-        __builtin_amdgcn_s_waitcnt(EAS_WAITVM(4));  // stage kt+1 landed (stage kt+2 may be in flight)
+        __builtin_amdgcn_s_waitcnt(EAS_WAITVM(PER));  // stage kt+1 landed (stage kt+2 may be in flight)
         __syncthreads();
         dma(kt + NSTAGE - 1, b_fast);  // the slot of stage kt-1, whose fragments every consumer has read
       }
@@ -703,71 +720,78 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
     return;
   }
   const int wm = wave >> 1, wn = wave & 1;
-  int fa_off[2][2], fb_off[2][2][2];
+  int fa_off[2][2], fb_off[2][NJ][2];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
+  for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = wm * 64 + i * 32 + (lane & 31);
       const int c = (2 * ks + (lane >> 5)) ^ ((r >> 2) & 3);
       fa_off[ks][i] = r * BK + c * 8;
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         // ds_read_b64_tr_b16: in each 16-lane group, source lane kq addresses row kq/4, columns 4(kq%4)..+3
         const int gq = lane >> 4, kq = lane & 15;
         const int row = 16 * ks + 8 * (gq >> 1) + 4 * h + (kq >> 2);
-        const int col = wn * 64 + i * 32 + 16 * (gq & 1) + 4 * (kq & 3);
+        const int col = wn * (BN / 2) + j * 32 + 16 * (gq & 1) + 4 * (kq & 3);
         const int chunk = (col >> 3) ^ (4 * (row & 3));
-        fb_off[ks][i][h] = row * BN + chunk * 8 + (col & 7);
+        fb_off[ks][j][h] = row * BN + chunk * 8 + (col & 7);
       }
-    }
-  eas_f32x16 acc[2][2];
+  }
+  eas_f32x16 acc[2][NJ];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = (eas_f32x16){};
-  typedef eas_h8 frag_t[2][2];  // [ks][i]
-  auto read_stage = [&](int kt, frag_t& fa, frag_t& fb) {
-    const eas_op_t* as = As + (kt % NSTAGE) * STAGE_H;
-    const eas_op_t* bs = Bs + (kt % NSTAGE) * STAGE_H;
+    for (int j = 0; j < NJ; ++j) acc[i][j] = (eas_f32x16){};
+  typedef eas_h8 afrag_t[2][2];   // [ks][i]
+  typedef eas_h8 bfrag_t[2][NJ];  // [ks][j]
+  auto read_stage = [&](int kt, afrag_t& fa, bfrag_t& fb) {
+    const eas_op_t* as = As + (kt % NSTAGE) * STAGE_A;
+    const eas_op_t* bs = Bs + (kt % NSTAGE) * STAGE_B;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        fa[ks][i] = *(const eas_h8*)(as + fa_off[ks][i]);
-        const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][0]));
-        const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][i][1]));
+      for (int i = 0; i < 2; ++i) fa[ks][i] = *(const eas_h8*)(as + fa_off[ks][i]);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
+        const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
         const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
-        fb[ks][i] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
+        fb[ks][j] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
       }
+    }
   };
-  auto mfmas = [&](const frag_t& fa, const frag_t& fb) {
+  auto mfmas = [&](const afrag_t& fa, const bfrag_t& fb) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = EAS_MFMA32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < NJ; ++j) acc[i][j] = EAS_MFMA32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
   };
   // At the barrier of stage kt the producers' DMA of stage kt+1 has landed; after it the wave
   // issues stage kt's MFMAs from the fragments read one stage earlier and, between them, every
   // fragment read of stage kt+1 into the other set.  After this barrier the producers refill the
   // slot of stage kt-1, whose fragments every consumer read (and used) before it.
-  auto step = [&](int kt, const frag_t& fa, const frag_t& fb, frag_t& na, frag_t& nb) {
+  auto step = [&](int kt, const afrag_t& fa, const bfrag_t& fb, afrag_t& na, bfrag_t& nb) {
+    constexpr int NMFMA = 4 * NJ, NREAD = 4 + 4 * NJ;
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     read_stage(kt + 1, na, nb);
     mfmas(fa, fb);
 #pragma unroll
-    for (int s = 0; s < 6; ++s) {  // 12 LDS reads: two after each of the first 6 MFMAs
+    for (int s = 0; s < NREAD / 2; ++s) {  // the LDS reads two by two after the first MFMAs
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA - NREAD / 2, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
   // the last stage of a K that is not a multiple of 8: halves at k >= K hold the next row of A
-  auto mask_tail = [&](frag_t& fa) {
+  auto mask_tail = [&](afrag_t& fa) {
     if constexpr (K % 8 != 0) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
@@ -780,7 +804,8 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
     }
   };
   __syncthreads();  // stage 0 landed
-  frag_t a0, b0, a1, b1;
+  afrag_t a0, a1;
+  bfrag_t b0, b1;
   read_stage(0, a0, b0);
   int kt = 0;
   for (; kt + 2 < KT; kt += 2) {  // two stages per iteration: the fragment sets alternate
@@ -800,11 +825,11 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm * 64 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
-        const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+        const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
         if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
       }
 }
@@ -1200,9 +1225,32 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__t128(
   int m0, n0;
   eas_tile_origin<128, 128>(M, N, m0, n0);
   if (dma_ok)
-    eas_gemm_t128<CT, K>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
+    eas_gemm_t128<CT, K, 128>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
   else
     eas_gemm_elementwise<AT, BT, CT, K, 128>(A, B, C, ldb, M, N, m0, n0);
+}
+
+extern "C" __global__ __launch_bounds__(512) void @NAME@__t128x256(
+    @PARAMS@) {
+  constexpr int K = @K@;
+  typedef @AT@ AT;
+  typedef @BT@ BT;
+  typedef @CT@ CT;
+  const int ldb = (int)@LDB@;
+  // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
+  const AT* __restrict__ A = @A@ + (size_t)__eas_m_lo * K;
+  const BT* __restrict__ B = @B@ + __eas_n_lo;
+  CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
+  const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
+  __shared__ __attribute__((aligned(1024))) eas_op_t smem[4 * (128 * 32 + 32 * 256)];  // DMA ring 4 x (8 + 16) KB
+  const bool dma_ok = (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
+                      ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
+  int m0, n0;
+  eas_tile_origin<128, 256>(M, N, m0, n0);
+  if (dma_ok)
+    eas_gemm_t128<CT, K, 256>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
+  else
+    eas_gemm_elementwise<AT, BT, CT, K, 128, 256>(A, B, C, ldb, M, N, m0, n0);
 }
 """
 
@@ -1587,7 +1635,7 @@ TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
 PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
-T128_THREADS = 512  # the 128 x 128 entry of f16 GEMMs: 4 consumer + 4 producer waves
+T128_THREADS = 512  # the 128 x 128 and 128 x 256 entries of f16 GEMMs: 4 consumer + 4 producer waves
 F32_THREADS = 512  # both fp32 entries: 4 consumer + 4 producer waves
 SKINNY_M = 128  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
@@ -1657,6 +1705,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "pp_entry": f"{ir.name}__pp" if pingpong else None, "pp_threads": PP_THREADS,
         "t128_entry": f"{ir.name}__t128" if (pingpong or spec.f32) else None, "f32": spec.f32,
         "t128_threads": F32_THREADS if spec.f32 else T128_THREADS,
+        "t128x256_entry": f"{ir.name}__t128x256" if pingpong else None,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value,
         "op_dtype": "f32" if spec.f32 else spec.op_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

@@ -1034,6 +1034,7 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
     m, n = m_hi - m_lo, n_hi - n_lo
     tiles = -(-m // p["BM"]) * -(-n // p["BN"])
     tiles128 = -(-m // 128) * -(-n // 128)
+    tiles128x256 = -(-m // 128) * -(-n // 256)
     choice = _gemm_entry_choice()
     if m <= p.get("skinny_m", 0):
         # The 4-wave entry runs its skinny path for every launch of at most skinny_m rows (one
@@ -1045,6 +1046,9 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
         if m > SKINNY_CUT and p.get("pp_entry") and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
             if choice == "tile128" or (choice == "auto" and groups > compute_units):
                 other = LaunchPlan((tiles128, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128_entry"])
+            elif choice == "tile128x256":
+                other = LaunchPlan((tiles128x256, 1, 1), (p["t128_threads"], 1, 1), hidden,
+                                   entry=p["t128x256_entry"])
             elif choice == "8wave":
                 other = LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
         return other or LaunchPlan((groups, 1, 1), (p["threads"], 1, 1), hidden)
@@ -1055,20 +1059,24 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
             return LaunchPlan((tiles128, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128_entry"])
         return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
     if p.get("pp_entry") and choice != "4wave" and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
-        # 128 x 128 tiles when 256 x 256 ones would fill at most half of the CUs
-        if choice == "tile128" or (choice == "auto" and 2 * tiles <= compute_units):
+        # When 256 x 256 tiles would fill at most half of the CUs: 128 x 128 tiles if they take one
+        # round of CUs, else 128 x 256 ones (at most twice the 256 x 256 count, so one round too)
+        small = choice == "auto" and 2 * tiles <= compute_units
+        if choice == "tile128x256" or (small and tiles128 > compute_units):
+            return LaunchPlan((tiles128x256, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128x256_entry"])
+        if choice == "tile128" or small:
             return LaunchPlan((tiles128, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128_entry"])
         return LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
     return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
 
 
-_ENTRY_CHOICES = ("auto", "8wave", "tile128", "4wave")
+_ENTRY_CHOICES = ("auto", "8wave", "tile128", "tile128x256", "4wave")
 SKINNY_CUT = 16  # up to this many rows a launch always takes the skinny path
 
 
 def _gemm_entry_choice() -> str:
     """``EAS_HIP_GEMM_ENTRY``: ``auto`` (default), or one entry for every f16 launch
-    the DMA takes: ``8wave``, ``tile128`` or ``4wave``."""
+    the DMA takes: ``8wave``, ``tile128``, ``tile128x256`` or ``4wave``."""
     v = os.environ.get("EAS_HIP_GEMM_ENTRY", "auto").strip().lower() or "auto"
     if v not in _ENTRY_CHOICES:
         raise ValueError(f"EAS_HIP_GEMM_ENTRY must be one of {_ENTRY_CHOICES}, got {v!r}")

@@ -203,9 +203,9 @@ def test_full_size_4096_sampled_rows(gpu_runtime, k):
 @pytest.mark.parametrize("mnk", [(300, 520, 200), (257, 264, 72), (520, 256, 1000), (136, 128, 36), (129, 300, 8),
                                  (130, 260, 4100), (100, 20000, 72)])
 def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
-    """The 8-wave (ping-pong), 128-tile and 4-wave entries on the same launch: each within
-    tolerance of float64 (edge tiles, K tails of 8 and of 4, one stage, 129 rows: just above the
-    skinny path)."""
+    """The 8-wave (ping-pong), 128 x 128, 128 x 256 and 4-wave entries on the same launch: each
+    within tolerance of float64 (edge tiles, K tails of 8 and of 4, one stage, 129 rows: just above
+    the skinny path)."""
     from easy_as_amd.runtime.hip import plan_launch
 
     m, n, k = mnk
@@ -213,7 +213,8 @@ def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
     ck = K.matmul_mma_kernel.compile(a, b, np.zeros(1, np.float32), m, n, BM=32, BN=32, BK=8, K=k, NT=512)
     args = {"a": a, "b": b, "c": np.zeros(m * n, np.float32), "M": m, "N": n}
     outs = {}
-    for choice, entry in (("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128"), ("4wave", None)):
+    for choice, entry in (("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128"),
+                          ("tile128x256", "matmul_mma_kernel__t128x256"), ("4wave", None)):
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
         assert plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args)).entry == entry
         c = np.full(m * n, np.nan, np.float32)
@@ -223,8 +224,8 @@ def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
     # the same MFMA sequence per output element: equal up to f32 rounding (at most 128 rows the
     # 4-wave entry runs the skinny path, whose waves split K: another summation order)
     tol = 1e-6 if m > 128 else 1e-5 * math.sqrt(k)
-    assert ops.rel_err(outs["8wave"], outs["4wave"]) <= tol
-    assert ops.rel_err(outs["tile128"], outs["4wave"]) <= tol
+    for choice in ("8wave", "tile128", "tile128x256"):
+        assert ops.rel_err(outs[choice], outs["4wave"]) <= tol, choice
     if m <= 128 and -(-n // 64) > 256:  # more column groups than CUs: the 128-tile entry by default
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "auto")
         assert plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args)).entry == "matmul_mma_kernel__t128"
@@ -266,7 +267,8 @@ def test_8wave_entry_with_32x32x16_mfma(gpu_runtime, monkeypatch, mnk, dtype):
     assert ops.rel_err(outs["32"].reshape(m, n).astype(np.float64), outs["16"].reshape(m, n).astype(np.float64)) <= 1e-6
 
 
-@pytest.mark.parametrize("choice,entry", [("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128")])
+@pytest.mark.parametrize("choice,entry", [("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128"),
+                                          ("tile128x256", "matmul_mma_kernel__t128x256")])
 def test_dma_entry_guard_for_an_operand_it_cannot_see(gpu_runtime, monkeypatch, choice, entry):
     """An eas.Tensor viewing torch memory at a 2-byte offset: the plan cannot see the address,
     picks a DMA entry, and the entry's own check sends the launch to its element-wise guard.

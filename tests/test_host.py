@@ -246,10 +246,12 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
 
 
 @pytest.mark.parametrize("mn,entry,grid", [((4096, 4096), "__pp", 256), ((3072, 3072), "__pp", 144),
-                                           ((2560, 2560), "__t128", 400), ((2048, 2048), "__t128", 256),
+                                           ((2560, 2560), "__t128x256", 200), ((2048, 2048), "__t128", 256),
+                                           ((512, 14336), "__t128x256", 224), ((256, 14336), "__t128", 224),
                                            ((8192, 8192), "__pp", 1024)])
 def test_plan_tile_size_follows_the_cu_count(mn, entry, grid):
-    # 256 x 256 tiles unless they would fill at most half of the 256 CUs
+    # 256 x 256 tiles unless they would fill at most half of the 256 CUs; then 128 x 128 tiles if
+    # they take one round of CUs, else 128 x 256
     m, n = mn
     f16, f32 = np.zeros(1, np.float16), np.zeros(1, np.float32)
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, m, n, BM=32, BN=32, BK=8, K=64, NT=512)
