@@ -834,36 +834,43 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
       }
 }
 
-// Skinny path (M <= 128, decode-like): one workgroup per 64 columns, the four waves split K.
-// Each wave streams its K range of B (and A) HBM -> LDS into a private 4-stage ring (3 stages for
-// 8 row tiles; no barriers in the loop), multiplies MT row tiles of 16 (1, 2, 4 or 8) by four
-// column tiles with v_mfma_f32_16x16x32_f16 (B transposed by ds_read_b64_tr_b16), and the waves
-// add their 16 MT x 64 partial sums through LDS at the end.
-template <typename CT, int K, int MT>
+// Skinny path (M <= 128, decode-like): one workgroup per NT = 64 columns (128 for launches of at
+// most 16 rows whose 64-column groups would need more than one round of CUs), the four waves
+// split K.  Each wave streams its K range of B (and A) HBM -> LDS into a private 4-stage ring (3
+// stages where 4 would not fit the LDS; no barriers in the loop), multiplies MT row tiles of 16
+// (1, 2, 4 or 8) by NT / 16 column tiles with v_mfma_f32_16x16x32_f16 (B transposed by
+// ds_read_b64_tr_b16), and the waves add their 16 MT x NT partial sums through LDS at the end.
+template <typename CT, int K, int MT, int NT = 64>
 static __device__ __forceinline__ void eas_gemm_skinny_dma(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
-                                                           CT* __restrict__ C, int ldb, int M, int N, eas_op_t* smem) {
+                                                           CT* __restrict__ C, int ldb, int M, int N, int n0,
+                                                           eas_op_t* smem) {
+  static_assert(NT == 64 || NT == 128, "64 or 128 columns per workgroup");
   typedef float eas_f32x4_acc __attribute__((ext_vector_type(4)));
-  constexpr int NT = 64, KS = 32, NST = MT > 4 ? 3 : 4, MR = 16 * MT;  // 8 row tiles: 3 stages fit the LDS
+  constexpr int KS = 32, MR = 16 * MT, NJ = NT / 16;
   constexpr int KW = ((K + 4 * KS - 1) / (4 * KS)) * KS;  // k rows per wave
-  constexpr int BST = KS * NT, AST = MR * KS, STH = BST + AST;  // halves per stage: B [32][64], A [MR][32]
-  constexpr int LOADS = 4 + MT;                                   // DMA instructions per stage
+  constexpr int BST = KS * NT, AST = MR * KS, STH = BST + AST;  // halves per stage: B [32][NT], A [MR][32]
+  constexpr int NST = 4 * 4 * STH * 2 <= 147456 ? 4 : 3;        // stages per wave ring (144 KB of LDS)
+  static_assert(4 * NST * STH * 2 <= 147456, "the rings fit the entry's LDS");
+  constexpr int NBQ = NT / 16, CH = NT / 8;                     // B DMA instructions per stage, chunks per row
+  constexpr int LOADS = NBQ + MT;                               // DMA instructions per stage
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n0 = blockIdx.x * NT;
   const int kb = wave * KW, ke = min(K, kb + KW);
   const int nsteps = ke > kb ? (ke - kb + KS - 1) / KS : 0;
   eas_op_t* ws = smem + wave * NST * STH;
   const uint32_t lds_ws = (uint32_t)(size_t)(EAS_LDS eas_op_t*)ws;
   const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
   const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
-  // B DMA q: rows 8q + lane/8 of the stage, chunk lane%8 stored at chunk ^ s(row),
-  // s(r) = 2((r/2)%2) + 4((r/8)%2) keeps each 16-lane transposed read conflict free
-  uint32_t b_off[4];
-  int b_row[4];
+  // B DMA q: rows (64 / CH) q + lane / CH of the stage, chunk lane % CH stored at chunk ^ s(row).
+  // 128-byte rows (NT 64): s(r) = 2((r/2)%2) + 4((r/8)%2); 256-byte rows (NT 128): s(r) =
+  // 2(r%4) + 8((r/8)%2).  Either keeps each half-wave of a transposed read conflict free.
+  auto swz = [](int r) { return NT == 64 ? 2 * ((r >> 1) & 1) + 4 * ((r >> 3) & 1) : 2 * (r & 3) + 8 * ((r >> 3) & 1); };
+  uint32_t b_off[NBQ];
+  int b_row[NBQ];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = 8 * q + (lane >> 3);
-    const int lc = (lane & 7) ^ (2 * ((r >> 1) & 1) + 4 * ((r >> 3) & 1));
+  for (int q = 0; q < NBQ; ++q) {
+    const int r = (64 / CH) * q + lane / CH;
+    const int lc = (lane % CH) ^ swz(r);
     b_row[q] = r;
     b_off[q] = ((uint32_t)r * (uint32_t)ldb + (uint32_t)(n0 + lc * 8)) * 2u;
   }
@@ -874,7 +881,7 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const eas_op_t* __res
     const int k0 = kb + t * KS;
     const uint32_t dst = lds_ws + (uint32_t)((t % NST) * STH) * 2u;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NBQ; ++q) {
       uint32_t off = b_off[q] + (uint32_t)k0 * (uint32_t)ldb * 2u;
       if (k0 + b_row[q] >= ke) off = 0x80000000u;  // another wave's rows, or past K: zeros
       eas_dma16(rb, off, dst + q * 1024);
@@ -889,21 +896,21 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const eas_op_t* __res
   // 16x16x32 operands: A lane l holds A[l%16][8(l/16)..+7]; B lane l holds B[8(l/16)..+7][l%16]
   const int fm = lane & 15;
   const int fa = fm * KS + (((lane >> 4) ^ ((fm >> 2) & 3)) * 8);
-  int fb[4][2];
+  int fb[NJ][2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int g = lane >> 4, kq = lane & 15;
       const int row = 8 * g + 4 * h + (kq >> 2), col = 16 * j + 4 * (kq & 3);
-      const int pc = (col >> 3) ^ (2 * ((row >> 1) & 1) + 4 * ((row >> 3) & 1));
+      const int pc = (col >> 3) ^ swz(row);
       fb[j][h] = row * NT + pc * 8 + (col & 7);
     }
-  eas_f32x4_acc acc[MT][4];
+  eas_f32x4_acc acc[MT][NJ];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[mt][j] = (eas_f32x4_acc){};
+    for (int j = 0; j < NJ; ++j) acc[mt][j] = (eas_f32x4_acc){};
 #pragma unroll
   for (int p = 0; p < NST - 1; ++p)
     if (p < nsteps) dma_step(p);
@@ -919,7 +926,7 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const eas_op_t* __res
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) a[mt] = *(const eas_h8*)(st + BST + mt * 16 * KS + fa);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(st + fb[j][0]));
       const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(st + fb[j][1]));
       const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
@@ -930,30 +937,31 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const eas_op_t* __res
   }
   __syncthreads();
   // 16x16 D layout: lane l, register r holds (row 4(l/16) + r, col l%16)
-  float* red = (float*)smem;  // [4 waves][MR][64]
+  float* red = (float*)smem;  // [4 waves][MR][NT]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         red[(wave * MR + 16 * mt + 4 * (lane >> 4) + r) * NT + 16 * j + (lane & 15)] = acc[mt][j][r];
   __syncthreads();
 #pragma unroll
-  for (int e = 0; e < MR / 4; ++e) {
-    const int idx = tid + 256 * e, row = idx >> 6, col = idx & 63;
+  for (int e = 0; e < MR * NT / 256; ++e) {
+    const int idx = tid + 256 * e, row = idx / NT, col = idx % NT;
     const float sum = (red[row * NT + col] + red[(MR + row) * NT + col]) +
                       (red[(2 * MR + row) * NT + col] + red[(3 * MR + row) * NT + col]);
     if (row < M && n0 + col < N) C[(size_t)row * ldb + n0 + col] = (CT)sum;
   }
 }
 
-// Skinny path for inputs the DMA cannot take (f32 or unaligned): one thread per (column, 4 MT rows).
+// Skinny path for inputs the DMA cannot take (f32 or unaligned): one thread per (column, 4 MT rows)
+// of the 64 columns from n0.
 template <typename AT, typename BT, typename CT, int K, int MT>
 static __device__ __forceinline__ void eas_gemm_skinny_simple(const AT* __restrict__ A, const BT* __restrict__ B,
-                                                              CT* __restrict__ C, int ldb, int M, int N) {
+                                                              CT* __restrict__ C, int ldb, int M, int N, int n0) {
   constexpr int R = 4 * MT;  // rows per thread: r0, r0 + 4, ...
-  const int tid = threadIdx.x, col = blockIdx.x * 64 + (tid & 63), r0 = tid >> 6;
+  const int tid = threadIdx.x, col = n0 + (tid & 63), r0 = tid >> 6;
   if (col >= N) return;
   float acc[R];
 #pragma unroll
@@ -1153,19 +1161,40 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
   const bool dma_ok = OP_IN && (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
                       ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
   const bool skinny_dma_ok = dma_ok && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0);
-  if (M <= SKINNY_M) {  // the launch plan gives one workgroup per 64 columns; 1, 2, 4 or 8 row tiles of 16
+  if (M <= SKINNY_M) {
+    // The launch plan gives one workgroup per 64 columns, or per 128 when that keeps a launch of at
+    // most 16 rows to one round of CUs; the grid says which.  1, 2, 4 or 8 row tiles of 16.
+    const bool wide = (int)gridDim.x * 64 < N;
+    const int n0 = (int)blockIdx.x * (wide ? 128 : 64);
     if constexpr (OP_IN) {
       if (skinny_dma_ok) {
-        if (M <= 16) eas_gemm_skinny_dma<CT, K, 1>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, smem);
-        else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, smem);
-        else if (M <= 64) eas_gemm_skinny_dma<CT, K, 4>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, smem);
-        else eas_gemm_skinny_dma<CT, K, 8>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, smem);
-        return;
+        const eas_op_t* __restrict__ Ah = (const eas_op_t*)A;
+        const eas_op_t* __restrict__ Bh = (const eas_op_t*)B;
+        if (wide) {
+          if (M <= 16) {  // the only launches planned on the 128-column grid
+            eas_gemm_skinny_dma<CT, K, 1, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
+            return;
+          }
+        } else {
+          if (M <= 16) eas_gemm_skinny_dma<CT, K, 1>(Ah, Bh, C, ldb, M, N, n0, smem);
+          else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2>(Ah, Bh, C, ldb, M, N, n0, smem);
+          else if (M <= 64) eas_gemm_skinny_dma<CT, K, 4>(Ah, Bh, C, ldb, M, N, n0, smem);
+          else eas_gemm_skinny_dma<CT, K, 8>(Ah, Bh, C, ldb, M, N, n0, smem);
+          return;
+        }
       }
     }
-    if (M <= 16) eas_gemm_skinny_simple<AT, BT, CT, K, 1>(A, B, C, ldb, M, N);
-    else if (M <= 64) eas_gemm_skinny_simple<AT, BT, CT, K, 4>(A, B, C, ldb, M, N);
-    else eas_gemm_skinny_simple<AT, BT, CT, K, 8>(A, B, C, ldb, M, N);
+    // inputs the DMA cannot take (on a 128-column grid, 64 columns at a time)
+    if (M <= 16) {
+      eas_gemm_skinny_simple<AT, BT, CT, K, 1>(A, B, C, ldb, M, N, n0);
+      if (wide) eas_gemm_skinny_simple<AT, BT, CT, K, 1>(A, B, C, ldb, M, N, n0 + 64);
+    } else if (M <= 64) {
+      eas_gemm_skinny_simple<AT, BT, CT, K, 4>(A, B, C, ldb, M, N, n0);
+      if (wide) eas_gemm_skinny_simple<AT, BT, CT, K, 4>(A, B, C, ldb, M, N, n0 + 64);
+    } else {
+      eas_gemm_skinny_simple<AT, BT, CT, K, 8>(A, B, C, ldb, M, N, n0);
+      if (wide) eas_gemm_skinny_simple<AT, BT, CT, K, 8>(A, B, C, ldb, M, N, n0 + 64);
+    }
     return;
   }
   int m0, n0;

@@ -1039,9 +1039,12 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
     if m <= p.get("skinny_m", 0):
         # The 4-wave entry runs its skinny path for every launch of at most skinny_m rows (one
         # workgroup per skinny_n columns, all rows), so it is only ever launched on that grid.
-        # From 17 rows on, a launch whose skinny grid would take more than one round of CUs goes
-        # to the 128 x 128 entry instead (or to the entry EAS_HIP_GEMM_ENTRY names).
+        # Up to 16 rows, a launch whose groups would take more than one round of CUs gets twice
+        # the columns per workgroup (the kernel reads which from the grid).  From 17 rows on, such
+        # a launch goes to the 128 x 128 entry instead (or to the entry EAS_HIP_GEMM_ENTRY names).
         groups = -(-n // p["skinny_n"])
+        if m <= SKINNY_CUT and groups > compute_units:
+            groups = -(-n // (2 * p["skinny_n"]))
         other = None
         if m > SKINNY_CUT and p.get("pp_entry") and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
             if choice == "tile128" or (choice == "auto" and groups > compute_units):

@@ -70,6 +70,25 @@ def test_skinny_path_matches_f64(gpu_runtime, mnk):
     _check(c, a, b, m, n, k)
 
 
+@pytest.mark.parametrize("mnk,dtype", [((1, 16448, 64), np.float16), ((16, 16390, 200), np.float16),
+                                       ((7, 16448, 36), np.float16), ((16, 16390, 40), np.float32),
+                                       ((12, 28672, 1000), np.float16)])
+def test_skinny_path_on_128_column_groups(gpu_runtime, mnk, dtype):
+    """Up to 16 rows with more 64-column groups than CUs: one workgroup per 128 columns (a last
+    group of 64 or 6 columns; K % 8 != 0 and f32 inputs take the path without the DMA, 64 columns
+    at a time)."""
+    from easy_as_amd.runtime.hip import plan_launch
+
+    m, n, k = mnk
+    a, b = _inputs(m, n, k, dtype)
+    ck = K.matmul_mma_kernel.compile(a, b, np.zeros(1, np.float32), m, n, BM=32, BN=32, BK=8, K=k, NT=512)
+    args = {"a": a, "b": b, "M": m, "N": n}
+    assert plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args)).grid == (-(-n // 128), 1, 1)
+    c = np.full(m * n, np.nan, np.float32)
+    _mma(K.matmul_mma_kernel, a, b, c, m, n, k)
+    _check(c, a.astype(np.float16), b.astype(np.float16), m, n, k)
+
+
 @pytest.mark.parametrize("mnk,dtype", [((7, 101, 64), np.float16), ((16, 96, 72), np.float32),
                                        ((40, 101, 64), np.float16), ((64, 96, 72), np.float32),
                                        ((100, 101, 64), np.float16)])
@@ -81,11 +100,11 @@ def test_skinny_fallback_unaligned_or_f32(gpu_runtime, mnk, dtype):
     _check(c, a.astype(np.float16), b.astype(np.float16), m, n, k)
 
 
-@pytest.mark.parametrize("m", [16, 64, 128])
-def test_decode_shape_f16_out(gpu_runtime, m):
+@pytest.mark.parametrize("m,n", [(16, 14336), (64, 14336), (128, 14336), (16, 28672)])
+def test_decode_shape_f16_out(gpu_runtime, m, n):
     import torch
 
-    n, k = 14336, 4096
+    k = 4096
     rng = np.random.default_rng(3)
     a = rng.standard_normal(m * k, dtype=np.float32).astype(np.float16)
     b = (0.02 * rng.standard_normal(k * n, dtype=np.float32)).astype(np.float16)
