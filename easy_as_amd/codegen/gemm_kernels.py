@@ -1170,11 +1170,11 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
       if (skinny_dma_ok) {
         const eas_op_t* __restrict__ Ah = (const eas_op_t*)A;
         const eas_op_t* __restrict__ Bh = (const eas_op_t*)B;
-        if (wide) {
-          if (M <= 16) {  // the only launches planned on the 128-column grid
-            eas_gemm_skinny_dma<CT, K, 1, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
-            return;
-          }
+        if (wide) {  // planned for up to 64 rows
+          if (M <= 16) eas_gemm_skinny_dma<CT, K, 1, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
+          else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
+          else if (M <= 64) eas_gemm_skinny_dma<CT, K, 4, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
+          if (M <= 64) return;
         } else {
           if (M <= 16) eas_gemm_skinny_dma<CT, K, 1>(Ah, Bh, C, ldb, M, N, n0, smem);
           else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2>(Ah, Bh, C, ldb, M, N, n0, smem);

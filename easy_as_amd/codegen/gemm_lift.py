@@ -1039,11 +1039,12 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
     if m <= p.get("skinny_m", 0):
         # The 4-wave entry runs its skinny path for every launch of at most skinny_m rows (one
         # workgroup per skinny_n columns, all rows), so it is only ever launched on that grid.
-        # Up to 16 rows, a launch whose groups would take more than one round of CUs gets twice
-        # the columns per workgroup (the kernel reads which from the grid).  From 17 rows on, such
-        # a launch goes to the 128 x 128 entry instead (or to the entry EAS_HIP_GEMM_ENTRY names).
+        # Up to WIDE_M rows, a launch whose groups would take more than one round of CUs gets
+        # twice the columns per workgroup (the kernel reads which from the grid).  From 17 rows
+        # on, a launch whose groups still take more than one round goes to the 128 x 128 entry
+        # instead (or to the entry EAS_HIP_GEMM_ENTRY names).
         groups = -(-n // p["skinny_n"])
-        if m <= SKINNY_CUT and groups > compute_units:
+        if m <= WIDE_M and groups > compute_units:
             groups = -(-n // (2 * p["skinny_n"]))
         other = None
         if m > SKINNY_CUT and p.get("pp_entry") and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
@@ -1075,6 +1076,7 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
 
 _ENTRY_CHOICES = ("auto", "8wave", "tile128", "tile128x256", "4wave")
 SKINNY_CUT = 16  # up to this many rows a launch always takes the skinny path
+WIDE_M = 64  # up to this many rows the skinny path may take 128 columns per workgroup
 
 
 def _gemm_entry_choice() -> str:

@@ -72,9 +72,13 @@ def test_skinny_path_matches_f64(gpu_runtime, mnk):
 
 @pytest.mark.parametrize("mnk,dtype", [((1, 16448, 64), np.float16), ((16, 16390, 200), np.float16),
                                        ((7, 16448, 36), np.float16), ((16, 16390, 40), np.float32),
-                                       ((12, 28672, 1000), np.float16)])
+                                       ((12, 28672, 1000), np.float16),
+                                       # 2 and 4 row tiles of 16 (17-64 rows)
+                                       ((17, 16448, 72), np.float16), ((32, 16390, 200), np.float16),
+                                       ((48, 16448, 1000), np.float16), ((64, 20480, 64), np.float16),
+                                       ((40, 16390, 36), np.float16), ((64, 16448, 40), np.float32)])
 def test_skinny_path_on_128_column_groups(gpu_runtime, mnk, dtype):
-    """Up to 16 rows with more 64-column groups than CUs: one workgroup per 128 columns (a last
+    """Up to 64 rows with more 64-column groups than CUs: one workgroup per 128 columns (a last
     group of 64 or 6 columns; K % 8 != 0 and f32 inputs take the path without the DMA, 64 columns
     at a time)."""
     from easy_as_amd.runtime.hip import plan_launch
