@@ -328,7 +328,9 @@ def _matmul(name: str, rt, torch, steps: int, warmup: int, data: str = "seeded",
     if tms is not None:
         res["torch_matmul"] = {"op": vendor_op, "TFLOP/s": round(flops / (tms * 1e-3) / 1e12, 1),
                                "ms_per_launch": round(tms, 5), "out_dtype": str(out_dt).replace("torch.", ""),
-                               "timing": "event trials alternating with the eas kernel's"}
+                               "timing": "event trials alternating with the eas kernel's; each call is issued "
+                                         "from Python, so a kernel shorter than the call's host cost "
+                                         "(~30 us) reads slow here, where a kernel trace times it exactly"}
         _log(f"{name}: {vendor_op} {res['torch_matmul']['TFLOP/s']} TFLOP/s, {tms:.4f} ms/launch")
     if cpu_baseline and data == "seeded":
         res["cpu_baseline"] = _matmul_cpu_baseline(name, ha, hb, m, n, k)
