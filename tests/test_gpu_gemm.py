@@ -337,6 +337,33 @@ _BASELINE_SHAPES = [
 ]
 
 
+# LLM-linear shapes on each entry the launch plan picks by itself (which one is asserted), every
+# output checked the same way: 128 x 256 tiles, 128 x 128 tiles, 128-column skinny groups, and
+# the 128-tile entry for a wide launch of more than 64 rows.
+_PLAN_SHAPES = [
+    ("matmul_mma_kernel", 512, 14336, 1024, "f16", "n1", "n02", False, "__t128x256"),
+    ("matmul_mma_kernel", 2048, 2048, 2048, "f16", "u", "u", False, "__t128"),
+    ("matmul_mma_f16out_kernel", 48, 28672, 2048, "f16", "n1", "n02", True, ""),
+    ("matmul_mma_f16out_kernel", 128, 28672, 1024, "f16", "n1", "n02", True, "__t128"),
+]
+
+
+@pytest.mark.parametrize("case", _PLAN_SHAPES, ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}x{c[3]}")
+def test_plan_entries_on_llm_shapes_every_output_vs_float64(gpu_runtime, case):
+    import torch
+
+    from easy_as_amd.runtime.hip import plan_launch
+
+    kname, m, n, k, op, da, db, out16, suffix = case
+    z = torch.zeros(1, dtype=torch.float16, device="cuda")
+    ck = getattr(K, kname).compile(z, z, z if out16 else torch.zeros(1, device="cuda"), m, n, BM=32, BN=32, BK=8,
+                                   K=k, NT=512)
+    args = {"M": m, "N": n}
+    entry = plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args)).entry
+    assert entry == (kname + suffix if suffix else None), entry
+    test_baseline_shapes_every_output_vs_float64(gpu_runtime, case[:8])
+
+
 @pytest.mark.parametrize("case", _BASELINE_SHAPES, ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}x{c[3]}")
 def test_baseline_shapes_every_output_vs_float64(gpu_runtime, case):
     import torch
