@@ -834,10 +834,10 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
       }
 }
 
-// Skinny path (M <= 128, decode-like): one workgroup per NT = 64 columns (128 for launches of at
-// most 16 rows whose 64-column groups would need more than one round of CUs), the four waves
-// split K.  Each wave streams its K range of B (and A) HBM -> LDS into a private 4-stage ring (3
-// stages where 4 would not fit the LDS; no barriers in the loop), multiplies MT row tiles of 16
+// Skinny path (M <= 128, decode-like): one workgroup per NT = 64 columns (128 for launches whose
+// 64-column groups would need more than one round of CUs), the four waves split K.  Each wave
+// streams its K range of B (and A) HBM -> LDS into a private ring of 4 stages (3 or 2 where 4
+// would not fit the LDS; no barriers in the loop), multiplies MT row tiles of 16
 // (1, 2, 4 or 8) by NT / 16 column tiles with v_mfma_f32_16x16x32_f16 (B transposed by
 // ds_read_b64_tr_b16), and the waves add their 16 MT x NT partial sums through LDS at the end.
 template <typename CT, int K, int MT, int NT = 64>
@@ -849,7 +849,7 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const eas_op_t* __res
   constexpr int KS = 32, MR = 16 * MT, NJ = NT / 16;
   constexpr int KW = ((K + 4 * KS - 1) / (4 * KS)) * KS;  // k rows per wave
   constexpr int BST = KS * NT, AST = MR * KS, STH = BST + AST;  // halves per stage: B [32][NT], A [MR][32]
-  constexpr int NST = 4 * 4 * STH * 2 <= 147456 ? 4 : 3;        // stages per wave ring (144 KB of LDS)
+  constexpr int NST = 4 * 4 * STH * 2 <= 147456 ? 4 : 4 * 3 * STH * 2 <= 147456 ? 3 : 2;  // per wave (144 KB)
   static_assert(4 * NST * STH * 2 <= 147456, "the rings fit the entry's LDS");
   constexpr int NBQ = NT / 16, CH = NT / 8;                     // B DMA instructions per stage, chunks per row
   constexpr int LOADS = NBQ + MT;                               // DMA instructions per stage
@@ -935,23 +935,30 @@ static __device__ __forceinline__ void eas_gemm_skinny_dma(const eas_op_t* __res
       for (int mt = 0; mt < MT; ++mt) acc[mt][j] = EAS_MFMA16(a[mt], b, acc[mt][j], 0, 0, 0);
     }
   }
-  __syncthreads();
-  // 16x16 D layout: lane l, register r holds (row 4(l/16) + r, col l%16)
-  float* red = (float*)smem;  // [4 waves][MR][NT]
+  // The waves' partial sums meet in LDS, RP rows at a time: [4 waves][RP][NT] floats must fit the
+  // entry's 144 KB (all rows at once, except 8 row tiles on 128 columns: two passes of 64 rows).
+  constexpr int RP = 4 * MR * NT * 4 <= 147456 ? MR : 64;
+  static_assert(4 * RP * NT * 4 <= 147456 && MR % RP == 0, "the reduction fits the LDS");
+  float* red = (float*)smem;  // [4 waves][RP][NT]
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int p0 = 0; p0 < MR; p0 += RP) {
+    __syncthreads();  // every wave is past its K loop (first pass) or the previous pass's reads
+    // 16x16 D layout: lane l, register r holds (row 4(l/16) + r, col l%16)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
+    for (int mt = p0 / 16; mt < (p0 + RP) / 16; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        red[(wave * MR + 16 * mt + 4 * (lane >> 4) + r) * NT + 16 * j + (lane & 15)] = acc[mt][j][r];
-  __syncthreads();
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
-  for (int e = 0; e < MR * NT / 256; ++e) {
-    const int idx = tid + 256 * e, row = idx / NT, col = idx % NT;
-    const float sum = (red[row * NT + col] + red[(MR + row) * NT + col]) +
-                      (red[(2 * MR + row) * NT + col] + red[(3 * MR + row) * NT + col]);
-    if (row < M && n0 + col < N) C[(size_t)row * ldb + n0 + col] = (CT)sum;
+        for (int r = 0; r < 4; ++r)
+          red[(wave * RP + 16 * mt - p0 + 4 * (lane >> 4) + r) * NT + 16 * j + (lane & 15)] = acc[mt][j][r];
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < RP * NT / 256; ++e) {
+      const int idx = tid + 256 * e, row = idx / NT, col = idx % NT;
+      const float sum = (red[row * NT + col] + red[(RP + row) * NT + col]) +
+                        (red[(2 * RP + row) * NT + col] + red[(3 * RP + row) * NT + col]);
+      if (p0 + row < M && n0 + col < N) C[(size_t)(p0 + row) * ldb + n0 + col] = (CT)sum;
+    }
   }
 }
 
@@ -1162,19 +1169,20 @@ extern "C" __global__ __launch_bounds__(256) void @NAME@(
                       ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
   const bool skinny_dma_ok = dma_ok && (K % 8 == 0) && (ldb % 8 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 16 == 0);
   if (M <= SKINNY_M) {
-    // The launch plan gives one workgroup per 64 columns, or per 128 when that keeps a launch of at
-    // most 16 rows to one round of CUs; the grid says which.  1, 2, 4 or 8 row tiles of 16.
+    // The launch plan gives one workgroup per 64 columns, or per 128 when that keeps the launch to
+    // one round of CUs; the grid says which.  1, 2, 4 or 8 row tiles of 16.
     const bool wide = (int)gridDim.x * 64 < N;
     const int n0 = (int)blockIdx.x * (wide ? 128 : 64);
     if constexpr (OP_IN) {
       if (skinny_dma_ok) {
         const eas_op_t* __restrict__ Ah = (const eas_op_t*)A;
         const eas_op_t* __restrict__ Bh = (const eas_op_t*)B;
-        if (wide) {  // planned for up to 64 rows
+        if (wide) {
           if (M <= 16) eas_gemm_skinny_dma<CT, K, 1, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
           else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
           else if (M <= 64) eas_gemm_skinny_dma<CT, K, 4, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
-          if (M <= 64) return;
+          else eas_gemm_skinny_dma<CT, K, 8, 128>(Ah, Bh, C, ldb, M, N, n0, smem);
+          return;
         } else {
           if (M <= 16) eas_gemm_skinny_dma<CT, K, 1>(Ah, Bh, C, ldb, M, N, n0, smem);
           else if (M <= 32) eas_gemm_skinny_dma<CT, K, 2>(Ah, Bh, C, ldb, M, N, n0, smem);

@@ -1076,7 +1076,7 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
 
 _ENTRY_CHOICES = ("auto", "8wave", "tile128", "tile128x256", "4wave")
 SKINNY_CUT = 16  # up to this many rows a launch always takes the skinny path
-WIDE_M = 64  # up to this many rows the skinny path may take 128 columns per workgroup
+WIDE_M = 128  # up to this many rows the skinny path may take 128 columns per workgroup
 
 
 def _gemm_entry_choice() -> str:

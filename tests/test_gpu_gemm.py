@@ -76,9 +76,12 @@ def test_skinny_path_matches_f64(gpu_runtime, mnk):
                                        # 2 and 4 row tiles of 16 (17-64 rows)
                                        ((17, 16448, 72), np.float16), ((32, 16390, 200), np.float16),
                                        ((48, 16448, 1000), np.float16), ((64, 20480, 64), np.float16),
-                                       ((40, 16390, 36), np.float16), ((64, 16448, 40), np.float32)])
+                                       ((40, 16390, 36), np.float16), ((64, 16448, 40), np.float32),
+                                       # 8 row tiles (65-128 rows): 2-stage rings, two reduction passes
+                                       ((65, 16448, 72), np.float16), ((128, 16390, 200), np.float16),
+                                       ((100, 20480, 1000), np.float16), ((128, 16448, 36), np.float16)])
 def test_skinny_path_on_128_column_groups(gpu_runtime, mnk, dtype):
-    """Up to 64 rows with more 64-column groups than CUs: one workgroup per 128 columns (a last
+    """Up to 128 rows with more 64-column groups than CUs: one workgroup per 128 columns (a last
     group of 64 or 6 columns; K % 8 != 0 and f32 inputs take the path without the DMA, 64 columns
     at a time)."""
     from easy_as_amd.runtime.hip import plan_launch
@@ -249,9 +252,10 @@ def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
     tol = 1e-6 if m > 128 else 1e-5 * math.sqrt(k)
     for choice in ("8wave", "tile128", "tile128x256"):
         assert ops.rel_err(outs[choice], outs["4wave"]) <= tol, choice
-    if m <= 128 and -(-n // 64) > 256:  # more column groups than CUs: the 128-tile entry by default
+    if m <= 128 and -(-n // 64) > 256:  # more 64-column groups than CUs: 128-column skinny groups
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "auto")
-        assert plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args)).entry == "matmul_mma_kernel__t128"
+        plan = plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args))
+        assert plan.entry is None and plan.grid == (-(-n // 128), 1, 1)
 
 
 @pytest.mark.parametrize("mnk", [(300, 520, 200), (257, 264, 72), (520, 256, 1000), (130, 260, 4100),
@@ -338,13 +342,15 @@ _BASELINE_SHAPES = [
 
 
 # LLM-linear shapes on each entry the launch plan picks by itself (which one is asserted), every
-# output checked the same way: 128 x 256 tiles, 128 x 128 tiles, 128-column skinny groups, and
-# the 128-tile entry for a wide launch of more than 64 rows.
+# output checked the same way: 128 x 256 tiles, 128 x 128 tiles, 128-column skinny groups (2 and 8
+# row tiles), and the 128-tile entry for a launch of more than 16 rows too wide for one round of
+# 128-column groups.
 _PLAN_SHAPES = [
     ("matmul_mma_kernel", 512, 14336, 1024, "f16", "n1", "n02", False, "__t128x256"),
     ("matmul_mma_kernel", 2048, 2048, 2048, "f16", "u", "u", False, "__t128"),
     ("matmul_mma_f16out_kernel", 48, 28672, 2048, "f16", "n1", "n02", True, ""),
-    ("matmul_mma_f16out_kernel", 128, 28672, 1024, "f16", "n1", "n02", True, "__t128"),
+    ("matmul_mma_f16out_kernel", 128, 28672, 1024, "f16", "n1", "n02", True, ""),
+    ("matmul_mma_f16out_kernel", 100, 40960, 512, "f16", "n1", "n02", True, "__t128"),
 ]
 
 

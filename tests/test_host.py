@@ -235,15 +235,15 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
         plan = plan_launch(ck, {"M": m, "N": 14336}, grid=(448, K.cdiv(m, 32), 1))
         assert plan.hidden == (0, m, 0, 14336) and plan.grid == (224, 1, 1)
         assert plan.block == (256, 1, 1) and plan.entry is None
-    # 65-128 rows with more column groups than CUs: 128 x 128 tiles instead of two skinny rounds
-    plan = plan_launch(ck, {"M": 128, "N": 28672}, grid=(896, 4, 1))
-    assert plan.grid == (224, 1, 1) and plan.entry == "matmul_mma_kernel__t128" and plan.block == (512, 1, 1)
-    # up to 64 rows: 128 columns per workgroup rather than a second round of CUs
-    for m in (16, 17, 64):
+    # up to 128 rows: 128 columns per workgroup rather than a second round of CUs
+    for m in (16, 17, 64, 65, 128):
         plan = plan_launch(ck, {"M": m, "N": 28672}, grid=(896, K.cdiv(m, 32), 1))
         assert plan.grid == (224, 1, 1) and plan.entry is None
-    plan = plan_launch(ck, {"M": 65, "N": 28672}, grid=(896, 3, 1))
-    assert plan.grid == (224, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
+    # 17-128 rows too wide for one round of 128-column groups: 128 x 128 tiles
+    plan = plan_launch(ck, {"M": 65, "N": 40960}, grid=(1280, 3, 1))
+    assert plan.grid == (320, 1, 1) and plan.entry == "matmul_mma_kernel__t128"
+    plan = plan_launch(ck, {"M": 128, "N": 40960}, grid=(1280, 4, 1))
+    assert plan.grid == (320, 1, 1) and plan.entry == "matmul_mma_kernel__t128" and plan.block == (512, 1, 1)
     plan = plan_launch(ck, {"M": 16, "N": 16384}, grid=(512, 1, 1))
     assert plan.grid == (256, 1, 1) and plan.entry is None  # 256 groups of 64: still one round
     plan = plan_launch(ck, {"M": 16, "N": 16390}, grid=(513, 1, 1))
