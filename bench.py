@@ -426,14 +426,60 @@ def _stamped_f32_source(src: str, entry: str) -> str:
     return _PHASE_STAMP_F32 + src[:start] + body + src[end:]
 
 
+# The f16 128-row entries (128 x 128 and 128 x 256): the same stamps as the fp32 entries, written
+# by lane 0 of consumer wave 0, inside the body both entries share; the entry not measured passes
+# a null stamp pointer.
+_PHASE_STAMP_WS = (
+    "#define EAS_WS_STAMP(slot) do { if (__eas_stamps && threadIdx.x == 0) "
+    "__eas_stamps[blockIdx.x * 8u + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)\n"
+    "#define EAS_WS_CLOCK(slot) do { if (__eas_stamps && threadIdx.x == 0) "
+    "__eas_stamps[blockIdx.x * 8u + (slot)] = __builtin_amdgcn_s_memtime(); } while (0)\n"
+    "#define EAS_WS_XCD() do { if (__eas_stamps && threadIdx.x == 0) __eas_stamps[blockIdx.x * 8u + 5u] = "
+    "(unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u); } while (0)\n")
+
+
+def _stamped_ws_source(src: str, entry: str) -> str:
+    """The generated f16 GEMM source with a stamp buffer appended to ``entry``'s arguments (the
+    128 x 128 or the 128 x 256 entry) and stamps at: entry, start of the K loop (stage 0 landed),
+    end of the K loop (last MFMA issued), C stores issued, C stores complete, plus shader clocks
+    around the K loop.  Raises if the source does not have the expected shape."""
+    src = src.split("\n", 1)[1]  # the eas-launch line describes the unstamped argument list
+    bn = 256 if entry.endswith("__t128x256") else 128
+    call = "eas_gemm_t128<CT, K, {}>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
+    edits = [
+        ("eas_op_t* smem) {\n  static_assert(BN == 128 || BN == 256",
+         "eas_op_t* smem, unsigned long long* __restrict__ __eas_stamps) {\n  static_assert(BN == 128 || BN == 256"),
+        ("  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n  if (wave >= 4) {\n    // DMA instructions",
+         "  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n  EAS_WS_STAMP(0);\n  EAS_WS_XCD();\n"
+         "  if (wave >= 4) {\n    // DMA instructions"),
+        ("  __syncthreads();  // stage 0 landed\n  afrag_t a0, a1;\n",
+         "  __syncthreads();  // stage 0 landed\n  EAS_WS_STAMP(1);\n  EAS_WS_CLOCK(6);\n  afrag_t a0, a1;\n"),
+        ("  } else {\n    mask_tail(a0);\n    mfmas(a0, b0);\n  }\n",
+         "  } else {\n    mask_tail(a0);\n    mfmas(a0, b0);\n  }\n  EAS_WS_STAMP(2);\n  EAS_WS_CLOCK(7);\n"),
+        ("C[(size_t)row * ldb + col] = (CT)acc[i][j][r];\n      }\n}\n\n// Skinny path",
+         "C[(size_t)row * ldb + col] = (CT)acc[i][j][r];\n      }\n  EAS_WS_STAMP(3);\n"
+         "  __builtin_amdgcn_s_waitcnt(0);\n  EAS_WS_STAMP(4);\n}\n\n// Skinny path"),
+        (call.format(128), call.format(128)[:-2] + (", __eas_stamps);" if bn == 128 else ", nullptr);")),
+        (call.format(256), call.format(256)[:-2] + (", __eas_stamps);" if bn == 256 else ", nullptr);")),
+    ]
+    for old, new in edits:
+        if src.count(old) != 1:
+            raise RuntimeError(f"--phases: unexpected f16 GEMM source shape at {old[:48]!r}")
+        src = src.replace(old, new)
+    head = src.index(f"void {entry}(")
+    close = src.index(") {", head)
+    src = src[:close] + ",\n    unsigned long long* __restrict__ __eas_stamps" + src[close:]
+    return _PHASE_STAMP_WS + src
+
+
 def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
-    """Per-phase time budget of one launch of the 8-wave GEMM entry, or of either fp32 entry, on
-    the configuration's seeded inputs: after settling, ``trials`` times run ``lead`` launches back
-    to back and one more, and read the last launch's stamps.  Medians over the trials of: spread
-    of workgroup starts, prologue, K loop (median, min, max over wave groups, median per XCD), C
-    store issue, store completion, median and last end; all in microseconds from the first
-    workgroup's start.  The fp32 entries add the K loop's shader clocks per BK = 32 stage and the
-    shader clock they imply."""
+    """Per-phase time budget of one launch of the 8-wave GEMM entry, of either f16 128-row entry,
+    or of either fp32 entry, on the configuration's seeded inputs: after settling, ``trials`` times
+    run ``lead`` launches back to back and one more, and read the last launch's stamps.  Medians
+    over the trials of: spread of workgroup starts, prologue, K loop (median, min, max over wave
+    groups, median per XCD), C store issue, store completion, median and last end; all in
+    microseconds from the first workgroup's start.  The fp32 and 128-row entries add the K loop's
+    shader clocks per BK = 32 stage and the shader clock they imply."""
     import kernels as K
     from easy_as_amd.runtime.hip import compile_code, plan_launch, struct
 
@@ -453,8 +499,11 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
     mod = rt._mod()
     plan = plan_launch(ck, args, grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), compute_units=rt._cus)
     entry = plan.entry or ck.geometry.entry if plan is not None else None
+    ws = entry is not None and (entry.endswith("__t128") or entry.endswith("__t128x256")) and not tiled
     if tiled:
         src, per_wg = _stamped_f32_source(ck.src, entry), 1
+    elif ws:
+        src, per_wg = _stamped_ws_source(ck.src, entry), 1
     elif entry is None or not entry.endswith("__pp"):
         raise RuntimeError(f"--phases needs the 8-wave GEMM entry; {name} launches {entry}")
     else:
@@ -487,7 +536,7 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
         t = s[:, :, :5].astype(np.float64) * 0.01  # 100 MHz ticks -> us
         t -= t[:, :, 0].min()
         loop = t[:, :, 2] - t[:, :, 1]
-        if tiled:  # shader clocks over the K loop (slots 6, 7), per BK = 32 stage
+        if tiled or ws:  # shader clocks over the K loop (slots 6, 7), per BK = 32 stage
             clk = (s[:, 0, 7] - s[:, 0, 6]).astype(np.float64)
             runs.append({"loop_clocks_per_stage": float(np.median(clk)) / -(-k // 32),
                          "loop_shader_GHz": float(np.median(clk / (loop[:, 0] * 1e3)))})
@@ -510,12 +559,16 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
     out.update({"unit": "us", "entry": entry, "workgroups": groups, "trials": trials,
                 "method": f"median over {trials} trials of the last of {lead + 1} back-to-back launches; "
                           "s_memrealtime stamps by lane 0 of each wave group"
-                          + (" (consumer wave 0); s_memtime shader clocks over the K loop" if tiled else "")})
-    if tiled:
+                          + (" (consumer wave 0); s_memtime shader clocks over the K loop" if tiled or ws else "")})
+    if tiled or ws:
         out["loop_clocks_per_stage"] = round(float(np.median([r["loop_clocks_per_stage"] for r in runs])), 1)
         out["loop_shader_GHz"] = round(float(np.median([r["loop_shader_GHz"] for r in runs])), 3)
+    if tiled:
         # v_mfma_f32_32x32x2_f32 keeps a SIMD's MFMA pipe 64 clocks; 16 steps of 2 k per stage
         out["mfma_clocks_per_stage"] = 64 * 16 * (4 if entry.endswith("__t128") else 1)
+    elif ws:
+        # v_mfma_f32_32x32x16_f16 keeps it 32 clocks; 8 (128 x 128) or 16 (128 x 256) per stage
+        out["mfma_clocks_per_stage"] = 32 * (16 if entry.endswith("__t128x256") else 8)
     del a, b, c, stamps
     torch.cuda.empty_cache()
     return out
@@ -854,9 +907,10 @@ def main() -> int:
                    help="matmul workloads only: M,N,K instead of the configuration's shape (a scaling study, "
                         "not the metric)")
     p.add_argument("--phases", action="store_true",
-                   help="matmul workloads on the 8-wave GEMM entry or an fp32 entry: add an in-kernel "
-                        "per-phase time budget of one launch (a stamped copy of the kernel, timed after the "
-                        "measurement; the fp32 entries also give shader clocks per K stage)")
+                   help="matmul workloads on the 8-wave GEMM entry, an f16 128-row entry or an fp32 entry: "
+                        "add an in-kernel per-phase time budget of one launch (a stamped copy of the kernel, "
+                        "timed after the measurement; the 128-row and fp32 entries also give shader clocks "
+                        "per K stage)")
     p.add_argument("--data", choices=MATMUL_DATA, default="seeded",
                    help="matmul workloads only: input data (anything but 'seeded' is not the metric's data)")
     args = p.parse_args()

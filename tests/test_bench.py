@@ -123,6 +123,54 @@ def test_stamped_f32_source_stamps_only_its_entry(name, entry):
                                   entry)
 
 
+def _ws_source(m, n, k):
+    from easy_as_amd.runtime.hip import plan_launch
+
+    z = np.zeros(1, np.float16)
+    ck = K.matmul_mma_kernel.compile(z, z, np.zeros(1, np.float32), m, n, BM=32, BN=32, BK=8, K=k, NT=512)
+    plan = plan_launch(ck, {"M": m, "N": n}, grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), compute_units=256)
+    return ck, plan.entry
+
+
+@pytest.mark.parametrize("mnk, entry", [((2048, 2048, 2048), "matmul_mma_kernel__t128"),
+                                        ((512, 14336, 1024), "matmul_mma_kernel__t128x256")])
+def test_stamped_ws_source_stamps_only_its_entry(mnk, entry):
+    from easy_as_amd.runtime.hip import compile_code
+    from easy_as_amd.runtime.hip_ext import load_hip_ext
+
+    ck, got = _ws_source(*mnk)
+    assert got == entry
+    src = bench._stamped_ws_source(ck.src, entry)
+    for slot in range(5):
+        assert src.count(f"EAS_WS_STAMP({slot});") == 1
+    assert src.count("EAS_WS_CLOCK(6);") == src.count("EAS_WS_CLOCK(7);") == src.count("EAS_WS_XCD();") == 1
+    assert src.count("unsigned long long* __restrict__ __eas_stamps") == 2  # the body and the entry
+    assert src.count(", nullptr);") == 1  # the other 128-row entry passes no stamp buffer
+    mod = load_hip_ext(require=False)
+    if mod is not None:
+        assert compile_code(mod, src, ck.ir.name)[:4] == b"\x7fELF"
+    with pytest.raises(RuntimeError, match="unexpected f16 GEMM source shape"):
+        bench._stamped_ws_source(ck.src.replace("  __syncthreads();  // stage 0 landed\n  afrag_t", "  afrag_t"),
+                                 entry)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape, workgroups, mfma_clocks", [((2048, 2048, 2048), 256, 256),
+                                                            ((512, 14336, 1024), 224, 512)])
+def test_phases_of_the_128_row_entries(monkeypatch, shape, workgroups, mfma_clocks):
+    import torch
+
+    from easy_as_amd.runtime import get_runtime
+
+    monkeypatch.setitem(bench.SHAPE_OVERRIDE, "mma", shape)
+    print(f"phases: mma {shape}", flush=True)
+    ph = bench._gemm_phases("mma", get_runtime("hip"), torch, trials=2, lead=3)
+    assert ph["workgroups"] == workgroups and ph["mfma_clocks_per_stage"] == mfma_clocks
+    assert 0 < ph["prologue"] < ph["loop_median"] < ph["end_median"] <= ph["end_last"] < 1000
+    assert mfma_clocks <= ph["loop_clocks_per_stage"] < 8 * mfma_clocks
+    assert 0.5 < ph["loop_shader_GHz"] < 3.0
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("name, stages, mfma_clocks", [("tiled1024", 32, 1024), ("tiled2048", 64, 4096)])
 def test_phases_of_the_fp32_entries(name, stages, mfma_clocks):
