@@ -369,9 +369,9 @@ def _stamped_pp_source(src: str, entry: str) -> str:
          "    if (g == 1) __syncthreads();\n    EAS_STAMP(1);\n    for (int kt = 0; kt < KT; ++kt) stage(kt, kt % NSTAGE, b_fast);"),
         ("  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier\n",
          "  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier\n  EAS_STAMP(2);\n"),
-        ("(CT)acc16[i][j][r];\n        }\n  }\n}",
+        ("(CT)acc16[i][j][r];\n        }\n  }\n}\n\n// Guard body",
          "(CT)acc16[i][j][r];\n        }\n  }\n  EAS_STAMP(3);\n  __builtin_amdgcn_s_waitcnt(0);\n"
-         "  EAS_STAMP(4);\n}"),
+         "  EAS_STAMP(4);\n}\n\n// Guard body"),
         ("eas_gemm_pp<CT, K, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);",
          "eas_gemm_pp<CT, K, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem, __eas_stamps);"),
     ]
@@ -445,19 +445,19 @@ def _stamped_ws_source(src: str, entry: str) -> str:
     around the K loop.  Raises if the source does not have the expected shape."""
     src = src.split("\n", 1)[1]  # the eas-launch line describes the unstamped argument list
     bn = 256 if entry.endswith("__t128x256") else 128
-    call = "eas_gemm_t128<CT, K, {}>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
+    call = "eas_gemm_t128<CT, K, {}, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
     edits = [
-        ("eas_op_t* smem) {\n  static_assert(BN == 128 || BN == 256",
-         "eas_op_t* smem, unsigned long long* __restrict__ __eas_stamps) {\n  static_assert(BN == 128 || BN == 256"),
-        ("  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n  if (wave >= 4) {\n    // DMA instructions",
-         "  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);\n  EAS_WS_STAMP(0);\n  EAS_WS_XCD();\n"
-         "  if (wave >= 4) {\n    // DMA instructions"),
+        ("eas_op_t* smem) {\n  static_assert((BN == 128 || BN == 256)",
+         "eas_op_t* smem, unsigned long long* __restrict__ __eas_stamps) {\n  static_assert((BN == 128 || BN == 256)"),
+        ("  auto bsw = [](int r) { return (4 * (r & 3)) ^ (2 * ((r >> 3) & 1)); };\n  if (wave >= 4) {",
+         "  auto bsw = [](int r) { return (4 * (r & 3)) ^ (2 * ((r >> 3) & 1)); };\n  EAS_WS_STAMP(0);\n"
+         "  EAS_WS_XCD();\n  if (wave >= 4) {"),
         ("  __syncthreads();  // stage 0 landed\n  afrag_t a0, a1;\n",
          "  __syncthreads();  // stage 0 landed\n  EAS_WS_STAMP(1);\n  EAS_WS_CLOCK(6);\n  afrag_t a0, a1;\n"),
         ("  } else {\n    mask_tail(a0);\n    mfmas(a0, b0);\n  }\n",
          "  } else {\n    mask_tail(a0);\n    mfmas(a0, b0);\n  }\n  EAS_WS_STAMP(2);\n  EAS_WS_CLOCK(7);\n"),
-        ("C[(size_t)row * ldb + col] = (CT)acc[i][j][r];\n      }\n}\n\n// Skinny path",
-         "C[(size_t)row * ldb + col] = (CT)acc[i][j][r];\n      }\n  EAS_WS_STAMP(3);\n"
+        ("(CT)acc16[i][j][r];\n        }\n  }\n}\n\n// Skinny path",
+         "(CT)acc16[i][j][r];\n        }\n  }\n  EAS_WS_STAMP(3);\n"
          "  __builtin_amdgcn_s_waitcnt(0);\n  EAS_WS_STAMP(4);\n}\n\n// Skinny path"),
         (call.format(128), call.format(128)[:-2] + (", __eas_stamps);" if bn == 128 else ", nullptr);")),
         (call.format(256), call.format(256)[:-2] + (", __eas_stamps);" if bn == 256 else ", nullptr);")),
@@ -567,8 +567,8 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
         # v_mfma_f32_32x32x2_f32 keeps a SIMD's MFMA pipe 64 clocks; 16 steps of 2 k per stage
         out["mfma_clocks_per_stage"] = 64 * 16 * (4 if entry.endswith("__t128") else 1)
     elif ws:
-        # v_mfma_f32_32x32x16_f16 keeps it 32 clocks; 8 (128 x 128) or 16 (128 x 256) per stage
-        out["mfma_clocks_per_stage"] = 32 * (16 if entry.endswith("__t128x256") else 8)
+        # v_mfma_f32_16x16x32_f16 keeps it 16 clocks; 16 (128 x 128) or 32 (128 x 256) per stage
+        out["mfma_clocks_per_stage"] = 16 * (32 if entry.endswith("__t128x256") else 16)
     del a, b, c, stamps
     torch.cuda.empty_cache()
     return out

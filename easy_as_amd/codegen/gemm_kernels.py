@@ -620,15 +620,16 @@ static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict
 // 8 waves (512 threads), specialised like the fp32 entries, on a ring of 4 stages of 8 KB of A
 // and BN / 16 KB of B.  Waves 4-7 produce: the DMA of stage kt+3, 2 A + BN / 64 B loads of 1 KB
 // per wave per stage, with the stage offset in soffset, so the loads cost the MFMA waves sharing
-// their SIMDs nothing.  Waves 0-3 consume, 64 x BN/2 each (2 x BN/64 accumulators of 32x32x16):
-// the fragments of stage kt+1 are read between stage kt's MFMAs.  A load costs the SIMD that
+// their SIMDs nothing.  Waves 0-3 consume, 64 x BN/2 each (MI 16: 4 x BN/32 accumulators of
+// 16x16x32; MI 32: 2 x BN/64 of 32x32x16): the fragments of stage kt+1 are read between stage
+// kt's MFMAs.  A load costs the SIMD that
 // issues it tens of clocks of MFMA issue, which in a 4-wave form of this body (each wave loading
 // its quarter of every stage beside 8 MFMAs) was most of the stage.
-template <typename CT, int K, int BN>
+template <typename CT, int K, int BN, int MI = 32>
 static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
                                                      eas_op_t* smem) {
-  static_assert(BN == 128 || BN == 256, "128 x 128 and 128 x 256 tiles");
+  static_assert((BN == 128 || BN == 256) && (MI == 32 || MI == 16), "128 x 128 or 128 x 256 tiles, 32- or 16-row MFMAs");
   constexpr int BM = 128, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
   constexpr int NJ = BN / 64;               // 32-column accumulators per consumer wave
   constexpr int NBI = BN / 64;              // B loads per producer wave per stage
@@ -639,10 +640,14 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
   eas_op_t* Bs = smem + NSTAGE * STAGE_A;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // B's 16-byte chunk of row r is stored at chunk ^ bsw(r): bits 2-3 spread the four rows of a
+  // transposing read over the banks, bit 1 keeps rows 8 apart (the two 16-lane groups of a
+  // half-wave in the 16 x 16 x 32 mapping) apart.  Rows r and r + 4 share the mask.
+  auto bsw = [](int r) { return (4 * (r & 3)) ^ (2 * ((r >> 3) & 1)); };
   if (wave >= 4) {
     // DMA instructions write 1 KB of a stage each.  A instruction q = 2 pw + i: rows 16q + lane/4,
     // chunk lane%4 stored at chunk ^ ((row/4)%4).  B instruction q = NBI pw + i: rows
-    // (64 / CH) q + lane / CH, chunk lane % CH stored at chunk ^ 4(row%4).
+    // (64 / CH) q + lane / CH, chunk lane % CH stored at chunk ^ bsw(row).
     // Rows past M load zeros, and so do columns past N when no 8-column chunk straddles N, so
     // every address a load reads, lane offset plus stage offset, lies inside A or B.  An edge tile
     // whose chunk straddles N (N % 8 != 0) adds the stage offset to the lane offset instead, where
@@ -667,7 +672,7 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
     for (int i = 0; i < NBI; ++i) {
       const int q = pw * NBI + i;
       const int r_b = (64 / CH) * q + lane / CH;
-      const int c_b = (lane % CH) ^ (4 * (r_b & 3));
+      const int c_b = (lane % CH) ^ bsw(r_b);
       b_raw[i] = ((uint32_t)r_b * (uint32_t)ldb + (uint32_t)(n0 + c_b * 8)) * 2u;
       b_off[i] = n0 + c_b * 8 < N ? b_raw[i] : 0x80000000u;
       b_tail[i] = r_b < KLAST ? b_raw[i] + (uint32_t)((KT - 1) * BK * 2) * (uint32_t)ldb : 0x80000000u;
@@ -720,64 +725,75 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
     return;
   }
   const int wm = wave >> 1, wn = wave & 1;
-  int fa_off[2][2], fb_off[2][NJ][2];
+  // Fragments per stage: 4 of A and BN / 32 of B, 8 halves a lane each.  MI 32
+  // (v_mfma_f32_32x32x16): A f = 2 ks + i holds A[row 32 i + l%32][k 16 ks + 8(l/32)..+7], B f =
+  // ks NJ + j holds B[k 16 ks + 8(l/32)..+7][col 32 j + l%32]; MI 16 (v_mfma_f32_16x16x32): A f = i
+  // holds A[row 16 i + l%16][k 8(l/16)..+7], B f = j holds B[k 8(l/16)..+7][col 16 j + l%16]
+  // (rows and columns within the wave's 64 x BN/2).
+  constexpr int NA = 4, NB = BN / 32;
+  int fa_off[NA], fb_off[NB];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r = wm * 64 + i * 32 + (lane & 31);
-      const int c = (2 * ks + (lane >> 5)) ^ ((r >> 2) & 3);
-      fa_off[ks][i] = r * BK + c * 8;
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        // ds_read_b64_tr_b16: in each 16-lane group, source lane kq addresses row kq/4, columns 4(kq%4)..+3
-        const int gq = lane >> 4, kq = lane & 15;
-        const int row = 16 * ks + 8 * (gq >> 1) + 4 * h + (kq >> 2);
-        const int col = wn * (BN / 2) + j * 32 + 16 * (gq & 1) + 4 * (kq & 3);
-        const int chunk = (col >> 3) ^ (4 * (row & 3));
-        fb_off[ks][j][h] = row * BN + chunk * 8 + (col & 7);
-      }
+  for (int f = 0; f < NA; ++f) {
+    const int r = MI == 32 ? wm * 64 + (f & 1) * 32 + (lane & 31) : wm * 64 + f * 16 + (lane & 15);
+    const int c = MI == 32 ? (2 * (f >> 1) + (lane >> 5)) : (lane >> 4);
+    fa_off[f] = r * BK + ((c ^ ((r >> 2) & 3)) * 8);
   }
-  eas_f32x16 acc[2][NJ];
+#pragma unroll
+  for (int f = 0; f < NB; ++f) {
+    // ds_read_b64_tr_b16: in each 16-lane group, source lane kq addresses row kq/4, columns
+    // 4(kq%4)..+3; the second read of a pair (rows 4 further down) is 4 BN halves on
+    const int gq = lane >> 4, kq = lane & 15;
+    const int row = MI == 32 ? 16 * (f / NJ) + 8 * (gq >> 1) + (kq >> 2) : 8 * gq + (kq >> 2);
+    const int col = MI == 32 ? wn * (BN / 2) + (f % NJ) * 32 + 16 * (gq & 1) + 4 * (kq & 3)
+                             : wn * (BN / 2) + f * 16 + 4 * (kq & 3);
+    fb_off[f] = row * BN + ((col >> 3) ^ bsw(row)) * 8 + (col & 7);
+  }
+  eas_f32x16 acc[2][NJ];      // MI 32: [i][j] tiles of 32 x 32
+  eas_f32x4 acc16[4][NB];     // MI 16: [i][j] tiles of 16 x 16
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = (eas_f32x16){};
-  typedef eas_h8 afrag_t[2][2];   // [ks][i]
-  typedef eas_h8 bfrag_t[2][NJ];  // [ks][j]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc16[i][j] = (eas_f32x4){};
+  typedef eas_h8 afrag_t[NA];
+  typedef eas_h8 bfrag_t[NB];
   auto read_stage = [&](int kt, afrag_t& fa, bfrag_t& fb) {
     const eas_op_t* as = As + (kt % NSTAGE) * STAGE_A;
     const eas_op_t* bs = Bs + (kt % NSTAGE) * STAGE_B;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int f = 0; f < NA; ++f) fa[f] = *(const eas_h8*)(as + fa_off[f]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) fa[ks][i] = *(const eas_h8*)(as + fa_off[ks][i]);
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][0]));
-        const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[ks][j][1]));
-        const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
-        fb[ks][j] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
-      }
+    for (int f = 0; f < NB; ++f) {
+      const eas_h4t lo = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[f]));
+      const eas_h4t hi = EAS_DS_TR16((EAS_LDS eas_h4t*)(bs + fb_off[f] + 4 * BN));
+      const eas_h4 l4 = __builtin_bit_cast(eas_h4, lo), h4 = __builtin_bit_cast(eas_h4, hi);
+      fb[f] = (eas_h8){l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
     }
   };
   auto mfmas = [&](const afrag_t& fa, const bfrag_t& fb) {
+    if constexpr (MI == 32) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) acc[i][j] = EAS_MFMA32(fa[ks][i], fb[ks][j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < NJ; ++j) acc[i][j] = EAS_MFMA32(fa[2 * ks + i], fb[ks * NJ + j], acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc16[i][j] = EAS_MFMA16(fa[i], fb[j], acc16[i][j], 0, 0, 0);
+    }
   };
   // At the barrier of stage kt the producers' DMA of stage kt+1 has landed; after it the wave
   // issues stage kt's MFMAs from the fragments read one stage earlier and, between them, every
   // fragment read of stage kt+1 into the other set.  After this barrier the producers refill the
   // slot of stage kt-1, whose fragments every consumer read (and used) before it.
   auto step = [&](int kt, const afrag_t& fa, const bfrag_t& fb, afrag_t& na, bfrag_t& nb) {
-    constexpr int NMFMA = 4 * NJ, NREAD = 4 + 4 * NJ;
+    constexpr int NMFMA = MI == 32 ? 4 * NJ : 4 * NB, NREAD = NA + 2 * NB;
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     read_stage(kt + 1, na, nb);
@@ -794,12 +810,11 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
   auto mask_tail = [&](afrag_t& fa) {
     if constexpr (K % 8 != 0) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int f = 0; f < NA; ++f)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const bool past = (KT - 1) * BK + 16 * ks + 8 * (lane >> 5) + e >= K;
-#pragma unroll
-          for (int i = 0; i < 2; ++i) fa[ks][i][e] = past ? (eas_op_t)0.0f : fa[ks][i][e];
+          const int k = (KT - 1) * BK + (MI == 32 ? 16 * (f >> 1) + 8 * (lane >> 5) : 8 * (lane >> 4)) + e;
+          fa[f][e] = k >= K ? (eas_op_t)0.0f : fa[f][e];
         }
     }
   };
@@ -821,17 +836,31 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
     mfmas(a0, b0);
   }
   const bool full = (m0 + BM <= M) && (n0 + BN <= N);
-  // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
+  if constexpr (MI == 32) {
+    // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
+      for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
-        const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
-        if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + wm * 64 + i * 32 + (r / 4) * 8 + (lane >> 5) * 4 + (r % 4);
+          const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+          if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc[i][j][r];
+        }
+  } else {
+    // lane l, register r of a 16x16 tile holds (row 4*(l/16) + r, col l%16)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
+          const int col = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
+          if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc16[i][j][r];
+        }
+  }
 }
 
 // Skinny path (M <= 128, decode-like): one workgroup per NT = 64 columns (128 for launches whose
@@ -1262,7 +1291,7 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__t128(
   int m0, n0;
   eas_tile_origin<128, 128>(M, N, m0, n0);
   if (dma_ok)
-    eas_gemm_t128<CT, K, 128>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
+    eas_gemm_t128<CT, K, 128, @PP_MI@>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
   else
     eas_gemm_elementwise<AT, BT, CT, K, 128>(A, B, C, ldb, M, N, m0, n0);
 }
@@ -1285,7 +1314,7 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__t128x256(
   int m0, n0;
   eas_tile_origin<128, 256>(M, N, m0, n0);
   if (dma_ok)
-    eas_gemm_t128<CT, K, 256>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
+    eas_gemm_t128<CT, K, 256, @PP_MI@>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
   else
     eas_gemm_elementwise<AT, BT, CT, K, 128, 256>(A, B, C, ldb, M, N, m0, n0);
 }
@@ -1676,10 +1705,12 @@ T128_THREADS = 512  # the 128 x 128 and 128 x 256 entries of f16 GEMMs: 4 consum
 F32_THREADS = 512  # both fp32 entries: 4 consumer + 4 producer waves
 SKINNY_M = 128  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
-# MFMA shape of the 8-wave entry's body: 16 (v_mfma_f32_16x16x32, the default) or 32
-# (v_mfma_f32_32x32x16).  Measured on MI355X with random inputs, where the part runs
-# power-limited: 16 x 16 x 32 is 2.5-5 % faster (4096³ f16 1172-1181 -> 1219-1222 TFLOP/s,
-# 8192³ 1271-1277 -> 1331-1335), since it moves fewer accumulator bytes per flop.
+# MFMA shape of the 8-wave and 128-row entries' bodies: 16 (v_mfma_f32_16x16x32, the default) or
+# 32 (v_mfma_f32_32x32x16).  Measured on MI355X with random inputs, where the part runs
+# power-limited: 16 x 16 x 32 is 2.5-5 % faster on the 8-wave entry (4096³ f16 1172-1181 ->
+# 1219-1222 TFLOP/s, 8192³ 1271-1277 -> 1331-1335), since it moves fewer accumulator bytes per
+# flop, and 2.5-4.7 % on the 128 x 128 entry (2048³ 24.32 -> 23.17 µs, 256 x 14336 x 4096
+# 40.96 -> 39.95 µs by rocprof).
 def pp_mfma() -> int:
     """``EAS_HIP_GEMM_MFMA``: 16 (default) or 32, read each time a GEMM source is emitted."""
     v = os.environ.get("EAS_HIP_GEMM_MFMA", "16").strip() or "16"

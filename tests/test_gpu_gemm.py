@@ -261,10 +261,11 @@ def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
 @pytest.mark.parametrize("mnk", [(300, 520, 200), (257, 264, 72), (520, 256, 1000), (130, 260, 4100),
                                  (1024, 1024, 1024)])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-def test_8wave_entry_with_32x32x16_mfma(gpu_runtime, monkeypatch, mnk, dtype):
-    """EAS_HIP_GEMM_MFMA=32: the 8-wave entry's 4 x 2 tiles of v_mfma_f32_32x32x16 per wave, against
-    float64 and against the default 16 x 16 x 32 body on the same launch (same products, other
-    summation order inside an MFMA: equal to f32 rounding)."""
+@pytest.mark.parametrize("choice", ["8wave", "tile128", "tile128x256"])
+def test_entries_with_32x32x16_mfma(gpu_runtime, monkeypatch, mnk, dtype, choice):
+    """EAS_HIP_GEMM_MFMA=32: the 8-wave entry's 4 x 2 tiles of v_mfma_f32_32x32x16 per wave, and the
+    128-row entries' 2 x 2 (2 x 4), against float64 and against the default 16 x 16 x 32 bodies on
+    the same launch (same products, other summation order inside an MFMA: equal to f32 rounding)."""
     import torch
 
     import eas
@@ -279,13 +280,14 @@ def test_8wave_entry_with_32x32x16_mfma(gpu_runtime, monkeypatch, mnk, dtype):
     else:
         da, db = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
         src_kernel = K.matmul_mma_kernel
-    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "8wave")
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
     outs = {}
     for mi in ("32", "16"):
         monkeypatch.setenv("EAS_HIP_GEMM_MFMA", mi)
         kern = eas.kernel(src_kernel.fn)
         ck = kern.compile(da, db, torch.zeros(1, device="cuda"), m, n, BM=32, BN=32, BK=8, K=k, NT=512)
-        assert f"eas_gemm_pp<CT, K, {mi}>" in ck.src
+        assert f"eas_gemm_pp<CT, K, {mi}>" in ck.src and f"eas_gemm_t128<CT, K, 128, {mi}>" in ck.src
+        assert f"eas_gemm_t128<CT, K, 256, {mi}>" in ck.src
         tc = torch.full((m * n,), float("nan"), device="cuda", dtype=torch.float32)
         _mma(kern, da, db, tc, m, n, k)
         torch.cuda.synchronize()
