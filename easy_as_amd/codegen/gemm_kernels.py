@@ -622,10 +622,10 @@ static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict
 // per wave per stage, with the stage offset in soffset, so the loads cost the MFMA waves sharing
 // their SIMDs nothing.  Waves 0-3 consume, 64 x BN/2 each (MI 16: 4 x BN/32 accumulators of
 // 16x16x32; MI 32: 2 x BN/64 of 32x32x16): the fragments of stage kt+1 are read between stage
-// kt's MFMAs.  A load costs the SIMD that
-// issues it tens of clocks of MFMA issue, which in a 4-wave form of this body (each wave loading
-// its quarter of every stage beside 8 MFMAs) was most of the stage.
-template <typename CT, int K, int BN, int MI = 32>
+// kt's MFMAs.  A load costs the SIMD that issues it tens of clocks of MFMA issue, which in a
+// 4-wave form of this body (each wave loading its quarter of every stage beside its MFMAs) was
+// most of the stage.
+template <typename CT, int K, int BN, int MI = 16>
 static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
                                                      eas_op_t* smem) {
