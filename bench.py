@@ -440,18 +440,18 @@ _PHASE_STAMP_WS = (
 
 def _stamped_ws_source(src: str, entry: str) -> str:
     """The generated f16 GEMM source with a stamp buffer appended to ``entry``'s arguments (the
-    128 x 128 or the 128 x 256 entry) and stamps at: entry, start of the K loop (stage 0 landed),
+    128 x 128, 128 x 256 or 128 x 64 entry) and stamps at: entry, start of the K loop (stage 0 landed),
     end of the K loop (last MFMA issued), C stores issued, C stores complete, plus shader clocks
     around the K loop.  Raises if the source does not have the expected shape."""
     src = src.split("\n", 1)[1]  # the eas-launch line describes the unstamped argument list
-    bn = 256 if entry.endswith("__t128x256") else 128
+    bn = 256 if entry.endswith("__t128x256") else 64 if entry.endswith("__t128x64") else 128
     call = "eas_gemm_t128<CT, K, {}, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
     edits = [
-        ("eas_op_t* smem) {\n  static_assert((BN == 128 || BN == 256)",
-         "eas_op_t* smem, unsigned long long* __restrict__ __eas_stamps) {\n  static_assert((BN == 128 || BN == 256)"),
-        ("  auto bsw = [](int r) { return (4 * (r & 3)) ^ (2 * ((r >> 3) & 1)); };\n  if (wave >= 4) {",
-         "  auto bsw = [](int r) { return (4 * (r & 3)) ^ (2 * ((r >> 3) & 1)); };\n  EAS_WS_STAMP(0);\n"
-         "  EAS_WS_XCD();\n  if (wave >= 4) {"),
+        ("eas_op_t* smem) {\n  static_assert((BN == 64 || BN == 128 || BN == 256)",
+         "eas_op_t* smem, unsigned long long* __restrict__ __eas_stamps) {\n"
+         "  static_assert((BN == 64 || BN == 128 || BN == 256)"),
+        ("(2 * ((r >> 3) & 1));\n  };\n  if (wave >= 4) {",
+         "(2 * ((r >> 3) & 1));\n  };\n  EAS_WS_STAMP(0);\n  EAS_WS_XCD();\n  if (wave >= 4) {"),
         ("  __syncthreads();  // stage 0 landed\n  afrag_t a0, a1;\n",
          "  __syncthreads();  // stage 0 landed\n  EAS_WS_STAMP(1);\n  EAS_WS_CLOCK(6);\n  afrag_t a0, a1;\n"),
         ("  } else {\n    mask_tail(a0);\n    mfmas(a0, b0);\n  }\n",
@@ -461,6 +461,7 @@ def _stamped_ws_source(src: str, entry: str) -> str:
          "  __builtin_amdgcn_s_waitcnt(0);\n  EAS_WS_STAMP(4);\n}\n\n// Skinny path"),
         (call.format(128), call.format(128)[:-2] + (", __eas_stamps);" if bn == 128 else ", nullptr);")),
         (call.format(256), call.format(256)[:-2] + (", __eas_stamps);" if bn == 256 else ", nullptr);")),
+        (call.format(64), call.format(64)[:-2] + (", __eas_stamps);" if bn == 64 else ", nullptr);")),
     ]
     for old, new in edits:
         if src.count(old) != 1:
@@ -499,7 +500,7 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
     mod = rt._mod()
     plan = plan_launch(ck, args, grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), compute_units=rt._cus)
     entry = plan.entry or ck.geometry.entry if plan is not None else None
-    ws = entry is not None and (entry.endswith("__t128") or entry.endswith("__t128x256")) and not tiled
+    ws = entry is not None and entry.endswith(("__t128", "__t128x256", "__t128x64")) and not tiled
     if tiled:
         src, per_wg = _stamped_f32_source(ck.src, entry), 1
     elif ws:
@@ -567,8 +568,9 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
         # v_mfma_f32_32x32x2_f32 keeps a SIMD's MFMA pipe 64 clocks; 16 steps of 2 k per stage
         out["mfma_clocks_per_stage"] = 64 * 16 * (4 if entry.endswith("__t128") else 1)
     elif ws:
-        # v_mfma_f32_16x16x32_f16 keeps it 16 clocks; 16 (128 x 128) or 32 (128 x 256) per stage
-        out["mfma_clocks_per_stage"] = 16 * (32 if entry.endswith("__t128x256") else 16)
+        # v_mfma_f32_16x16x32_f16 keeps it 16 clocks; BN / 8 of them per stage (BN = 64, 128, 256)
+        bn = 256 if entry.endswith("__t128x256") else 64 if entry.endswith("__t128x64") else 128
+        out["mfma_clocks_per_stage"] = 16 * bn // 8
     del a, b, c, stamps
     torch.cuda.empty_cache()
     return out

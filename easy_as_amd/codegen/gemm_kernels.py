@@ -12,10 +12,10 @@ entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
   four waves alternate load phases and MFMA phases one barrier apart, each
   wave holding 128 x 64 of the tile (8 x 4 ``v_mfma_f32_16x16x32_f16``
   accumulators; ``EAS_HIP_GEMM_MFMA=32`` selects 4 x 2 of ``32x32x16``).
-* ``<name>__t128`` and ``<name>__t128x256`` (512 threads): the same DMA operands
-  on 128 x 128 and 128 x 256 tiles, for launches whose 256 x 256 grid would leave
-  CUs idle: 4 waves issue the DMA, 4 waves of 64 x 64 (64 x 128) read fragments
-  and run the MFMAs.
+* ``<name>__t128``, ``<name>__t128x256`` and ``<name>__t128x64`` (512 threads):
+  the same DMA operands on 128 x 128, 128 x 256 and 128 x 64 tiles, for launches
+  whose 256 x 256 grid would leave CUs idle: 4 waves issue the DMA, 4 waves of
+  64 x 64 (64 x 128, 64 x 32) read fragments and run the MFMAs.
 * ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
   AGPRs): the skinny path (launches of at most 128 rows), the 4-wave DMA body,
   and the register body; a uniform branch picks one per launch.
@@ -616,9 +616,9 @@ static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict
   }
 }
 
-// 128 x BN tile body (BN = 128 or 256) for launches whose 256 x 256 grid would leave CUs idle:
-// 8 waves (512 threads), specialised like the fp32 entries, on a ring of 4 stages of 8 KB of A
-// and BN / 16 KB of B.  Waves 4-7 produce: the DMA of stage kt+3, 2 A + BN / 64 B loads of 1 KB
+// 128 x BN tile body (BN = 64, 128 or 256) for launches whose 256 x 256 grid would leave CUs
+// idle: 8 waves (512 threads), specialised like the fp32 entries, on a ring of 4 stages of 8 KB
+// of A and BN / 16 KB of B.  Waves 4-7 produce: the DMA of stage kt+3, 2 A + BN / 64 B loads of 1 KB
 // per wave per stage, with the stage offset in soffset, so the loads cost the MFMA waves sharing
 // their SIMDs nothing.  Waves 0-3 consume, 64 x BN/2 each (MI 16: 4 x BN/32 accumulators of
 // 16x16x32; MI 32: 2 x BN/64 of 32x32x16): the fragments of stage kt+1 are read between stage
@@ -629,10 +629,11 @@ template <typename CT, int K, int BN, int MI = 16>
 static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
                                                      eas_op_t* smem) {
-  static_assert((BN == 128 || BN == 256) && (MI == 32 || MI == 16), "128 x 128 or 128 x 256 tiles, 32- or 16-row MFMAs");
+  static_assert((BN == 64 || BN == 128 || BN == 256) && (MI == 32 || MI == 16) && (BN != 64 || MI == 16),
+                "128 x 64, 128 x 128 or 128 x 256 tiles; 32- or 16-row MFMAs (16 on 64 columns)");
   constexpr int BM = 128, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
   constexpr int NJ = BN / 64;               // 32-column accumulators per consumer wave
-  constexpr int NBI = BN / 64;              // B loads per producer wave per stage
+  constexpr int NBI = BN / 64;              // B loads per producer wave per stage (1, 2 or 4)
   constexpr int CH = BN / 8;                // 16-byte chunks per B row
   constexpr int STAGE_A = BM * BK, STAGE_B = BK * BN;  // halves per stage
   constexpr int KLAST = K - (KT - 1) * BK;  // k extent of the last stage
@@ -640,10 +641,14 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
   eas_op_t* Bs = smem + NSTAGE * STAGE_A;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // B's 16-byte chunk of row r is stored at chunk ^ bsw(r): bits 2-3 spread the four rows of a
-  // transposing read over the banks, bit 1 keeps rows 8 apart (the two 16-lane groups of a
-  // half-wave in the 16 x 16 x 32 mapping) apart.  Rows r and r + 4 share the mask.
-  auto bsw = [](int r) { return (4 * (r & 3)) ^ (2 * ((r >> 3) & 1)); };
+  // B's 16-byte chunk of row r is stored at chunk ^ bsw(r).  Rows of 256 or 512 bytes: bits 2-3
+  // spread the four rows of a transposing read over the banks, bit 1 keeps rows 8 apart (the two
+  // 16-lane groups of a half-wave in the 16 x 16 x 32 mapping) apart.  Rows of 128 bytes (two a
+  // bank cycle): 2((r/2)%2) + 4((r/8)%2), as the skinny path's.  In both, rows r and r + 4 of a
+  // transposing read pair (r % 8 < 4) share the mask.
+  auto bsw = [](int r) {
+    return BN == 64 ? 2 * ((r >> 1) & 1) + 4 * ((r >> 3) & 1) : (4 * (r & 3)) ^ (2 * ((r >> 3) & 1));
+  };
   if (wave >= 4) {
     // DMA instructions write 1 KB of a stage each.  A instruction q = 2 pw + i: rows 16q + lane/4,
     // chunk lane%4 stored at chunk ^ ((row/4)%4).  B instruction q = NBI pw + i: rows
@@ -1318,6 +1323,29 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__t128x256(
   else
     eas_gemm_elementwise<AT, BT, CT, K, 128, 256>(A, B, C, ldb, M, N, m0, n0);
 }
+
+extern "C" __global__ __launch_bounds__(512) void @NAME@__t128x64(
+    @PARAMS@) {
+  constexpr int K = @K@;
+  typedef @AT@ AT;
+  typedef @BT@ BT;
+  typedef @CT@ CT;
+  const int ldb = (int)@LDB@;
+  // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
+  const AT* __restrict__ A = @A@ + (size_t)__eas_m_lo * K;
+  const BT* __restrict__ B = @B@ + __eas_n_lo;
+  CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
+  const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
+  __shared__ __attribute__((aligned(1024))) eas_op_t smem[4 * (128 * 32 + 32 * 64)];  // DMA ring 4 x (8 + 4) KB
+  const bool dma_ok = (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
+                      ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
+  int m0, n0;
+  eas_tile_origin<128, 64>(M, N, m0, n0);
+  if (dma_ok)
+    eas_gemm_t128<CT, K, 64, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
+  else
+    eas_gemm_elementwise<AT, BT, CT, K, 128, 64>(A, B, C, ldb, M, N, m0, n0);
+}
 """
 
 # The fp32 entries (the tiled threadgroup kernel lifted to v_mfma_f32_32x32x2_f32) run 8 waves
@@ -1701,7 +1729,7 @@ TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
 PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
-T128_THREADS = 512  # the 128 x 128 and 128 x 256 entries of f16 GEMMs: 4 consumer + 4 producer waves
+T128_THREADS = 512  # the 128-row entries of f16 GEMMs: 4 consumer + 4 producer waves
 F32_THREADS = 512  # both fp32 entries: 4 consumer + 4 producer waves
 SKINNY_M = 128  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
@@ -1774,6 +1802,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "t128_entry": f"{ir.name}__t128" if (pingpong or spec.f32) else None, "f32": spec.f32,
         "t128_threads": F32_THREADS if spec.f32 else T128_THREADS,
         "t128x256_entry": f"{ir.name}__t128x256" if pingpong else None,
+        "t128x64_entry": f"{ir.name}__t128x64" if pingpong else None,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value,
         "op_dtype": "f32" if spec.f32 else spec.op_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

@@ -133,7 +133,8 @@ def _ws_source(m, n, k):
 
 
 @pytest.mark.parametrize("mnk, entry", [((2048, 2048, 2048), "matmul_mma_kernel__t128"),
-                                        ((512, 14336, 1024), "matmul_mma_kernel__t128x256")])
+                                        ((512, 14336, 1024), "matmul_mma_kernel__t128x256"),
+                                        ((1024, 1024, 1024), "matmul_mma_kernel__t128x64")])
 def test_stamped_ws_source_stamps_only_its_entry(mnk, entry):
     from easy_as_amd.runtime.hip import compile_code
     from easy_as_amd.runtime.hip_ext import load_hip_ext
@@ -145,7 +146,7 @@ def test_stamped_ws_source_stamps_only_its_entry(mnk, entry):
         assert src.count(f"EAS_WS_STAMP({slot});") == 1
     assert src.count("EAS_WS_CLOCK(6);") == src.count("EAS_WS_CLOCK(7);") == src.count("EAS_WS_XCD();") == 1
     assert src.count("unsigned long long* __restrict__ __eas_stamps") == 2  # the body and the entry
-    assert src.count(", nullptr);") == 1  # the other 128-row entry passes no stamp buffer
+    assert src.count(", nullptr);") == 2  # the other 128-row entries pass no stamp buffer
     mod = load_hip_ext(require=False)
     if mod is not None:
         assert compile_code(mod, src, ck.ir.name)[:4] == b"\x7fELF"
@@ -156,7 +157,8 @@ def test_stamped_ws_source_stamps_only_its_entry(mnk, entry):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape, workgroups, mfma_clocks", [((2048, 2048, 2048), 256, 256),
-                                                            ((512, 14336, 1024), 224, 512)])
+                                                            ((512, 14336, 1024), 224, 512),
+                                                            ((1024, 1024, 1024), 128, 128)])
 def test_phases_of_the_128_row_entries(monkeypatch, shape, workgroups, mfma_clocks):
     import torch
 

@@ -149,8 +149,8 @@ def test_bf16_mma_host_tensors(gpu_runtime):
 
 @pytest.mark.parametrize("mnk", [(300, 520, 200), (520, 256, 1000), (129, 300, 8)])
 def test_bf16_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
-    """The 8-wave, 128 x 128, 128 x 256 and 4-wave entries run the same bf16 MFMA sequence per
-    output."""
+    """The 8-wave, 128 x 128, 128 x 256, 128 x 64 and 4-wave entries run the same bf16 MFMA sequence
+    per output."""
     from easy_as_amd.runtime.hip import plan_launch
 
     m, n, k = mnk
@@ -159,7 +159,8 @@ def test_bf16_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
                                           NT=512)
     outs = {}
     for choice, entry in (("8wave", "matmul_mma_bf16_kernel__pp"), ("tile128", "matmul_mma_bf16_kernel__t128"),
-                          ("tile128x256", "matmul_mma_bf16_kernel__t128x256"), ("4wave", None)):
+                          ("tile128x256", "matmul_mma_bf16_kernel__t128x256"),
+                          ("tile128x64", "matmul_mma_bf16_kernel__t128x64"), ("4wave", None)):
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
         args = {"a": torch.zeros(m * k, dtype=torch.bfloat16, device="cuda"),
                 "b": torch.zeros(k * n, dtype=torch.bfloat16, device="cuda"),
@@ -168,5 +169,5 @@ def test_bf16_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
         c, ref = _gemm(m, n, k, seed=3)
         _check(c, ref, k, False)
         outs[choice] = c
-    for choice in ("8wave", "tile128", "tile128x256"):
+    for choice in ("8wave", "tile128", "tile128x256", "tile128x64"):
         assert ops.rel_err(outs[choice], outs["4wave"]) <= 1e-6, choice

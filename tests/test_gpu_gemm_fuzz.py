@@ -6,8 +6,9 @@ log scale, so the cases cover:
 * skinny and full-tile launches;
 * odd K (A rows not 4-byte aligned) and K below one stage;
 * N not a multiple of 4, and every entry the launch plan picks by itself;
-* each shape again on the 128 x 128 and 128 x 256-tile entries (``EAS_HIP_GEMM_ENTRY=tile128``,
-  ``tile128x256``), which the plan picks by itself only for launches of more than 128 rows.
+* each shape again on the 128 x 128, 128 x 256 and 128 x 64-tile entries
+  (``EAS_HIP_GEMM_ENTRY=tile128``, ``tile128x256``, ``tile128x64``), which the plan picks by
+  itself only for launches of more than 128 rows.
 
 Every output is checked with the tolerances the parity bars state.  The output buffer is
 longer than M x N, and its tail must keep its sentinel (no write past C)."""
@@ -92,7 +93,7 @@ def test_random_shape_matches_float64(gpu_runtime, monkeypatch, seed):
             return c
     # the entry the launch plan picks, and the 128-row entries on every shape (their edge tiles,
     # K tails and zero-filled stages)
-    for choice in ("auto", "tile128", "tile128x256"):
+    for choice in ("auto", "tile128", "tile128x256", "tile128x64"):
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
         c = run()
         got, tail = c[:m * n], c[m * n:]
