@@ -444,7 +444,9 @@ def _stamped_ws_source(src: str, entry: str) -> str:
     end of the K loop (last MFMA issued), C stores issued, C stores complete, plus shader clocks
     around the K loop.  Raises if the source does not have the expected shape."""
     src = src.split("\n", 1)[1]  # the eas-launch line describes the unstamped argument list
-    bn = 256 if entry.endswith("__t128x256") else 64 if entry.endswith("__t128x64") else 128
+    bm, bn = {"__t128x256": (128, 256), "__t128x64": (128, 64), "__t64x64": (64, 64)}.get(
+        entry[entry.rindex("__"):], (128, 128))
+    t64 = "eas_gemm_t128<CT, K, 64, 16, 64>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
     call = "eas_gemm_t128<CT, K, {}, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
     edits = [
         ("eas_op_t* smem) {\n  static_assert((BN == 64 || BN == 128 || BN == 256)",
@@ -459,9 +461,10 @@ def _stamped_ws_source(src: str, entry: str) -> str:
         ("(CT)acc16[i][j][r];\n        }\n  }\n}\n\n// Skinny path",
          "(CT)acc16[i][j][r];\n        }\n  }\n  EAS_WS_STAMP(3);\n"
          "  __builtin_amdgcn_s_waitcnt(0);\n  EAS_WS_STAMP(4);\n}\n\n// Skinny path"),
-        (call.format(128), call.format(128)[:-2] + (", __eas_stamps);" if bn == 128 else ", nullptr);")),
+        (call.format(128), call.format(128)[:-2] + (", __eas_stamps);" if (bm, bn) == (128, 128) else ", nullptr);")),
         (call.format(256), call.format(256)[:-2] + (", __eas_stamps);" if bn == 256 else ", nullptr);")),
-        (call.format(64), call.format(64)[:-2] + (", __eas_stamps);" if bn == 64 else ", nullptr);")),
+        (call.format(64), call.format(64)[:-2] + (", __eas_stamps);" if bn == 64 and bm == 128 else ", nullptr);")),
+        (t64, t64[:-2] + (", __eas_stamps);" if bm == 64 else ", nullptr);")),
     ]
     for old, new in edits:
         if src.count(old) != 1:
@@ -500,7 +503,7 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
     mod = rt._mod()
     plan = plan_launch(ck, args, grid=(K.cdiv(n, 32), K.cdiv(m, 32), 1), compute_units=rt._cus)
     entry = plan.entry or ck.geometry.entry if plan is not None else None
-    ws = entry is not None and entry.endswith(("__t128", "__t128x256", "__t128x64")) and not tiled
+    ws = entry is not None and entry.endswith(("__t128", "__t128x256", "__t128x64", "__t64x64")) and not tiled
     if tiled:
         src, per_wg = _stamped_f32_source(ck.src, entry), 1
     elif ws:
@@ -568,9 +571,10 @@ def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
         # v_mfma_f32_32x32x2_f32 keeps a SIMD's MFMA pipe 64 clocks; 16 steps of 2 k per stage
         out["mfma_clocks_per_stage"] = 64 * 16 * (4 if entry.endswith("__t128") else 1)
     elif ws:
-        # v_mfma_f32_16x16x32_f16 keeps it 16 clocks; BN / 8 of them per stage (BN = 64, 128, 256)
-        bn = 256 if entry.endswith("__t128x256") else 64 if entry.endswith("__t128x64") else 128
-        out["mfma_clocks_per_stage"] = 16 * bn // 8
+        # v_mfma_f32_16x16x32_f16 keeps it 16 clocks; BM BN / 1024 of them per stage
+        bm, bn = {"__t128x256": (128, 256), "__t128x64": (128, 64), "__t64x64": (64, 64)}.get(
+            entry[entry.rindex("__"):], (128, 128))
+        out["mfma_clocks_per_stage"] = 16 * bm * bn // 1024
     del a, b, c, stamps
     torch.cuda.empty_cache()
     return out

@@ -616,22 +616,24 @@ static __device__ __forceinline__ void eas_gemm_elementwise(const AT* __restrict
   }
 }
 
-// 128 x BN tile body (BN = 64, 128 or 256) for launches whose 256 x 256 grid would leave CUs
-// idle: 8 waves (512 threads), specialised like the fp32 entries, on a ring of 4 stages of 8 KB
-// of A and BN / 16 KB of B.  Waves 4-7 produce: the DMA of stage kt+3, 2 A + BN / 64 B loads of 1 KB
-// per wave per stage, with the stage offset in soffset, so the loads cost the MFMA waves sharing
-// their SIMDs nothing.  Waves 0-3 consume, 64 x BN/2 each (MI 16: 4 x BN/32 accumulators of
-// 16x16x32; MI 32: 2 x BN/64 of 32x32x16): the fragments of stage kt+1 are read between stage
-// kt's MFMAs.  A load costs the SIMD that issues it tens of clocks of MFMA issue, which in a
+// BM x BN tile body (128 x 64, 128 x 128, 128 x 256 or 64 x 64) for launches whose 256 x 256 grid
+// would leave CUs idle: 8 waves (512 threads), specialised like the fp32 entries, on a ring of 4
+// stages of BM / 16 KB of A and BN / 16 KB of B.  Waves 4-7 produce: the DMA of stage kt+3,
+// BM / 64 A + BN / 64 B loads of 1 KB per wave per stage, with the stage offset in soffset, so the
+// loads cost the MFMA waves sharing their SIMDs nothing.  Waves 0-3 consume, BM/2 x BN/2 each
+// (MI 16: BM/32 x BN/32 accumulators of 16x16x32; MI 32: 2 x BN/64 of 32x32x16): the fragments of
+// stage kt+1 are read between stage kt's MFMAs.  A load costs the SIMD that issues it tens of clocks of MFMA issue, which in a
 // 4-wave form of this body (each wave loading its quarter of every stage beside its MFMAs) was
 // most of the stage.
-template <typename CT, int K, int BN, int MI = 16>
+template <typename CT, int K, int BN, int MI = 16, int BM = 128>
 static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict__ A, const eas_op_t* __restrict__ B,
                                                      CT* __restrict__ C, int ldb, int M, int N, int m0, int n0,
                                                      eas_op_t* smem) {
-  static_assert((BN == 64 || BN == 128 || BN == 256) && (MI == 32 || MI == 16) && (BN != 64 || MI == 16),
-                "128 x 64, 128 x 128 or 128 x 256 tiles; 32- or 16-row MFMAs (16 on 64 columns)");
-  constexpr int BM = 128, BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
+  static_assert((BN == 64 || BN == 128 || BN == 256) && (MI == 32 || MI == 16) && (BN != 64 || MI == 16) &&
+                    (BM == 128 || (BM == 64 && BN == 64)),
+                "128 x 64, 128 x 128, 128 x 256 or 64 x 64 tiles; 32- or 16-row MFMAs (16 on 64 columns)");
+  constexpr int BK = 32, NSTAGE = 4, KT = (K + BK - 1) / BK;
+  constexpr int NAI = BM / 64;              // A loads per producer wave per stage (1 or 2)
   constexpr int NJ = BN / 64;               // 32-column accumulators per consumer wave
   constexpr int NBI = BN / 64;              // B loads per producer wave per stage (1, 2 or 4)
   constexpr int CH = BN / 8;                // 16-byte chunks per B row
@@ -663,10 +665,10 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
     const eas_rsrc ra = eas_make_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
     const eas_rsrc rb = eas_make_rsrc(B, ((uint32_t)(K - 1) * (uint32_t)ldb + (uint32_t)N) * 2u);
     const uint32_t lds_a = (uint32_t)(size_t)(EAS_LDS eas_op_t*)As, lds_b = (uint32_t)(size_t)(EAS_LDS eas_op_t*)Bs;
-    uint32_t a_off[2], a_tail[2], b_raw[NBI], b_off[NBI], b_tail[NBI];
+    uint32_t a_off[NAI], a_tail[NAI], b_raw[NBI], b_off[NBI], b_tail[NBI];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int q = pw * 2 + i;
+    for (int i = 0; i < NAI; ++i) {
+      const int q = pw * NAI + i;
       const int r_a = 16 * q + (lane >> 2);
       const int c_a = (lane & 3) ^ ((r_a >> 2) & 3);
       const uint32_t a_raw = ((uint32_t)(m0 + r_a) * (uint32_t)K + (uint32_t)(c_a * 8)) * 2u;
@@ -687,8 +689,8 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
       const uint32_t st_b = lds_b + (uint32_t)((kt % NSTAGE) * STAGE_B * 2);
       const uint32_t sa = (uint32_t)(kt * BK * 2), sb = (uint32_t)(kt * BK * 2) * (uint32_t)ldb;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const uint32_t dst = st_a + (uint32_t)((pw * 2 + i) * 1024);
+      for (int i = 0; i < NAI; ++i) {
+        const uint32_t dst = st_a + (uint32_t)((pw * NAI + i) * 1024);
         if (kt >= KT)
           eas_dma16s(ra, 0x80000000u, 0u, dst);
         else if (K % BK != 0 && kt == KT - 1)
@@ -711,7 +713,7 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
     };
     // one barrier per stage, as many as the consumers
     auto produce = [&](auto b_fast) {
-      constexpr int PER = 2 + NBI;  // loads per stage
+      constexpr int PER = NAI + NBI;  // loads per stage
 #pragma unroll
       for (int p = 0; p < NSTAGE - 1; ++p) dma(p, b_fast);
       __builtin_amdgcn_s_waitcnt(EAS_WAITVM(2 * PER));  // stage 0 landed (stages 1 and 2 may be in flight)
@@ -735,11 +737,11 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
   // ks NJ + j holds B[k 16 ks + 8(l/32)..+7][col 32 j + l%32]; MI 16 (v_mfma_f32_16x16x32): A f = i
   // holds A[row 16 i + l%16][k 8(l/16)..+7], B f = j holds B[k 8(l/16)..+7][col 16 j + l%16]
   // (rows and columns within the wave's 64 x BN/2).
-  constexpr int NA = 4, NB = BN / 32;
+  constexpr int NA = MI == 32 ? 4 : BM / 32, NB = BN / 32;  // MI 16: BM / 32 row tiles of 16 per wave
   int fa_off[NA], fb_off[NB];
 #pragma unroll
   for (int f = 0; f < NA; ++f) {
-    const int r = MI == 32 ? wm * 64 + (f & 1) * 32 + (lane & 31) : wm * 64 + f * 16 + (lane & 15);
+    const int r = MI == 32 ? wm * 64 + (f & 1) * 32 + (lane & 31) : wm * (BM / 2) + f * 16 + (lane & 15);
     const int c = MI == 32 ? (2 * (f >> 1) + (lane >> 5)) : (lane >> 4);
     fa_off[f] = r * BK + ((c ^ ((r >> 2) & 3)) * 8);
   }
@@ -754,13 +756,13 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
     fb_off[f] = row * BN + ((col >> 3) ^ bsw(row)) * 8 + (col & 7);
   }
   eas_f32x16 acc[2][NJ];      // MI 32: [i][j] tiles of 32 x 32
-  eas_f32x4 acc16[4][NB];     // MI 16: [i][j] tiles of 16 x 16
+  eas_f32x4 acc16[NA][NB];    // MI 16: [i][j] tiles of 16 x 16
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = (eas_f32x16){};
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NA; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc16[i][j] = (eas_f32x4){};
   typedef eas_h8 afrag_t[NA];
@@ -788,7 +790,7 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
           for (int j = 0; j < NJ; ++j) acc[i][j] = EAS_MFMA32(fa[2 * ks + i], fb[ks * NJ + j], acc[i][j], 0, 0, 0);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < NA; ++i)
 #pragma unroll
         for (int j = 0; j < NB; ++j) acc16[i][j] = EAS_MFMA16(fa[i], fb[j], acc16[i][j], 0, 0, 0);
     }
@@ -798,7 +800,7 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
   // fragment read of stage kt+1 into the other set.  After this barrier the producers refill the
   // slot of stage kt-1, whose fragments every consumer read (and used) before it.
   auto step = [&](int kt, const afrag_t& fa, const bfrag_t& fb, afrag_t& na, bfrag_t& nb) {
-    constexpr int NMFMA = MI == 32 ? 4 * NJ : 4 * NB, NREAD = NA + 2 * NB;
+    constexpr int NMFMA = MI == 32 ? 4 * NJ : NA * NB, NREAD = NA + 2 * NB;
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     read_stage(kt + 1, na, nb);
@@ -856,12 +858,12 @@ static __device__ __forceinline__ void eas_gemm_t128(const eas_op_t* __restrict_
   } else {
     // lane l, register r of a 16x16 tile holds (row 4*(l/16) + r, col l%16)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NA; ++i)
 #pragma unroll
       for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
+          const int row = m0 + wm * (BM / 2) + i * 16 + (lane >> 4) * 4 + r;
           const int col = n0 + wn * (BN / 2) + j * 16 + (lane & 15);
           if (full || (row < M && col < N)) C[(size_t)row * ldb + col] = (CT)acc16[i][j][r];
         }
@@ -1346,6 +1348,29 @@ extern "C" __global__ __launch_bounds__(512) void @NAME@__t128x64(
   else
     eas_gemm_elementwise<AT, BT, CT, K, 128, 64>(A, B, C, ldb, M, N, m0, n0);
 }
+
+extern "C" __global__ __launch_bounds__(512) void @NAME@__t64x64(
+    @PARAMS@) {
+  constexpr int K = @K@;
+  typedef @AT@ AT;
+  typedef @BT@ BT;
+  typedef @CT@ CT;
+  const int ldb = (int)@LDB@;
+  // the launch rectangle [m_lo, m_hi) x [n_lo, n_hi), moved to the origin
+  const AT* __restrict__ A = @A@ + (size_t)__eas_m_lo * K;
+  const BT* __restrict__ B = @B@ + __eas_n_lo;
+  CT* __restrict__ C = @C@ + (size_t)__eas_m_lo * ldb + __eas_n_lo;
+  const int M = (int)(__eas_m_hi - __eas_m_lo), N = (int)(__eas_n_hi - __eas_n_lo);
+  __shared__ __attribute__((aligned(1024))) eas_op_t smem[4 * (64 * 32 + 32 * 64)];  // DMA ring 4 x (4 + 4) KB
+  const bool dma_ok = (K % 2 == 0) && (ldb % 2 == 0) && ((((uint64_t)A) | ((uint64_t)B)) % 4 == 0) &&
+                      ((uint64_t)M * K * 2 < (1ull << 31)) && (((uint64_t)(K - 1) * ldb + N) * 2 < (1ull << 31));
+  int m0, n0;
+  eas_tile_origin<64, 64>(M, N, m0, n0);
+  if (dma_ok)
+    eas_gemm_t128<CT, K, 64, 16, 64>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);
+  else
+    eas_gemm_elementwise<AT, BT, CT, K, 64, 64>(A, B, C, ldb, M, N, m0, n0);
+}
 """
 
 # The fp32 entries (the tiled threadgroup kernel lifted to v_mfma_f32_32x32x2_f32) run 8 waves
@@ -1803,6 +1828,7 @@ def emit_gemm(ir: IRModule, block: int, spec: GemmSpec) -> Lowered:
         "t128_threads": F32_THREADS if spec.f32 else T128_THREADS,
         "t128x256_entry": f"{ir.name}__t128x256" if pingpong else None,
         "t128x64_entry": f"{ir.name}__t128x64" if pingpong else None,
+        "t64_entry": f"{ir.name}__t64x64" if pingpong else None,
         "a": spec.a, "b": spec.b, "c": spec.c, "out_dtype": spec.c_dtype.value,
         "op_dtype": "f32" if spec.f32 else spec.op_dtype.value})
     return Lowered(PRELUDE + header + src, block, "thread", geo)

@@ -1036,6 +1036,7 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
     tiles128 = -(-m // 128) * -(-n // 128)
     tiles128x256 = -(-m // 128) * -(-n // 256)
     tiles128x64 = -(-m // 128) * -(-n // 64)
+    tiles64 = -(-m // 64) * -(-n // 64)
     choice = _gemm_entry_choice()
     if m <= p.get("skinny_m", 0):
         # The 4-wave entry runs its skinny path for every launch of at most skinny_m rows (one
@@ -1057,6 +1058,8 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
             elif choice == "tile128x64":
                 other = LaunchPlan((tiles128x64, 1, 1), (p["t128_threads"], 1, 1), hidden,
                                    entry=p["t128x64_entry"])
+            elif choice == "tile64":
+                other = LaunchPlan((tiles64, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t64_entry"])
             elif choice == "8wave":
                 other = LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
         return other or LaunchPlan((groups, 1, 1), (p["threads"], 1, 1), hidden)
@@ -1069,26 +1072,29 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
     if p.get("pp_entry") and choice != "4wave" and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
         # When 256 x 256 tiles would fill at most half of the CUs: 128 x 128 tiles if they take one
         # round of CUs, else 128 x 256 ones (at most twice the 256 x 256 count, so one round too);
-        # 128 x 64 ones if even 128 x 128 would fill at most half of the CUs
+        # 64 x 64 ones if even 128 x 128 would fill at most half of the CUs (128 x 64 measured
+        # between the two, so the plan leaves it to EAS_HIP_GEMM_ENTRY)
         small = choice == "auto" and 2 * tiles <= compute_units
         if choice == "tile128x256" or (small and tiles128 > compute_units):
             return LaunchPlan((tiles128x256, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128x256_entry"])
-        if choice == "tile128x64" or (small and 2 * tiles128 <= compute_units):
+        if choice == "tile128x64":
             return LaunchPlan((tiles128x64, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128x64_entry"])
+        if choice == "tile64" or (small and 2 * tiles128 <= compute_units):
+            return LaunchPlan((tiles64, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t64_entry"])
         if choice == "tile128" or small:
             return LaunchPlan((tiles128, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128_entry"])
         return LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])
     return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
 
 
-_ENTRY_CHOICES = ("auto", "8wave", "tile128", "tile128x256", "tile128x64", "4wave")
+_ENTRY_CHOICES = ("auto", "8wave", "tile128", "tile128x256", "tile128x64", "tile64", "4wave")
 SKINNY_CUT = 16  # up to this many rows a launch always takes the skinny path
 WIDE_M = 128  # up to this many rows the skinny path may take 128 columns per workgroup
 
 
 def _gemm_entry_choice() -> str:
     """``EAS_HIP_GEMM_ENTRY``: ``auto`` (default), or one entry for every f16 launch
-    the DMA takes: ``8wave``, ``tile128``, ``tile128x256``, ``tile128x64`` or ``4wave``."""
+    the DMA takes: ``8wave``, ``tile128``, ``tile128x256``, ``tile128x64``, ``tile64`` or ``4wave``."""
     v = os.environ.get("EAS_HIP_GEMM_ENTRY", "auto").strip().lower() or "auto"
     if v not in _ENTRY_CHOICES:
         raise ValueError(f"EAS_HIP_GEMM_ENTRY must be one of {_ENTRY_CHOICES}, got {v!r}")

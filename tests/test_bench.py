@@ -134,7 +134,7 @@ def _ws_source(m, n, k):
 
 @pytest.mark.parametrize("mnk, entry", [((2048, 2048, 2048), "matmul_mma_kernel__t128"),
                                         ((512, 14336, 1024), "matmul_mma_kernel__t128x256"),
-                                        ((1024, 1024, 1024), "matmul_mma_kernel__t128x64")])
+                                        ((1024, 1024, 1024), "matmul_mma_kernel__t64x64")])
 def test_stamped_ws_source_stamps_only_its_entry(mnk, entry):
     from easy_as_amd.runtime.hip import compile_code
     from easy_as_amd.runtime.hip_ext import load_hip_ext
@@ -146,7 +146,7 @@ def test_stamped_ws_source_stamps_only_its_entry(mnk, entry):
         assert src.count(f"EAS_WS_STAMP({slot});") == 1
     assert src.count("EAS_WS_CLOCK(6);") == src.count("EAS_WS_CLOCK(7);") == src.count("EAS_WS_XCD();") == 1
     assert src.count("unsigned long long* __restrict__ __eas_stamps") == 2  # the body and the entry
-    assert src.count(", nullptr);") == 2  # the other 128-row entries pass no stamp buffer
+    assert src.count(", nullptr);") == 3  # the other tile entries pass no stamp buffer
     mod = load_hip_ext(require=False)
     if mod is not None:
         assert compile_code(mod, src, ck.ir.name)[:4] == b"\x7fELF"
@@ -158,7 +158,7 @@ def test_stamped_ws_source_stamps_only_its_entry(mnk, entry):
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape, workgroups, mfma_clocks", [((2048, 2048, 2048), 256, 256),
                                                             ((512, 14336, 1024), 224, 512),
-                                                            ((1024, 1024, 1024), 128, 128)])
+                                                            ((1024, 1024, 1024), 256, 64)])
 def test_phases_of_the_128_row_entries(monkeypatch, shape, workgroups, mfma_clocks):
     import torch
 
@@ -169,7 +169,7 @@ def test_phases_of_the_128_row_entries(monkeypatch, shape, workgroups, mfma_cloc
     ph = bench._gemm_phases("mma", get_runtime("hip"), torch, trials=2, lead=3)
     assert ph["workgroups"] == workgroups and ph["mfma_clocks_per_stage"] == mfma_clocks
     assert 0 < ph["prologue"] < ph["loop_median"] < ph["end_median"] <= ph["end_last"] < 1000
-    assert mfma_clocks <= ph["loop_clocks_per_stage"] < 8 * mfma_clocks
+    assert mfma_clocks <= ph["loop_clocks_per_stage"] < max(8 * mfma_clocks, 1024)
     assert 0.5 < ph["loop_shader_GHz"] < 3.0
 
 

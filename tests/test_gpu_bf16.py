@@ -160,7 +160,8 @@ def test_bf16_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
     outs = {}
     for choice, entry in (("8wave", "matmul_mma_bf16_kernel__pp"), ("tile128", "matmul_mma_bf16_kernel__t128"),
                           ("tile128x256", "matmul_mma_bf16_kernel__t128x256"),
-                          ("tile128x64", "matmul_mma_bf16_kernel__t128x64"), ("4wave", None)):
+                          ("tile128x64", "matmul_mma_bf16_kernel__t128x64"),
+                          ("tile64", "matmul_mma_bf16_kernel__t64x64"), ("4wave", None)):
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
         args = {"a": torch.zeros(m * k, dtype=torch.bfloat16, device="cuda"),
                 "b": torch.zeros(k * n, dtype=torch.bfloat16, device="cuda"),
@@ -169,5 +170,5 @@ def test_bf16_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
         c, ref = _gemm(m, n, k, seed=3)
         _check(c, ref, k, False)
         outs[choice] = c
-    for choice in ("8wave", "tile128", "tile128x256", "tile128x64"):
+    for choice in ("8wave", "tile128", "tile128x256", "tile128x64", "tile64"):
         assert ops.rel_err(outs[choice], outs["4wave"]) <= 1e-6, choice

@@ -241,7 +241,7 @@ def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
     outs = {}
     for choice, entry in (("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128"),
                           ("tile128x256", "matmul_mma_kernel__t128x256"), ("tile128x64", "matmul_mma_kernel__t128x64"),
-                          ("4wave", None)):
+                          ("tile64", "matmul_mma_kernel__t64x64"), ("4wave", None)):
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
         assert plan_launch(ck, args, grid=K.mma_grid({"BM": 32, "BN": 32}, args)).entry == entry
         c = np.full(m * n, np.nan, np.float32)
@@ -251,7 +251,7 @@ def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
     # the same MFMA sequence per output element: equal up to f32 rounding (at most 128 rows the
     # 4-wave entry runs the skinny path, whose waves split K: another summation order)
     tol = 1e-6 if m > 128 else 1e-5 * math.sqrt(k)
-    for choice in ("8wave", "tile128", "tile128x256", "tile128x64"):
+    for choice in ("8wave", "tile128", "tile128x256", "tile128x64", "tile64"):
         assert ops.rel_err(outs[choice], outs["4wave"]) <= tol, choice
     if m <= 128 and -(-n // 64) > 256:  # more 64-column groups than CUs: 128-column skinny groups
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "auto")
@@ -299,7 +299,8 @@ def test_entries_with_32x32x16_mfma(gpu_runtime, monkeypatch, mnk, dtype, choice
 
 @pytest.mark.parametrize("choice,entry", [("8wave", "matmul_mma_kernel__pp"), ("tile128", "matmul_mma_kernel__t128"),
                                           ("tile128x256", "matmul_mma_kernel__t128x256"),
-                                          ("tile128x64", "matmul_mma_kernel__t128x64")])
+                                          ("tile128x64", "matmul_mma_kernel__t128x64"),
+                                          ("tile64", "matmul_mma_kernel__t64x64")])
 def test_dma_entry_guard_for_an_operand_it_cannot_see(gpu_runtime, monkeypatch, choice, entry):
     """An eas.Tensor viewing torch memory at a 2-byte offset: the plan cannot see the address,
     picks a DMA entry, and the entry's own check sends the launch to its element-wise guard.
@@ -346,13 +347,13 @@ _BASELINE_SHAPES = [
 
 
 # LLM-linear shapes on each entry the launch plan picks by itself (which one is asserted), every
-# output checked the same way: 128 x 256, 128 x 128 and 128 x 64 tiles, 128-column skinny groups
+# output checked the same way: 128 x 256, 128 x 128 and 64 x 64 tiles, 128-column skinny groups
 # (2 and 8 row tiles), and the 128-tile entry for a launch of more than 16 rows too wide for one
 # round of 128-column groups.
 _PLAN_SHAPES = [
     ("matmul_mma_kernel", 512, 14336, 1024, "f16", "n1", "n02", False, "__t128x256"),
     ("matmul_mma_kernel", 2048, 2048, 2048, "f16", "u", "u", False, "__t128"),
-    ("matmul_mma_kernel", 1024, 1024, 1024, "f16", "u", "u", False, "__t128x64"),
+    ("matmul_mma_kernel", 1024, 1024, 1024, "f16", "u", "u", False, "__t64x64"),
     ("matmul_mma_f16out_kernel", 48, 28672, 2048, "f16", "n1", "n02", True, ""),
     ("matmul_mma_f16out_kernel", 128, 28672, 1024, "f16", "n1", "n02", True, ""),
     ("matmul_mma_f16out_kernel", 100, 40960, 512, "f16", "n1", "n02", True, "__t128"),

@@ -93,7 +93,7 @@ def test_random_shape_matches_float64(gpu_runtime, monkeypatch, seed):
             return c
     # the entry the launch plan picks, and the 128-row entries on every shape (their edge tiles,
     # K tails and zero-filled stages)
-    for choice in ("auto", "tile128", "tile128x256", "tile128x64"):
+    for choice in ("auto", "tile128", "tile128x256", "tile128x64", "tile64"):
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
         c = run()
         got, tail = c[:m * n], c[m * n:]

@@ -225,9 +225,9 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, 300, 520, BM=32, BN=32, BK=8, K=200, NT=512)
     assert ck.geometry.kind == "gemm"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(17, 10, 1))
-    # 6 tiles of 256 x 256, or 15 of 128 x 128, would leave CUs idle: 3 x 9 tiles of 128 x 64
-    assert plan.hidden == (0, 300, 0, 520) and plan.grid == (3 * 9, 1, 1)
-    assert plan.block == (512, 1, 1) and plan.entry == "matmul_mma_kernel__t128x64"
+    # 6 tiles of 256 x 256, or 15 of 128 x 128, would leave CUs idle: 5 x 9 tiles of 64 x 64
+    assert plan.hidden == (0, 300, 0, 520) and plan.grid == (5 * 9, 1, 1)
+    assert plan.block == (512, 1, 1) and plan.entry == "matmul_mma_kernel__t64x64"
     plan = plan_launch(ck, {"M": 300, "N": 520}, grid=(3, 2, 1))  # partial grid: 64 x 96 rectangle
     assert plan.hidden == (0, 64, 0, 96) and plan.grid == (2, 1, 1)  # 64 rows: skinny, 64 columns per workgroup
     # M <= 128 (decode-like): one workgroup per 64 columns, on the 4-wave entry
@@ -256,11 +256,11 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
 @pytest.mark.parametrize("mn,entry,grid", [((4096, 4096), "__pp", 256), ((3072, 3072), "__pp", 144),
                                            ((2560, 2560), "__t128x256", 200), ((2048, 2048), "__t128", 256),
                                            ((512, 14336), "__t128x256", 224), ((256, 14336), "__t128", 224),
-                                           ((1536, 1536), "__t128", 144), ((1024, 1024), "__t128x64", 128),
+                                           ((1536, 1536), "__t128", 144), ((1024, 1024), "__t64x64", 256),
                                            ((8192, 8192), "__pp", 1024)])
 def test_plan_tile_size_follows_the_cu_count(mn, entry, grid):
     # 256 x 256 tiles unless they would fill at most half of the 256 CUs; then 128 x 128 tiles if
-    # they take one round of CUs, else 128 x 256, and 128 x 64 if 128 x 128 would fill at most half
+    # they take one round of CUs, else 128 x 256, and 64 x 64 if 128 x 128 would fill at most half
     m, n = mn
     f16, f32 = np.zeros(1, np.float16), np.zeros(1, np.float32)
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, m, n, BM=32, BN=32, BK=8, K=64, NT=512)
@@ -325,8 +325,10 @@ def test_plan_dma_entries_only_for_operands_the_dma_takes(monkeypatch):
     assert plan_launch(ck, args, grid=(16, 16, 1)).entry is None
     monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "tile128x64")
     assert plan_launch(ck, args, grid=(16, 16, 1)).entry == "matmul_mma_kernel__t128x64"
-    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "auto")  # 512 x 512: 16 tiles of 128 x 128, so 128 x 64
-    assert plan_launch(ck, args, grid=(16, 16, 1)).entry == "matmul_mma_kernel__t128x64"
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "tile64")
+    assert plan_launch(ck, args, grid=(16, 16, 1)).entry == "matmul_mma_kernel__t64x64"
+    monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "auto")  # 512 x 512: 16 tiles of 128 x 128, so 64 x 64
+    assert plan_launch(ck, args, grid=(16, 16, 1)).entry == "matmul_mma_kernel__t64x64"
     monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", "fastest")
     with pytest.raises(ValueError):
         plan_launch(ck, args, grid=(16, 16, 1))
