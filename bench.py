@@ -426,9 +426,9 @@ def _stamped_f32_source(src: str, entry: str) -> str:
     return _PHASE_STAMP_F32 + src[:start] + body + src[end:]
 
 
-# The f16 128-row entries (128 x 128 and 128 x 256): the same stamps as the fp32 entries, written
-# by lane 0 of consumer wave 0, inside the body both entries share; the entry not measured passes
-# a null stamp pointer.
+# The f16 smaller-tile entries (128 x 128, 128 x 256, 64 x 64, 128 x 64): the same stamps as the
+# fp32 entries, written by lane 0 of consumer wave 0, inside the body they share; the entries not
+# measured pass a null stamp pointer.
 _PHASE_STAMP_WS = (
     "#define EAS_WS_STAMP(slot) do { if (__eas_stamps && threadIdx.x == 0) "
     "__eas_stamps[blockIdx.x * 8u + (slot)] = __builtin_amdgcn_s_memrealtime(); } while (0)\n"
@@ -477,12 +477,12 @@ def _stamped_ws_source(src: str, entry: str) -> str:
 
 
 def _gemm_phases(name: str, rt, torch, trials: int = 5, lead: int = 20) -> dict:
-    """Per-phase time budget of one launch of the 8-wave GEMM entry, of either f16 128-row entry,
+    """Per-phase time budget of one launch of the 8-wave GEMM entry, of an f16 smaller-tile entry,
     or of either fp32 entry, on the configuration's seeded inputs: after settling, ``trials`` times
     run ``lead`` launches back to back and one more, and read the last launch's stamps.  Medians
     over the trials of: spread of workgroup starts, prologue, K loop (median, min, max over wave
     groups, median per XCD), C store issue, store completion, median and last end; all in
-    microseconds from the first workgroup's start.  The fp32 and 128-row entries add the K loop's
+    microseconds from the first workgroup's start.  The fp32 and smaller-tile entries add the K loop's
     shader clocks per BK = 32 stage and the shader clock they imply."""
     import kernels as K
     from easy_as_amd.runtime.hip import compile_code, plan_launch, struct
@@ -913,9 +913,9 @@ def main() -> int:
                    help="matmul workloads only: M,N,K instead of the configuration's shape (a scaling study, "
                         "not the metric)")
     p.add_argument("--phases", action="store_true",
-                   help="matmul workloads on the 8-wave GEMM entry, an f16 128-row entry or an fp32 entry: "
+                   help="matmul workloads on the 8-wave GEMM entry, an f16 smaller-tile entry or an fp32 entry: "
                         "add an in-kernel per-phase time budget of one launch (a stamped copy of the kernel, "
-                        "timed after the measurement; the 128-row and fp32 entries also give shader clocks "
+                        "timed after the measurement; the smaller-tile and fp32 entries also give shader clocks "
                         "per K stage)")
     p.add_argument("--data", choices=MATMUL_DATA, default="seeded",
                    help="matmul workloads only: input data (anything but 'seeded' is not the metric's data)")

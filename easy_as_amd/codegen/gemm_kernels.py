@@ -600,7 +600,7 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
   }
 }
 
-// Guard body of the 8-wave and 128-row entries for inputs the DMA cannot take (the launch plan
+// Guard body of the 8-wave and smaller-tile entries for inputs the DMA cannot take (the launch plan
 // sends those to the 4-wave entry; this path only keeps a mistaken plan correct): one f32 dot
 // product per element of the TM x TN tile.
 template <typename AT, typename BT, typename CT, int K, int TM = 256, int TN = TM>
@@ -1754,11 +1754,11 @@ TILE = (256, 256)  # BM, BN
 TILE_F32 = (64, 64)
 THREADS = 256
 PP_THREADS = 512  # the 8-wave (ping-pong) entry of f16 GEMMs
-T128_THREADS = 512  # the 128-row entries of f16 GEMMs: 4 consumer + 4 producer waves
+T128_THREADS = 512  # the smaller-tile entries of f16 GEMMs: 4 consumer + 4 producer waves
 F32_THREADS = 512  # both fp32 entries: 4 consumer + 4 producer waves
 SKINNY_M = 128  # launches of at most this many rows run the skinny path: one workgroup per SKINNY_N columns
 SKINNY_N = 64
-# MFMA shape of the 8-wave and 128-row entries' bodies: 16 (v_mfma_f32_16x16x32, the default) or
+# MFMA shape of the 8-wave and smaller-tile entries' bodies: 16 (v_mfma_f32_16x16x32, the default) or
 # 32 (v_mfma_f32_32x32x16).  Measured on MI355X with random inputs, where the part runs
 # power-limited: 16 x 16 x 32 is 2.5-5 % faster on the 8-wave entry (4096³ f16 1172-1181 ->
 # 1219-1222 TFLOP/s, 8192³ 1271-1277 -> 1331-1335), since it moves fewer accumulator bytes per

@@ -197,7 +197,7 @@ def test_mma_kernel_lowers_to_mfma():
     ck = K.matmul_mma_kernel.compile(_h(64 * 64), _h(64 * 64), _f(64 * 64), 64, 64, BM=32, BN=32, BK=8, K=64,
                                      NT=512)
     assert "__builtin_amdgcn_mfma_f32_32x32x16_f16" in ck.src
-    # the 8-wave and 128-row entries' bodies run 16 x 16 x 32 MFMAs unless EAS_HIP_GEMM_MFMA=32 asks
+    # the 8-wave and smaller-tile entries' bodies run 16 x 16 x 32 MFMAs unless EAS_HIP_GEMM_MFMA=32 asks
     # otherwise
     assert "__builtin_amdgcn_mfma_f32_16x16x32_f16" in ck.src
     assert "eas_gemm_pp<CT, K, 16>" in ck.src and "eas_gemm_t128<CT, K, 128, 16>" in ck.src

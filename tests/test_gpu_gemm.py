@@ -265,7 +265,7 @@ def test_gemm_entries_agree(gpu_runtime, monkeypatch, mnk):
 @pytest.mark.parametrize("choice", ["8wave", "tile128", "tile128x256"])  # 128 x 64 is 16 x 16 x 32 only
 def test_entries_with_32x32x16_mfma(gpu_runtime, monkeypatch, mnk, dtype, choice):
     """EAS_HIP_GEMM_MFMA=32: the 8-wave entry's 4 x 2 tiles of v_mfma_f32_32x32x16 per wave, and the
-    128-row entries' 2 x 2 (2 x 4), against float64 and against the default 16 x 16 x 32 bodies on
+    128 x 128 and 128 x 256 entries' 2 x 2 (2 x 4), against float64 and against the default 16 x 16 x 32 bodies on
     the same launch (same products, other summation order inside an MFMA: equal to f32 rounding)."""
     import torch
 

@@ -91,7 +91,7 @@ def test_random_shape_matches_float64(gpu_runtime, monkeypatch, seed):
             c = np.full(m * n + PAD, np.nan, np.float16 if out16 else np.float32)
             kern(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512, _grid=K.mma_grid, _tptg=(512, 1, 1))
             return c
-    # the entry the launch plan picks, and the 128-row entries on every shape (their edge tiles,
+    # the entry the launch plan picks, and the smaller-tile entries on every shape (their edge tiles,
     # K tails and zero-filled stages)
     for choice in ("auto", "tile128", "tile128x256", "tile128x64", "tile64"):
         monkeypatch.setenv("EAS_HIP_GEMM_ENTRY", choice)
