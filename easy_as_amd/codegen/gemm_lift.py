@@ -1071,16 +1071,17 @@ def plan_gemm(geo: Any, groups: tuple[int, int, int], runtime_args: Any, live_x:
         return LaunchPlan((tiles, 1, 1), (p["threads"], 1, 1), hidden)
     if p.get("pp_entry") and choice != "4wave" and _dma_fits(p, runtime_args, K, ldb, m, n_lo, n):
         # When 256 x 256 tiles would fill at most half of the CUs: 128 x 128 tiles if they take one
-        # round of CUs, else 128 x 256 ones (at most twice the 256 x 256 count, so one round too);
-        # 64 x 64 ones if even 128 x 128 would fill at most half of the CUs (128 x 64 measured
-        # between the two, so the plan leaves it to EAS_HIP_GEMM_ENTRY)
+        # round of CUs, else 128 x 256 ones (at most twice the 256 x 256 count, so one round too).
+        # If even 128 x 128 would fill at most half of the CUs: 64 x 64 tiles while they need at most
+        # 1.75 rounds of CUs, else 128 x 64 (twice the 128 x 128 count: one round).
         small = choice == "auto" and 2 * tiles <= compute_units
         if choice == "tile128x256" or (small and tiles128 > compute_units):
             return LaunchPlan((tiles128x256, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128x256_entry"])
-        if choice == "tile128x64":
-            return LaunchPlan((tiles128x64, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128x64_entry"])
-        if choice == "tile64" or (small and 2 * tiles128 <= compute_units):
+        tiny = small and 2 * tiles128 <= compute_units
+        if choice == "tile64" or (tiny and 4 * tiles64 <= 7 * compute_units):
             return LaunchPlan((tiles64, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t64_entry"])
+        if choice == "tile128x64" or tiny:
+            return LaunchPlan((tiles128x64, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128x64_entry"])
         if choice == "tile128" or small:
             return LaunchPlan((tiles128, 1, 1), (p["t128_threads"], 1, 1), hidden, entry=p["t128_entry"])
         return LaunchPlan((tiles, 1, 1), (p["pp_threads"], 1, 1), hidden, entry=p["pp_entry"])

@@ -257,10 +257,12 @@ def test_plan_lifted_gemm_covers_the_reference_rectangle():
                                            ((2560, 2560), "__t128x256", 200), ((2048, 2048), "__t128", 256),
                                            ((512, 14336), "__t128x256", 224), ((256, 14336), "__t128", 224),
                                            ((1536, 1536), "__t128", 144), ((1024, 1024), "__t64x64", 256),
+                                           ((1280, 1280), "__t64x64", 400), ((2048, 1024), "__t128x64", 256),
                                            ((8192, 8192), "__pp", 1024)])
 def test_plan_tile_size_follows_the_cu_count(mn, entry, grid):
     # 256 x 256 tiles unless they would fill at most half of the 256 CUs; then 128 x 128 tiles if
-    # they take one round of CUs, else 128 x 256, and 64 x 64 if 128 x 128 would fill at most half
+    # they take one round of CUs, else 128 x 256; if 128 x 128 would fill at most half, 64 x 64
+    # while they need at most 1.75 rounds, else 128 x 64
     m, n = mn
     f16, f32 = np.zeros(1, np.float16), np.zeros(1, np.float32)
     ck = K.matmul_mma_kernel.compile(f16, f16, f32, m, n, BM=32, BN=32, BK=8, K=64, NT=512)
