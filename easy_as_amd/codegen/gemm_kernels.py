@@ -4,7 +4,7 @@ Launches of more than 128 rows tile C into 256 x 256 workgroup tiles (or 128 x
 128, below; the fp32 templates at the end of this module use 64 x 64 and 128 x 128).
 The 16-bit source is written once for its MFMA operand type ``eas_op_t``: f16, or
 bf16 when the kernel's threadgroup tiles are bf16 (``_OP_TYPES`` supplies the type,
-the MFMA and the transposing LDS read; everything else is the same).  It has three
+the MFMA and the transposing LDS read; everything else is the same).  It has these
 entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
 
 * ``<name>__pp`` (512 threads): the 8-wave ping-pong DMA body for A and B of the
@@ -12,10 +12,11 @@ entry points, and the launch plan (``gemm_lift.plan_gemm``) picks one:
   four waves alternate load phases and MFMA phases one barrier apart, each
   wave holding 128 x 64 of the tile (8 x 4 ``v_mfma_f32_16x16x32_f16``
   accumulators; ``EAS_HIP_GEMM_MFMA=32`` selects 4 x 2 of ``32x32x16``).
-* ``<name>__t128``, ``<name>__t128x256`` and ``<name>__t128x64`` (512 threads):
-  the same DMA operands on 128 x 128, 128 x 256 and 128 x 64 tiles, for launches
-  whose 256 x 256 grid would leave CUs idle: 4 waves issue the DMA, 4 waves of
-  64 x 64 (64 x 128, 64 x 32) read fragments and run the MFMAs.
+* ``<name>__t128``, ``<name>__t128x256``, ``<name>__t64x64`` and ``<name>__t128x64``
+  (512 threads): the same DMA operands on 128 x 128, 128 x 256, 64 x 64 and
+  128 x 64 tiles, for launches whose 256 x 256 grid would leave CUs idle: 4 waves
+  issue the DMA, 4 waves of 64 x 64 (64 x 128, 32 x 32, 64 x 32) read fragments
+  and run the MFMAs.
 * ``<name>`` (256 threads, 4 waves of 128 x 128, 4 x 4 accumulators in 256
   AGPRs): the skinny path (launches of at most 128 rows), the 4-wave DMA body,
   and the register body; a uniform branch picks one per launch.
