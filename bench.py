@@ -208,9 +208,10 @@ def _config(name: str) -> tuple:
 
 
 def _matmul_inputs(name: str, torch) -> tuple[object, object]:
-    """Host inputs: NumPy arrays, or torch bfloat16 CPU tensors (NumPy has no bfloat16)."""
+    """Host inputs: NumPy arrays, or torch bfloat16 CPU tensors (NumPy has no bfloat16), from
+    the configurations' seeds: A from default_rng(0), B from default_rng(1)."""
     _, m, n, k, da, db, _ = _config(name)
-    rng_a, rng_b = np.random.default_rng(10), np.random.default_rng(11)
+    rng_a, rng_b = np.random.default_rng(0), np.random.default_rng(1)
 
     def draw(rng, dist, size):
         if dist == "u":
@@ -446,8 +447,13 @@ def _stamped_ws_source(src: str, entry: str) -> str:
     src = src.split("\n", 1)[1]  # the eas-launch line describes the unstamped argument list
     bm, bn = {"__t128x256": (128, 256), "__t128x64": (128, 64), "__t64x64": (64, 64)}.get(
         entry[entry.rindex("__"):], (128, 128))
+    from easy_as_amd.codegen.gemm_kernels import pp_mfma
+
+    # the 128 x 128 and 128 x 256 entries take the MFMA shape EAS_HIP_GEMM_MFMA selects; 128 x 64
+    # and 64 x 64 fix 16 x 16 x 32
     t64 = "eas_gemm_t128<CT, K, 64, 16, 64>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
-    call = "eas_gemm_t128<CT, K, {}, 16>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
+    call = "eas_gemm_t128<CT, K, {}, {}>((const eas_op_t*)A, (const eas_op_t*)B, C, ldb, M, N, m0, n0, smem);"
+    call128, call256, call64 = call.format(128, pp_mfma()), call.format(256, pp_mfma()), call.format(64, 16)
     edits = [
         ("eas_op_t* smem) {\n  static_assert((BN == 64 || BN == 128 || BN == 256)",
          "eas_op_t* smem, unsigned long long* __restrict__ __eas_stamps) {\n"
@@ -461,9 +467,9 @@ def _stamped_ws_source(src: str, entry: str) -> str:
         ("(CT)acc16[i][j][r];\n        }\n  }\n}\n\n// Skinny path",
          "(CT)acc16[i][j][r];\n        }\n  }\n  EAS_WS_STAMP(3);\n"
          "  __builtin_amdgcn_s_waitcnt(0);\n  EAS_WS_STAMP(4);\n}\n\n// Skinny path"),
-        (call.format(128), call.format(128)[:-2] + (", __eas_stamps);" if (bm, bn) == (128, 128) else ", nullptr);")),
-        (call.format(256), call.format(256)[:-2] + (", __eas_stamps);" if bn == 256 else ", nullptr);")),
-        (call.format(64), call.format(64)[:-2] + (", __eas_stamps);" if bn == 64 and bm == 128 else ", nullptr);")),
+        (call128, call128[:-2] + (", __eas_stamps);" if (bm, bn) == (128, 128) else ", nullptr);")),
+        (call256, call256[:-2] + (", __eas_stamps);" if bn == 256 else ", nullptr);")),
+        (call64, call64[:-2] + (", __eas_stamps);" if bn == 64 and bm == 128 else ", nullptr);")),
         (t64, t64[:-2] + (", __eas_stamps);" if bm == 64 else ", nullptr);")),
     ]
     for old, new in edits:

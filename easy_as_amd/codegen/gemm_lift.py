@@ -4,8 +4,12 @@ The reference's simdgroup-MMA matmul (``examples/matmul_simdgroup.py:29-127``)
 computes one 8x8 fragment per 32-lane simdgroup with tiny tiles
 (``NT = (BM/8)(BN/8)*32 <= 1024``); lowered literally it cannot feed MI355X's
 matrix cores.  This module *proves* that a kernel's IR computes a dense GEMM and,
-only then, replaces it with a hand-written MFMA kernel (``v_mfma_f32_32x32x16_f16``,
-LDS-staged f16 tiles, B transposed in registers on its way into LDS).
+only then, replaces it with hand-written MFMA kernels (``codegen/gemm_kernels.py``):
+``v_mfma_f32_16x16x32_f16`` (or ``_bf16``) by default, A and B moved HBM -> LDS by
+``buffer_load ... lds`` DMA rings in their row-major layouts, B transposed on its
+way out of LDS by ``ds_read_b64_tr_b16``; operands the DMA cannot take (f32
+inputs, rows not 4-byte aligned) run a register-staged body instead.  The fp32
+tiled ``dot`` pattern lifts to ``v_mfma_f32_32x32x2_f32`` the same way.
 
 Proof method (no pattern matching on source text): the IR is executed
 symbolically for all NT threads of one threadgroup at once.  Thread ids are

@@ -38,6 +38,11 @@ struct eas_hip_kernel {
   hipFunction_t function;
   int device;
   eas_hip_launch_shape shape;  // kind EAS_HIP_KIND_RAW until set
+  // lifted GEMMs: every entry point of the code object, set by eas_hip_kernel_set_gemm
+  bool has_gemm;
+  eas_hip_gemm_shape gemm;
+  hipFunction_t gemm_fn[EAS_HIP_GEMM_NENTRIES];
+  int compute_units;
 };
 
 namespace {
@@ -386,9 +391,9 @@ int eas_hip_copy_d2d(void* dst, const void* src, size_t nbytes) {
   return EAS_HIP_OK;
 }
 
-static int launch_n(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],
-                    const uint32_t block[3], uint32_t dynamic_lds, void* stream, int n) {
-  if (!k || !grid || !block) return fail(EAS_HIP_ERR_INVALID, "kernel/grid/block must not be NULL");
+static int launch_fn(hipFunction_t fn, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],
+                     const uint32_t block[3], uint32_t dynamic_lds, void* stream, int n) {
+  if (!fn || !grid || !block) return fail(EAS_HIP_ERR_INVALID, "kernel/grid/block must not be NULL");
   if (kernarg_size && !kernarg) return fail(EAS_HIP_ERR_INVALID, "kernarg is NULL with nonzero size");
   for (int i = 0; i < 3; ++i) {
     if (grid[i] == 0 || block[i] == 0) return fail(EAS_HIP_ERR_INVALID, "grid/block dims must be > 0");
@@ -405,10 +410,16 @@ static int launch_n(const eas_hip_kernel* k, const void* kernarg, size_t kernarg
   void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(kernarg_size ? kernarg : &kEmpty),
                     HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
   for (int r = 0; r < n; ++r) {
-    HIP_TRY(hipModuleLaunchKernel(k->function, grid[0], grid[1], grid[2], block[0], block[1], block[2], dynamic_lds,
+    HIP_TRY(hipModuleLaunchKernel(fn, grid[0], grid[1], grid[2], block[0], block[1], block[2], dynamic_lds,
                                   static_cast<hipStream_t>(stream), nullptr, config));
   }
   return EAS_HIP_OK;
+}
+
+static int launch_n(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],
+                    const uint32_t block[3], uint32_t dynamic_lds, void* stream, int n) {
+  if (!k) return fail(EAS_HIP_ERR_INVALID, "kernel must not be NULL");
+  return launch_fn(k->function, kernarg, kernarg_size, grid, block, dynamic_lds, stream, n);
 }
 
 // ---- launch shapes -----------------------------------------------------------
@@ -424,21 +435,20 @@ static int check_shape(const eas_hip_launch_shape* s) {
     return fail(EAS_HIP_ERR_INVALID, "spmd and thread kernels take exactly one hidden extent");
   if (s->kind == EAS_HIP_KIND_THREAD && s->wg_size != s->block_size)
     return fail(EAS_HIP_ERR_INVALID, "a thread-mode kernel's workgroup is its BLOCK");
+  if (s->kind == EAS_HIP_KIND_GEMM && s->hidden != 4)
+    return fail(EAS_HIP_ERR_INVALID, "a lifted GEMM takes four hidden extents (m_lo, m_hi, n_lo, n_hi)");
   return EAS_HIP_OK;
 }
 
-int eas_hip_launch_shape_parse(const char* src, eas_hip_launch_shape* out) {
-  if (!src || !out) return fail(EAS_HIP_ERR_INVALID, "src/out must not be NULL");
-  const char* tag = "// eas-launch:";
+using Items = std::vector<std::pair<std::string, std::string>>;
+
+// The `key=value` items on the marker line `tag` of a generated source.
+static int marker_items(const char* src, const char* tag, const char* label, Items& items) {
   const char* p = strstr(src, tag);
   if (!p) return fail(EAS_HIP_ERR_INVALID, "source has no '%s' line", tag);
   p += strlen(tag);
   const char* end = strchr(p, '\n');
   std::string line(p, end ? (size_t)(end - p) : strlen(p));
-  eas_hip_launch_shape s{};
-  s.programs_per_wg = 1;
-  s.split = 1;
-  bool have_kind = false;
   size_t pos = 0;
   while (pos < line.size()) {
     while (pos < line.size() && line[pos] == ' ') ++pos;
@@ -447,8 +457,35 @@ int eas_hip_launch_shape_parse(const char* src, eas_hip_launch_shape* out) {
     pos = stop == std::string::npos ? line.size() : stop;
     if (item.empty()) continue;
     size_t eq = item.find('=');
-    if (eq == std::string::npos) return fail(EAS_HIP_ERR_INVALID, "malformed eas-launch item '%s'", item.c_str());
-    std::string key = item.substr(0, eq), val = item.substr(eq + 1);
+    if (eq == std::string::npos) return fail(EAS_HIP_ERR_INVALID, "malformed %s item '%s'", label, item.c_str());
+    items.emplace_back(item.substr(0, eq), item.substr(eq + 1));
+  }
+  return EAS_HIP_OK;
+}
+
+// A decimal u32 (digits only).
+static bool parse_u32(const std::string& val, uint32_t* out) {
+  if (val.empty() || val.size() > 10) return false;
+  uint64_t v = 0;
+  for (char c : val) {
+    if (c < '0' || c > '9') return false;
+    v = v * 10 + (uint64_t)(c - '0');
+  }
+  if (v > 0xFFFFFFFFull) return false;
+  *out = (uint32_t)v;
+  return true;
+}
+
+int eas_hip_launch_shape_parse(const char* src, eas_hip_launch_shape* out) {
+  if (!src || !out) return fail(EAS_HIP_ERR_INVALID, "src/out must not be NULL");
+  Items items;
+  int rc = marker_items(src, "// eas-launch:", "eas-launch", items);
+  if (rc) return rc;
+  eas_hip_launch_shape s{};
+  s.programs_per_wg = 1;
+  s.split = 1;
+  bool have_kind = false;
+  for (const auto& [key, val] : items) {
     if (key == "kind") {
       have_kind = true;
       if (val == "spmd") s.kind = EAS_HIP_KIND_SPMD;
@@ -458,19 +495,18 @@ int eas_hip_launch_shape_parse(const char* src, eas_hip_launch_shape* out) {
       else return fail(EAS_HIP_ERR_INVALID, "unknown eas-launch kind '%s'", val.c_str());
       continue;
     }
-    char* e = nullptr;
-    unsigned long v = strtoul(val.c_str(), &e, 10);
-    if (val.empty() || *e || v > 0xFFFFFFFFul) return fail(EAS_HIP_ERR_INVALID, "bad eas-launch value '%s'", item.c_str());
-    if (key == "block") s.block_size = (uint32_t)v;
-    else if (key == "wg") s.wg_size = (uint32_t)v;
-    else if (key == "ppw") s.programs_per_wg = (uint32_t)v;
-    else if (key == "split") s.split = (uint32_t)v;
-    else if (key == "args") s.arg_bytes = (uint32_t)v;
-    else if (key == "hidden") s.hidden = (uint32_t)v;
+    uint32_t v;
+    if (!parse_u32(val, &v)) return fail(EAS_HIP_ERR_INVALID, "bad eas-launch value '%s=%s'", key.c_str(), val.c_str());
+    if (key == "block") s.block_size = v;
+    else if (key == "wg") s.wg_size = v;
+    else if (key == "ppw") s.programs_per_wg = v;
+    else if (key == "split") s.split = v;
+    else if (key == "args") s.arg_bytes = v;
+    else if (key == "hidden") s.hidden = v;
     else return fail(EAS_HIP_ERR_INVALID, "unknown eas-launch key '%s'", key.c_str());
   }
   if (!have_kind) return fail(EAS_HIP_ERR_INVALID, "eas-launch line has no kind");
-  int rc = check_shape(&s);
+  rc = check_shape(&s);
   if (rc) return rc;
   *out = s;
   return EAS_HIP_OK;
@@ -481,12 +517,300 @@ int eas_hip_kernel_set_shape(eas_hip_kernel* k, const eas_hip_launch_shape* shap
   int rc = check_shape(shape);
   if (rc) return rc;
   k->shape = *shape;
+  if (shape->kind != EAS_HIP_KIND_GEMM) k->has_gemm = false;
   return EAS_HIP_OK;
 }
 
 int eas_hip_kernel_get_shape(const eas_hip_kernel* k, eas_hip_launch_shape* out) {
   if (!k || !out) return fail(EAS_HIP_ERR_INVALID, "kernel/out must not be NULL");
   *out = k->shape;
+  return EAS_HIP_OK;
+}
+
+// ---- lifted GEMMs ------------------------------------------------------------
+
+static const char* const kGemmSuffix[EAS_HIP_GEMM_NENTRIES] = {"", "__pp", "__t128", "__t128x256", "__t128x64",
+                                                               "__t64x64"};
+
+static int check_gemm(const eas_hip_gemm_shape* g) {
+  if (!g) return fail(EAS_HIP_ERR_INVALID, "GEMM shape must not be NULL");
+  const size_t len = strnlen(g->entry, sizeof(g->entry));
+  if (len == 0 || len == sizeof(g->entry)) return fail(EAS_HIP_ERR_INVALID, "GEMM shape has no entry name");
+  for (size_t i = 0; i < len; ++i) {
+    const char c = g->entry[i];
+    if (!(c == '_' || (c >= '0' && c <= '9') || (c >= 'a' && c <= 'z') || (c >= 'A' && c <= 'Z')))
+      return fail(EAS_HIP_ERR_INVALID, "GEMM entry name '%s' is not an identifier", g->entry);
+  }
+  if (!(g->entries & 1u) || g->entries >> EAS_HIP_GEMM_NENTRIES)
+    return fail(EAS_HIP_ERR_INVALID, "GEMM entry mask %#x must hold the kernel's own entry and no unknown one", g->entries);
+  if (!g->K || !g->tm || !g->tn || !g->bm || !g->bn || !g->skinny_n || g->row_axis > 1)
+    return fail(EAS_HIP_ERR_INVALID, "GEMM shape has a zero tile, K or skinny width, or a row axis other than 0 or 1");
+  for (uint32_t t : {g->threads, g->pp_threads, g->t128_threads})
+    if (!t || t > 1024 || t % 64) return fail(EAS_HIP_ERR_INVALID, "GEMM workgroup size %u is not 64..1024 in waves", t);
+  for (uint32_t e : {g->a_elem, g->b_elem, g->c_elem})
+    if (e != 2 && e != 4) return fail(EAS_HIP_ERR_INVALID, "GEMM element size %u is not 2 or 4", e);
+  if (g->ldb_off < 0) return fail(EAS_HIP_ERR_INVALID, "GEMM shape has no N (row stride) argument");
+  for (int32_t off : {g->m_off, g->ldb_off, g->row_base_off, g->col_base_off})
+    if (off >= 0 && off % 4) return fail(EAS_HIP_ERR_INVALID, "GEMM scalar offset %d is not u32-aligned", off);
+  if (g->a_off % 8 || g->b_off % 8) return fail(EAS_HIP_ERR_INVALID, "GEMM buffer offsets must be pointer-aligned");
+  return EAS_HIP_OK;
+}
+
+int eas_hip_gemm_shape_parse(const char* src, eas_hip_gemm_shape* out) {
+  if (!src || !out) return fail(EAS_HIP_ERR_INVALID, "src/out must not be NULL");
+  Items items;
+  int rc = marker_items(src, "// eas-gemm:", "eas-gemm", items);
+  if (rc) return rc;
+  eas_hip_gemm_shape g{};
+  g.m_off = g.ldb_off = g.row_base_off = g.col_base_off = -1;
+  struct U32 {
+    const char* key;
+    uint32_t* dst;
+    bool seen;
+  } u32s[] = {{"entries", &g.entries, false}, {"K", &g.K, false}, {"tm", &g.tm, false},
+              {"tn", &g.tn, false}, {"row_axis", &g.row_axis, false}, {"bm", &g.bm, false},
+              {"bn", &g.bn, false}, {"threads", &g.threads, false}, {"pp_threads", &g.pp_threads, false},
+              {"t128_threads", &g.t128_threads, false}, {"skinny_m", &g.skinny_m, false},
+              {"skinny_n", &g.skinny_n, false}, {"skinny_cut", &g.skinny_cut, false},
+              {"wide_m", &g.wide_m, false}, {"f32", &g.f32, false}, {"col_masked", &g.col_masked, false},
+              {"a", &g.a_arg, false}, {"b", &g.b_arg, false}, {"c", &g.c_arg, false},
+              {"a_off", &g.a_off, false}, {"b_off", &g.b_off, false}, {"a_elem", &g.a_elem, false},
+              {"b_elem", &g.b_elem, false}, {"c_elem", &g.c_elem, false}};
+  struct Off {
+    const char* key;
+    int32_t* dst;
+  } offs[] = {{"m", &g.m_off}, {"ldb", &g.ldb_off}, {"row_base", &g.row_base_off}, {"col_base", &g.col_base_off}};
+  bool have_entry = false;
+  for (const auto& [key, val] : items) {
+    if (key == "entry") {
+      if (val.size() >= sizeof(g.entry)) return fail(EAS_HIP_ERR_INVALID, "eas-gemm entry name too long");
+      memcpy(g.entry, val.c_str(), val.size() + 1);
+      have_entry = true;
+      continue;
+    }
+    uint32_t v;
+    if (!parse_u32(val, &v)) return fail(EAS_HIP_ERR_INVALID, "bad eas-gemm value '%s=%s'", key.c_str(), val.c_str());
+    bool known = false;
+    for (auto& u : u32s)
+      if (key == u.key) {
+        *u.dst = v;
+        u.seen = known = true;
+      }
+    for (auto& o : offs)
+      if (key == o.key) {
+        if (v > 0x7FFFFFFFu) return fail(EAS_HIP_ERR_INVALID, "eas-gemm offset '%s' too large", key.c_str());
+        *o.dst = (int32_t)v;
+        known = true;
+      }
+    if (!known) return fail(EAS_HIP_ERR_INVALID, "unknown eas-gemm key '%s'", key.c_str());
+  }
+  if (!have_entry) return fail(EAS_HIP_ERR_INVALID, "eas-gemm line has no entry");
+  for (const auto& u : u32s)
+    if (!u.seen) return fail(EAS_HIP_ERR_INVALID, "eas-gemm line lacks '%s'", u.key);
+  rc = check_gemm(&g);
+  if (rc) return rc;
+  *out = g;
+  return EAS_HIP_OK;
+}
+
+int eas_hip_kernel_set_gemm(eas_hip_kernel* k, const eas_hip_gemm_shape* g) {
+  if (!k) return fail(EAS_HIP_ERR_INVALID, "kernel must not be NULL");
+  if (k->shape.kind != EAS_HIP_KIND_GEMM)
+    return fail(EAS_HIP_ERR_INVALID, "the kernel's launch shape is not a lifted GEMM's (set its eas-launch shape first)");
+  int rc = check_gemm(g);
+  if (rc) return rc;
+  hipFunction_t fn[EAS_HIP_GEMM_NENTRIES] = {};
+  for (int e = 0; e < EAS_HIP_GEMM_NENTRIES; ++e) {
+    if (!(g->entries >> e & 1u)) continue;
+    const std::string name = std::string(g->entry) + kGemmSuffix[e];
+    hipError_t err = hipModuleGetFunction(&fn[e], k->module, name.c_str());
+    if (err != hipSuccess)
+      return fail(EAS_HIP_ERR_RUNTIME, "GEMM entry point %s is not in the code object: %s", name.c_str(),
+                  hipGetErrorString(err));
+  }
+  int cus = 0;
+  HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, k->device));
+  k->gemm = *g;
+  memcpy(k->gemm_fn, fn, sizeof(fn));
+  k->compute_units = cus;
+  k->has_gemm = true;
+  return EAS_HIP_OK;
+}
+
+namespace {
+
+using u128 = unsigned __int128;
+
+enum Choice { kAuto, k8Wave, kTile128, kTile128x256, kTile128x64, kTile64, k4Wave, kChoices };
+const char* const kChoiceNames[kChoices] = {"auto", "8wave", "tile128", "tile128x256", "tile128x64", "tile64", "4wave"};
+
+// The entry override: `choice`, or EAS_HIP_GEMM_ENTRY when NULL; blank means auto.
+int entry_choice(const char* choice, int* out) {
+  const char* raw = choice ? choice : getenv("EAS_HIP_GEMM_ENTRY");
+  std::string v = raw ? raw : "";
+  const size_t b = v.find_first_not_of(" \t\n\r\f\v"), e = v.find_last_not_of(" \t\n\r\f\v");
+  v = b == std::string::npos ? std::string() : v.substr(b, e - b + 1);
+  for (char& c : v) c = (char)((c >= 'A' && c <= 'Z') ? c - 'A' + 'a' : c);
+  if (v.empty()) v = "auto";
+  for (int i = 0; i < kChoices; ++i)
+    if (v == kChoiceNames[i]) {
+      *out = i;
+      return EAS_HIP_OK;
+    }
+  return fail(EAS_HIP_ERR_INVALID, "EAS_HIP_GEMM_ENTRY must be one of auto, 8wave, tile128, tile128x256, tile128x64, "
+                                   "tile64, 4wave; got '%s'", v.c_str());
+}
+
+int read_arg(const void* kernarg, size_t size, int32_t off, size_t bytes, const char* what, uint64_t* v) {
+  if (off < 0 || (size_t)off + bytes > size)
+    return fail(EAS_HIP_ERR_INVALID, "the packed arguments (%zu bytes) do not hold %s at byte %d", size, what, off);
+  uint64_t x = 0;
+  memcpy(&x, static_cast<const char*>(kernarg) + off, bytes);
+  *v = x;
+  return EAS_HIP_OK;
+}
+
+// Whether the DMA entries take the launch: every row of A and B (after the move to the
+// rectangle's origin) 4-byte aligned for 16-bit operands, 16-byte aligned for fp32; each
+// operand's extent under 2 GiB; A and B at such an alignment.
+bool dma_fits(uint64_t a_ptr, uint64_t b_ptr, uint64_t K, uint64_t ldb, uint64_t m, uint64_t n_lo, uint64_t n,
+              uint64_t elem) {
+  const uint64_t step = elem == 2 ? 2 : 4;
+  if (K % step || ldb % step || n_lo % step) return false;
+  if ((u128)m * K * elem >= ((u128)1 << 31) || ((u128)(K - 1) * ldb + n) * elem >= ((u128)1 << 31)) return false;
+  const uint64_t align = elem == 2 ? 4 : 16;
+  return a_ptr % align == 0 && b_ptr % align == 0;
+}
+
+uint64_t cdiv(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+int eas_hip_plan_gemm(const eas_hip_launch_shape* s, const eas_hip_gemm_shape* g, const void* kernarg,
+                      size_t kernarg_size, const uint64_t* arg_bytes, int nargs, int by_groups, const uint64_t size[3],
+                      const uint32_t tptg[3], int compute_units, const char* choice, eas_hip_gemm_plan* out) {
+  int rc = check_shape(s);
+  if (rc) return rc;
+  if (s->kind != EAS_HIP_KIND_GEMM) return fail(EAS_HIP_ERR_INVALID, "the kernel is not a lifted GEMM");
+  rc = check_gemm(g);
+  if (rc) return rc;
+  if (!size || !tptg || !out) return fail(EAS_HIP_ERR_INVALID, "size/tptg/out must not be NULL");
+  if (kernarg_size && !kernarg) return fail(EAS_HIP_ERR_INVALID, "kernarg is NULL with nonzero size");
+  if (compute_units <= 0) return fail(EAS_HIP_ERR_INVALID, "compute_units must be > 0");
+  const char* what = by_groups ? "threadgroups" : "threads_per_grid";
+  for (int i = 0; i < 3; ++i)
+    if (size[i] == 0) return fail(EAS_HIP_ERR_INVALID, "%s dims must be > 0", what);
+  const bool auto_tg = tptg[0] == 0 && tptg[1] == 0 && tptg[2] == 0;
+  if (!auto_tg && (tptg[0] != s->block_size || tptg[1] != 1 || tptg[2] != 1))
+    return fail(EAS_HIP_ERR_INVALID, "threads_per_threadgroup must be (%u, 1, 1) for this kernel, which was compiled "
+                                     "for BLOCK=%u threadgroups; got (%u, %u, %u)",
+                s->block_size, s->block_size, tptg[0], tptg[1], tptg[2]);
+  uint64_t groups[3] = {size[0], size[1], size[2]};
+  if (!by_groups) {
+    // the lift proved what whole threadgroups compute; a partial last one is another kernel
+    if (size[0] % s->block_size)
+      return fail(EAS_HIP_ERR_INVALID, "a lifted GEMM kernel runs whole threadgroups of %u threads: threads_per_grid "
+                                       "x = %llu is not a multiple of it", s->block_size, (unsigned long long)size[0]);
+    groups[0] = size[0] / s->block_size;
+  }
+  int ch = kAuto;
+  rc = entry_choice(choice, &ch);
+  if (rc) return rc;
+  uint64_t ldb = 0, M = 0, rb = 0, cb = 0, a_ptr = 0, b_ptr = 0;
+  if ((rc = read_arg(kernarg, kernarg_size, g->ldb_off, 4, "N", &ldb)) ||
+      (g->m_off >= 0 && (rc = read_arg(kernarg, kernarg_size, g->m_off, 4, "M", &M))) ||
+      (g->row_base_off >= 0 && (rc = read_arg(kernarg, kernarg_size, g->row_base_off, 4, "the row base", &rb))) ||
+      (g->col_base_off >= 0 && (rc = read_arg(kernarg, kernarg_size, g->col_base_off, 4, "the column base", &cb))) ||
+      (rc = read_arg(kernarg, kernarg_size, (int32_t)g->a_off, 8, "A", &a_ptr)) ||
+      (rc = read_arg(kernarg, kernarg_size, (int32_t)g->b_off, 8, "B", &b_ptr)))
+    return rc;
+  const u128 g_rows = groups[g->row_axis], g_cols = groups[1 - g->row_axis];
+  u128 m_lo = (u128)g->tm * rb, n_lo = (u128)g->tn * cb;
+  u128 m_hi = m_lo + g_rows * g->tm, n_hi = n_lo + g_cols * g->tn;
+  if (g->m_off >= 0 && m_hi > M) m_hi = M;
+  if (g->col_masked && n_hi > ldb) n_hi = ldb;
+  *out = eas_hip_gemm_plan{};
+  if (m_hi <= m_lo || n_hi <= n_lo) return EAS_HIP_OK;  // no element of C: nothing to run
+  const u128 K = g->K, wide = n_hi > ldb ? n_hi : (u128)ldb, lim = (u128)1 << 32;
+  if (m_hi * K >= lim || K * wide >= lim || m_hi * wide >= lim)
+    return fail(EAS_HIP_ERR_INVALID, "lifted GEMM: matrix too large for u32 indexing");
+  if (!arg_bytes)
+    return fail(EAS_HIP_ERR_INVALID, "a lifted GEMM's launch needs the byte length of each buffer argument (arg_bytes)");
+  const struct {
+    const char* name;
+    uint32_t arg, elem;
+    u128 need;
+  } bufs[] = {{"A", g->a_arg, g->a_elem, m_hi * K},
+              {"B", g->b_arg, g->b_elem, (K - 1) * ldb + n_hi},
+              {"C", g->c_arg, g->c_elem, (m_hi - 1) * ldb + n_hi}};
+  for (const auto& b : bufs) {
+    if (nargs < 0 || b.arg >= (uint32_t)nargs)
+      return fail(EAS_HIP_ERR_INVALID, "arg_bytes holds %d entries; %s is argument %u", nargs, b.name, b.arg);
+    const uint64_t have = arg_bytes[b.arg] / b.elem;
+    if (have < b.need)
+      return fail(EAS_HIP_ERR_INVALID, "buffer %s (argument %u) holds %llu elements; this launch touches %llu", b.name,
+                  b.arg, (unsigned long long)have, (unsigned long long)b.need);
+  }
+  const uint64_t m = (uint64_t)(m_hi - m_lo), n = (uint64_t)(n_hi - n_lo), cus = (uint64_t)compute_units;
+  const uint64_t tiles = cdiv(m, g->bm) * cdiv(n, g->bn), tiles128 = cdiv(m, 128) * cdiv(n, 128);
+  const uint64_t tiles128x256 = cdiv(m, 128) * cdiv(n, 256), tiles128x64 = cdiv(m, 128) * cdiv(n, 64);
+  const uint64_t tiles64 = cdiv(m, 64) * cdiv(n, 64);
+  const uint64_t elem = g->f32 ? 4 : 2;
+  auto has = [&](int e) { return (g->entries >> e & 1u) != 0; };
+  auto fits = [&] { return dma_fits(a_ptr, b_ptr, g->K, ldb, m, (uint64_t)n_lo, n, elem); };
+  int entry = EAS_HIP_GEMM_MAIN;
+  uint64_t wgs = tiles;
+  uint32_t threads = g->threads;
+  auto pick = [&](int e, uint64_t w, uint32_t t) {
+    entry = e;
+    wgs = w;
+    threads = t;
+  };
+  if (m <= g->skinny_m) {
+    // The 4-wave entry runs its skinny path for every launch of at most skinny_m rows (one
+    // workgroup per skinny_n columns, all rows), so it is only ever launched on that grid.  Up to
+    // wide_m rows, a launch whose groups would take more than one round of CUs gets twice the
+    // columns per workgroup (the kernel reads which from the grid).  Above skinny_cut rows, a
+    // launch whose groups still take more than one round goes to the 128 x 128 entry instead.
+    uint64_t grp = cdiv(n, g->skinny_n);
+    if (m <= g->wide_m && grp > cus) grp = cdiv(n, 2ull * g->skinny_n);
+    pick(EAS_HIP_GEMM_MAIN, grp, g->threads);
+    if (m > g->skinny_cut && has(EAS_HIP_GEMM_PP) && fits()) {
+      if (ch == kTile128 || (ch == kAuto && grp > cus)) pick(EAS_HIP_GEMM_T128, tiles128, g->t128_threads);
+      else if (ch == kTile128x256) pick(EAS_HIP_GEMM_T128X256, tiles128x256, g->t128_threads);
+      else if (ch == kTile128x64) pick(EAS_HIP_GEMM_T128X64, tiles128x64, g->t128_threads);
+      else if (ch == kTile64) pick(EAS_HIP_GEMM_T64X64, tiles64, g->t128_threads);
+      else if (ch == k8Wave) pick(EAS_HIP_GEMM_PP, tiles, g->pp_threads);
+    }
+  } else if (g->f32) {
+    // fp32: 128 x 128 tiles (a quarter of the DMA bytes per flop) while they still give every CU one
+    if (has(EAS_HIP_GEMM_T128) && fits() && (ch == kTile128 || (ch == kAuto && tiles128 >= cus)))
+      pick(EAS_HIP_GEMM_T128, tiles128, g->t128_threads);
+  } else if (has(EAS_HIP_GEMM_PP) && ch != k4Wave && fits()) {
+    // When 256 x 256 tiles would fill at most half of the CUs: 128 x 128 tiles if they take one
+    // round of CUs, else 128 x 256 ones.  If even 128 x 128 would fill at most half of the CUs:
+    // 64 x 64 tiles while they need at most 1.75 rounds of CUs, else 128 x 64.
+    const bool small = ch == kAuto && 2 * tiles <= cus;
+    const bool tiny = small && 2 * tiles128 <= cus;
+    if (ch == kTile128x256 || (small && tiles128 > cus)) pick(EAS_HIP_GEMM_T128X256, tiles128x256, g->t128_threads);
+    else if (ch == kTile64 || (tiny && 4 * tiles64 <= 7 * cus)) pick(EAS_HIP_GEMM_T64X64, tiles64, g->t128_threads);
+    else if (ch == kTile128x64 || tiny) pick(EAS_HIP_GEMM_T128X64, tiles128x64, g->t128_threads);
+    else if (ch == kTile128 || small) pick(EAS_HIP_GEMM_T128, tiles128, g->t128_threads);
+    else pick(EAS_HIP_GEMM_PP, tiles, g->pp_threads);
+  }
+  if (!has(entry))
+    return fail(EAS_HIP_ERR_INVALID, "GEMM entry %s%s is not in the code object", g->entry, kGemmSuffix[entry]);
+  if (wgs * threads > 0xFFFFFFFFull) return fail(EAS_HIP_ERR_INVALID, "lifted GEMM launch exceeds 2^32 work-items");
+  out->launch = 1;
+  out->entry = entry;
+  out->grid[0] = (uint32_t)wgs;
+  out->grid[1] = out->grid[2] = 1;
+  out->block[0] = threads;
+  out->block[1] = out->block[2] = 1;
+  out->hidden[0] = (uint32_t)m_lo;
+  out->hidden[1] = (uint32_t)m_hi;
+  out->hidden[2] = (uint32_t)n_lo;
+  out->hidden[3] = (uint32_t)n_hi;
   return EAS_HIP_OK;
 }
 
@@ -501,9 +825,8 @@ int eas_hip_plan_dispatch(const eas_hip_launch_shape* s, int by_groups, const ui
     return fail(EAS_HIP_ERR_INVALID, "the kernel's launch shape is unknown (a source without an eas-launch line): "
                                      "launch it with workgroup counts (launch_groups / eas_hip_launch)");
   if (s->kind == EAS_HIP_KIND_GEMM)
-    return fail(EAS_HIP_ERR_INVALID, "this kernel was lifted to an MFMA GEMM, whose workgroup grid and hidden extents "
-                                     "depend on M, N, K and its buffers: launch it through HipRuntime.run, or with the "
-                                     "entry, grid, block and hidden of plan_launch through launch_groups / eas_hip_launch");
+    return fail(EAS_HIP_ERR_INVALID, "a lifted GEMM's dispatch depends on M, N, K and its buffers: plan it with "
+                                     "eas_hip_plan_gemm");
   const char* what = by_groups ? "threadgroups" : "threads_per_grid";
   for (int i = 0; i < 3; ++i)
     if (size[i] == 0) return fail(EAS_HIP_ERR_INVALID, "%s dims must be > 0", what);
@@ -513,6 +836,9 @@ int eas_hip_plan_dispatch(const eas_hip_launch_shape* s, int by_groups, const ui
       return fail(EAS_HIP_ERR_INVALID, "threads_per_threadgroup must be (%u, 1, 1) for this kernel, which was compiled "
                                        "for BLOCK=%u threadgroups; got (%u, %u, %u)",
                   s->block_size, s->block_size, tptg[0], tptg[1], tptg[2]);
+    // bounded before multiplying, so a huge threadgroup count cannot wrap past the checks
+    if (by_groups && size[0] > 0xFFFFFFFFull / s->block_size)
+      return fail(EAS_HIP_ERR_INVALID, "%s x exceeds 2^32 threads", what);
     uint64_t groups_x = by_groups ? size[0] : (size[0] + s->block_size - 1) / s->block_size;
     uint64_t live = by_groups ? size[0] * s->block_size : size[0];
     if (live > 0xFFFFFFFFull || groups_x * s->block_size > 0xFFFFFFFFull)
@@ -567,37 +893,56 @@ int eas_hip_launch(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_
   return launch_n(k, kernarg, kernarg_size, grid, block, dynamic_lds, stream, repeat);
 }
 
-static int launch_reference(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, int by_groups,
-                            const uint64_t size[3], const uint32_t tptg[3], void* stream, int repeat) {
+static int launch_reference(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
+                            const uint64_t* arg_bytes, int nargs, int by_groups, const uint64_t size[3],
+                            const uint32_t tptg[3], void* stream, int repeat) {
   if (!k) return fail(EAS_HIP_ERR_INVALID, "kernel must not be NULL");
   if (repeat <= 0) return fail(EAS_HIP_ERR_INVALID, "repeat must be > 0");
   static const uint32_t kAuto[3] = {0, 0, 0};
-  uint32_t grid[3], block[3], hidden[EAS_HIP_MAX_HIDDEN];
-  int rc = eas_hip_plan_dispatch(&k->shape, by_groups, size, tptg ? tptg : kAuto, grid, block, hidden,
-                                 EAS_HIP_MAX_HIDDEN);
-  if (rc) return rc;
-  size_t want = expected_kernarg(k->shape, false);
+  const size_t want = expected_kernarg(k->shape, false);
   if (want && kernarg_size != want)
     return fail(EAS_HIP_ERR_INVALID, "kernel argument blob of %zu bytes does not match the kernel's %u bytes of "
                                      "arguments (the hidden extents are appended by the launch)",
                 kernarg_size, k->shape.arg_bytes);
   if (kernarg_size && !kernarg) return fail(EAS_HIP_ERR_INVALID, "kernarg is NULL with nonzero size");
+  uint32_t grid[3], block[3], hidden[EAS_HIP_MAX_HIDDEN];
+  hipFunction_t fn = k->function;
+  if (k->shape.kind == EAS_HIP_KIND_GEMM) {
+    if (!k->has_gemm)
+      return fail(EAS_HIP_ERR_INVALID, "this lifted GEMM kernel has no GEMM shape attached (eas_hip_kernel_set_gemm "
+                                       "with its source's eas-gemm line)");
+    eas_hip_gemm_plan plan;
+    int rc = eas_hip_plan_gemm(&k->shape, &k->gemm, kernarg, kernarg_size, arg_bytes, nargs, by_groups, size,
+                               tptg ? tptg : kAuto, k->compute_units, nullptr, &plan);
+    if (rc) return rc;
+    if (!plan.launch) return EAS_HIP_OK;
+    memcpy(grid, plan.grid, sizeof(grid));
+    memcpy(block, plan.block, sizeof(block));
+    memcpy(hidden, plan.hidden, sizeof(plan.hidden));
+    fn = k->gemm_fn[plan.entry];
+  } else {
+    int rc = eas_hip_plan_dispatch(&k->shape, by_groups, size, tptg ? tptg : kAuto, grid, block, hidden,
+                                   EAS_HIP_MAX_HIDDEN);
+    if (rc) return rc;
+  }
   std::vector<uint8_t> blob((kernarg_size + 3) / 4 * 4 + 4 * k->shape.hidden, 0);
   if (kernarg_size) memcpy(blob.data(), kernarg, kernarg_size);
   memcpy(blob.data() + (kernarg_size + 3) / 4 * 4, hidden, 4 * k->shape.hidden);
-  return launch_n(k, blob.data(), blob.size(), grid, block, 0, stream, repeat);
+  return launch_fn(fn, blob.data(), blob.size(), grid, block, 0, stream, repeat);
 }
 
-int eas_hip_launch_threads(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
-                           const uint64_t threads_per_grid[3], const uint32_t threads_per_threadgroup[3], void* stream,
-                           int repeat) {
-  return launch_reference(k, kernarg, kernarg_size, 0, threads_per_grid, threads_per_threadgroup, stream, repeat);
+int eas_hip_launch_threads(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint64_t* arg_bytes,
+                           int nargs, const uint64_t threads_per_grid[3], const uint32_t threads_per_threadgroup[3],
+                           void* stream, int repeat) {
+  return launch_reference(k, kernarg, kernarg_size, arg_bytes, nargs, 0, threads_per_grid, threads_per_threadgroup,
+                          stream, repeat);
 }
 
 int eas_hip_launch_threadgroups(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
-                                const uint64_t threadgroups[3], const uint32_t threads_per_threadgroup[3], void* stream,
-                                int repeat) {
-  return launch_reference(k, kernarg, kernarg_size, 1, threadgroups, threads_per_threadgroup, stream, repeat);
+                                const uint64_t* arg_bytes, int nargs, const uint64_t threadgroups[3],
+                                const uint32_t threads_per_threadgroup[3], void* stream, int repeat) {
+  return launch_reference(k, kernarg, kernarg_size, arg_bytes, nargs, 1, threadgroups, threads_per_threadgroup, stream,
+                          repeat);
 }
 
 int eas_hip_launch_timed(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],

@@ -43,21 +43,28 @@ struct Buffer {
   PyObject* owner;     // object kept alive by a wrapped pointer
 };
 
-// Async launches on one stream share completion events.  Consecutive launches join the
-// stream's open batch, whose event is recorded after its kBatchLaunches-th launch, or as
-// soon as someone waits on a launch in it; the stream runs in order, so that event marks the
-// completion of every launch in the batch.  On MI355X recording an event costs ~4.5 us of
-// host time against ~2.7 us for the launch itself, so one event per launch would almost
-// triple the cost of an async call.  All batch state is touched with the GIL held.
+// Async launches on one stream share completion events.  Consecutive launches on a stream
+// join its open batch, whose event is recorded after the batch's last permitted launch (at
+// most kBatchLaunches, fewer when the caller asks: `batch=`), when a launch arrives on another
+// stream, or as soon as someone waits on a launch in it; the stream runs in order, so that
+// event marks the completion of every launch in the batch.  Waiting on a pending launch
+// therefore also waits for the later launches of its batch, and for any other work queued on
+// that stream before the event was recorded.  At most one batch is open, and its stream is
+// the one the latest async launch used, so the event is recorded on a stream that was in use
+// moments before (a caller that destroys a stream must first wait on its pending launches).
+// On MI355X recording an event costs ~4.5 us of host time against ~2.7 us for the launch
+// itself, so one event per launch would almost triple the cost of an async call.  All batch
+// state is touched with the GIL held.
 struct Batch {
   void* stream;
   void* event;     // recorded completion event (nullptr while open, or if recording failed)
   int launches;
+  int limit;       // launches after which the batch closes
   int refs;        // unreleased pending capsules in this batch
   bool closed;     // no further launches join it
 };
 constexpr int kBatchLaunches = 16;
-std::vector<Batch*> g_open_batches;  // the open batch of each stream that has one
+std::vector<Batch*> g_open_batches;  // the open batch (at most one)
 
 struct Pending {
   Batch* batch;    // nullptr once released
@@ -109,15 +116,24 @@ void recycle_event(void* ev, bool ok) {
   else eas_hip_event_destroy(ev);
 }
 
-Batch* join_batch(void* stream) {
-  for (Batch* b : g_open_batches) {
+int close_batch(Batch* b);
+
+// The batch a launch just enqueued on `stream` belongs to: the open one if it is that
+// stream's (an open batch of another stream is closed first), else a new one that closes
+// after `limit` launches.  *rc receives the status of closing the other stream's batch.
+Batch* join_batch(void* stream, int limit, int* rc) {
+  *rc = EAS_HIP_OK;
+  while (!g_open_batches.empty()) {
+    Batch* b = g_open_batches.back();
     if (b->stream == stream) {
       ++b->launches;
       ++b->refs;
       return b;
     }
+    int crc = close_batch(b);  // removes it from g_open_batches
+    if (!*rc) *rc = crc;
   }
-  auto* b = new Batch{stream, nullptr, 1, 1, false};
+  auto* b = new Batch{stream, nullptr, 1, limit, 1, false};
   g_open_batches.push_back(b);
   return b;
 }
@@ -241,31 +257,36 @@ void append_aligned(std::vector<uint8_t>& blob, const void* data, size_t size, s
 
 // Pack argv into a kernel-argument blob at natural alignment; buffer capsules
 // become device pointers (and are appended to `keep`), bytes are copied raw,
-// int -> u32, float -> f32.  Mirrors bind_args_fast (_metal.mm:855-951).
-bool pack_args(PyObject* argv_obj, PyObject* writable_obj, std::vector<uint8_t>& blob, std::vector<PyObject*>* keep) {
+// int -> u32, float -> f32.  `sizes` (when given) receives each item's buffer length,
+// 0 for a scalar, as the reference's buffer objects carry theirs.  A NULL `writable_obj`
+// marks every item read-only.  Mirrors bind_args_fast (_metal.mm:855-951).
+bool pack_args(PyObject* argv_obj, PyObject* writable_obj, std::vector<uint8_t>& blob, std::vector<PyObject*>* keep,
+               std::vector<uint64_t>* sizes = nullptr) {
   PyObject* argv = PySequence_Fast(argv_obj, "argv must be a sequence");
   if (!argv) return false;
-  PyObject* writable = PySequence_Fast(writable_obj, "writable must be a sequence");
-  if (!writable) {
+  PyObject* writable = writable_obj ? PySequence_Fast(writable_obj, "writable must be a sequence") : nullptr;
+  if (writable_obj && !writable) {
     Py_DECREF(argv);
     return false;
   }
   bool ok = true;
   const Py_ssize_t n = PySequence_Fast_GET_SIZE(argv);
-  if (PySequence_Fast_GET_SIZE(writable) != n) {
+  if (writable && PySequence_Fast_GET_SIZE(writable) != n) {
     PyErr_SetString(PyExc_ValueError, "writable must have same length as argv");
     ok = false;
   }
   for (Py_ssize_t i = 0; ok && i < n; ++i) {
     PyObject* obj = PySequence_Fast_GET_ITEM(argv, i);
-    int want_write = PyObject_IsTrue(PySequence_Fast_GET_ITEM(writable, i));
+    int want_write = writable ? PyObject_IsTrue(PySequence_Fast_GET_ITEM(writable, i)) : 0;
     if (want_write < 0) {
       ok = false;
       break;
     }
+    if (sizes) sizes->push_back(0);
     if (Buffer* b = as_buffer(obj)) {
       uint64_t p = (uint64_t)(uintptr_t)b->ptr;
       append_aligned(blob, &p, 8, 8);
+      if (sizes) sizes->back() = (uint64_t)b->nbytes;
       if (keep) {
         Py_INCREF(obj);
         keep->push_back(obj);
@@ -313,7 +334,7 @@ bool pack_args(PyObject* argv_obj, PyObject* writable_obj, std::vector<uint8_t>&
     PyErr_Format(PyExc_TypeError, "unsupported arg %zd type (expected buffer capsule or scalar bytes/int/float)", i);
     ok = false;
   }
-  Py_DECREF(writable);
+  Py_XDECREF(writable);
   Py_DECREF(argv);
   if (!ok && keep) {
     for (PyObject* o : *keep) Py_DECREF(o);
@@ -406,12 +427,17 @@ PyObject* py_compiler_version(PyObject*, PyObject*) {
 }
 
 // Attach the launch shape on `src`'s eas-launch line to `k` (a source without one leaves the
-// kernel's shape unknown: it then runs only through launch_groups).
+// kernel's shape unknown: it then runs only through launch_groups), and a lifted GEMM's
+// plan inputs on its eas-gemm line.
 int attach_shape(eas_hip_kernel* k, const char* src) {
   if (!src || !strstr(src, "// eas-launch:")) return EAS_HIP_OK;
   eas_hip_launch_shape s;
   int rc = eas_hip_launch_shape_parse(src, &s);
-  return rc ? rc : eas_hip_kernel_set_shape(k, &s);
+  if (!rc) rc = eas_hip_kernel_set_shape(k, &s);
+  if (rc || s.kind != EAS_HIP_KIND_GEMM) return rc;
+  eas_hip_gemm_shape g;
+  rc = eas_hip_gemm_shape_parse(src, &g);
+  return rc ? rc : eas_hip_kernel_set_gemm(k, &g);
 }
 
 PyObject* new_kernel_capsule(eas_hip_kernel* k, const char* src) {
@@ -638,6 +664,7 @@ struct LaunchArgs {
   int repeat = 1;
   unsigned int lds = 0;
   PyObject* stream = nullptr;
+  int batch = kBatchLaunches;  // async: launches per completion event
   uint32_t g[3], b[3];
   uint64_t sz[3];
   uint32_t tg[3] = {0, 0, 0};
@@ -707,25 +734,30 @@ bool parse_tptg(PyObject* obj, uint32_t out[3]) {
 
 bool parse_launch(PyObject* args, PyObject* kwargs, Form form, LaunchArgs& a) {
   if (form == Form::kGroups) {
-    static const char* kw[] = {"kernel", "argv", "writable", "grid", "block", "repeat", "lds", "stream", nullptr};
-    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOOO|iIO", const_cast<char**>(kw), &a.kernel, &a.argv,
-                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.lds, &a.stream))
+    static const char* kw[] = {"kernel", "argv", "writable", "grid", "block", "repeat", "lds", "stream", "batch",
+                               nullptr};
+    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOOO|iIO$i", const_cast<char**>(kw), &a.kernel, &a.argv,
+                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.lds, &a.stream, &a.batch))
       return false;
   } else if (form == Form::kThreads) {
     static const char* kw[] = {"kernel", "argv", "writable", "threads_per_grid", "threads_per_threadgroup", "repeat",
-                               "stream", nullptr};
-    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOO|Oi$O", const_cast<char**>(kw), &a.kernel, &a.argv,
-                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.stream))
+                               "stream", "batch", nullptr};
+    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOO|Oi$Oi", const_cast<char**>(kw), &a.kernel, &a.argv,
+                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.stream, &a.batch))
       return false;
   } else {
     static const char* kw[] = {"kernel", "argv", "writable", "threadgroups", "threads_per_threadgroup", "repeat",
-                               "stream", nullptr};
-    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOOO|i$O", const_cast<char**>(kw), &a.kernel, &a.argv,
-                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.stream))
+                               "stream", "batch", nullptr};
+    if (!PyArg_ParseTupleAndKeywords(args, kwargs, "OOOOO|i$Oi", const_cast<char**>(kw), &a.kernel, &a.argv,
+                                     &a.writable, &a.size, &a.tptg, &a.repeat, &a.stream, &a.batch))
       return false;
   }
   if (a.repeat <= 0) {
     PyErr_SetString(PyExc_ValueError, "repeat must be > 0");
+    return false;
+  }
+  if (a.batch < 1 || a.batch > kBatchLaunches) {
+    PyErr_Format(PyExc_ValueError, "batch must be in [1, %d]", kBatchLaunches);
     return false;
   }
   a.k = as_kernel(a.kernel);
@@ -756,14 +788,17 @@ bool parse_launch(PyObject* args, PyObject* kwargs, Form form, LaunchArgs& a) {
   return parse_tptg(a.tptg, a.tg);
 }
 
-int dispatch(const LaunchArgs& a, Form form, const std::vector<uint8_t>& blob, void* stream) {
+int dispatch(const LaunchArgs& a, Form form, const std::vector<uint8_t>& blob, const std::vector<uint64_t>& sizes,
+             void* stream) {
+  const int nargs = (int)sizes.size();
   switch (form) {
     case Form::kGroups:
       return eas_hip_launch(a.k, blob.data(), blob.size(), a.g, a.b, a.lds, stream, a.repeat);
     case Form::kThreads:
-      return eas_hip_launch_threads(a.k, blob.data(), blob.size(), a.sz, a.tg, stream, a.repeat);
+      return eas_hip_launch_threads(a.k, blob.data(), blob.size(), sizes.data(), nargs, a.sz, a.tg, stream, a.repeat);
     default:
-      return eas_hip_launch_threadgroups(a.k, blob.data(), blob.size(), a.sz, a.tg, stream, a.repeat);
+      return eas_hip_launch_threadgroups(a.k, blob.data(), blob.size(), sizes.data(), nargs, a.sz, a.tg, stream,
+                                         a.repeat);
   }
 }
 
@@ -772,8 +807,9 @@ PyObject* launch_impl(PyObject* args, PyObject* kwargs, Form form, bool async) {
   LaunchArgs a;
   if (!parse_launch(args, kwargs, form, a)) return nullptr;
   std::vector<uint8_t> blob;
+  std::vector<uint64_t> sizes;
   auto* pending = async ? new Pending{nullptr, {}} : nullptr;
-  if (!pack_args(a.argv, a.writable, blob, pending ? &pending->keepalive : nullptr)) {
+  if (!pack_args(a.argv, a.writable, blob, pending ? &pending->keepalive : nullptr, &sizes)) {
     delete pending;
     return nullptr;
   }
@@ -783,7 +819,7 @@ PyObject* launch_impl(PyObject* args, PyObject* kwargs, Form form, bool async) {
     delete pending;
     return nullptr;
   }
-  int rc = dispatch(a, form, blob, stream);
+  int rc = dispatch(a, form, blob, sizes, stream);
   if (rc) {
     if (pending) release_pending(pending);
     delete pending;
@@ -798,9 +834,12 @@ PyObject* launch_impl(PyObject* args, PyObject* kwargs, Form form, bool async) {
   }
   Py_INCREF(a.kernel);
   pending->keepalive.push_back(a.kernel);
-  Batch* b = join_batch(stream);
+  Batch* b = join_batch(stream, a.batch, &rc);
   pending->batch = b;
-  if (b->launches >= kBatchLaunches) rc = close_batch(b);
+  if (b->launches >= b->limit) {
+    int crc = close_batch(b);
+    if (!rc) rc = crc;
+  }
   if (rc) {
     release_pending(pending);
     delete pending;
@@ -888,27 +927,66 @@ PyObject* py_kernel_shape(PyObject*, PyObject* args) {
   return shape_dict(s);
 }
 
-// launch_shape(src) -> dict: the shape on a generated source's eas-launch line (no GPU needed).
+PyObject* gemm_dict(const eas_hip_gemm_shape& g) {
+  return Py_BuildValue("{s:s,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:I,s:i,s:i,s:i,s:i,s:I,"
+                       "s:I,s:I,s:I,s:I,s:I,s:I,s:I}",
+                       "entry", g.entry, "entries", g.entries, "K", g.K, "tm", g.tm, "tn", g.tn, "row_axis",
+                       g.row_axis, "bm", g.bm, "bn", g.bn, "threads", g.threads, "pp_threads", g.pp_threads,
+                       "t128_threads", g.t128_threads, "skinny_m", g.skinny_m, "skinny_n", g.skinny_n, "skinny_cut",
+                       g.skinny_cut, "wide_m", g.wide_m, "f32", g.f32, "col_masked", g.col_masked, "m_off", g.m_off,
+                       "ldb_off", g.ldb_off, "row_base_off", g.row_base_off, "col_base_off", g.col_base_off, "a_arg",
+                       g.a_arg, "b_arg", g.b_arg, "c_arg", g.c_arg, "a_off", g.a_off, "b_off", g.b_off, "a_elem",
+                       g.a_elem, "b_elem", g.b_elem, "c_elem", g.c_elem);
+}
+
+// launch_shape(src) -> dict: the shape on a generated source's eas-launch line (no GPU needed);
+// a lifted GEMM's also holds its eas-gemm line under "gemm".
 PyObject* py_launch_shape(PyObject*, PyObject* args) {
   const char* src;
   if (!PyArg_ParseTuple(args, "s", &src)) return nullptr;
   eas_hip_launch_shape s;
   int rc = eas_hip_launch_shape_parse(src, &s);
   if (rc) return raise_status(rc);
-  return shape_dict(s);
+  PyObject* d = shape_dict(s);
+  if (!d || s.kind != EAS_HIP_KIND_GEMM) return d;
+  eas_hip_gemm_shape g;
+  rc = eas_hip_gemm_shape_parse(src, &g);
+  if (rc) {
+    Py_DECREF(d);
+    return raise_status(rc);
+  }
+  PyObject* gd = gemm_dict(g);
+  if (!gd || PyDict_SetItemString(d, "gemm", gd) != 0) {
+    Py_XDECREF(gd);
+    Py_DECREF(d);
+    return nullptr;
+  }
+  Py_DECREF(gd);
+  return d;
 }
 
-// plan_dispatch(src, size, threads_per_threadgroup=None, by_groups=False) -> (grid, block, hidden):
+const char* const kGemmSuffixes[EAS_HIP_GEMM_NENTRIES] = {"", "__pp", "__t128", "__t128x256", "__t128x64",
+                                                          "__t64x64"};
+
+// plan_dispatch(src, size, threads_per_threadgroup=None, by_groups=False, argv=None, compute_units=256,
+//               entry_choice=None):
 // the HIP dispatch that launch (by_groups False) or launch_tg (True) makes for a kernel compiled
-// from `src`, without a GPU.
+// from `src`, without a GPU: (grid, block, hidden).  A lifted GEMM's plan reads M, N, the tile
+// bases and the A and B addresses from `argv` (the kernel's own arguments, as launch takes them;
+// wrap_pointer capsules stand for buffers) and returns (grid, block, hidden, entry), entry None
+// for the kernel's own, or None when the launch covers no element of C.
 PyObject* py_plan_dispatch(PyObject*, PyObject* args, PyObject* kwargs) {
-  static const char* kw[] = {"src", "size", "threads_per_threadgroup", "by_groups", nullptr};
+  static const char* kw[] = {"src", "size", "threads_per_threadgroup", "by_groups", "argv", "compute_units",
+                             "entry_choice", nullptr};
   const char* src;
   PyObject* size_obj;
   PyObject* tptg_obj = nullptr;
   int by_groups = 0;
-  if (!PyArg_ParseTupleAndKeywords(args, kwargs, "sO|Op", const_cast<char**>(kw), &src, &size_obj, &tptg_obj,
-                                   &by_groups))
+  PyObject* argv = nullptr;
+  int cus = 256;
+  const char* choice = nullptr;
+  if (!PyArg_ParseTupleAndKeywords(args, kwargs, "sO|OpOiz", const_cast<char**>(kw), &src, &size_obj, &tptg_obj,
+                                   &by_groups, &argv, &cus, &choice))
     return nullptr;
   eas_hip_launch_shape s;
   int rc = eas_hip_launch_shape_parse(src, &s);
@@ -917,6 +995,28 @@ PyObject* py_plan_dispatch(PyObject*, PyObject* args, PyObject* kwargs) {
   uint32_t tg[3];
   if (!parse_size3(size_obj, sz, by_groups ? "threadgroups" : "threads_per_grid") || !parse_tptg(tptg_obj, tg))
     return nullptr;
+  if (s.kind == EAS_HIP_KIND_GEMM) {
+    if (!argv || argv == Py_None) {
+      PyErr_SetString(PyExc_TypeError, "a lifted GEMM's plan needs argv (its M, N and buffers)");
+      return nullptr;
+    }
+    eas_hip_gemm_shape g;
+    rc = eas_hip_gemm_shape_parse(src, &g);
+    if (rc) return raise_status(rc);
+    std::vector<uint8_t> blob;
+    std::vector<uint64_t> sizes;
+    if (!pack_args(argv, nullptr, blob, nullptr, &sizes)) return nullptr;
+    eas_hip_gemm_plan p;
+    rc = eas_hip_plan_gemm(&s, &g, blob.data(), blob.size(), sizes.data(), (int)sizes.size(), by_groups, sz, tg, cus,
+                           choice, &p);
+    if (rc) return raise_status(rc);
+    if (!p.launch) Py_RETURN_NONE;
+    PyObject* entry = p.entry == EAS_HIP_GEMM_MAIN ? (Py_INCREF(Py_None), Py_None)
+                                                   : PyUnicode_FromFormat("%s%s", g.entry, kGemmSuffixes[p.entry]);
+    if (!entry) return nullptr;
+    return Py_BuildValue("((III)(III)(IIII)N)", p.grid[0], p.grid[1], p.grid[2], p.block[0], p.block[1], p.block[2],
+                         p.hidden[0], p.hidden[1], p.hidden[2], p.hidden[3], entry);
+  }
   uint32_t grid[3], block[3], hidden[EAS_HIP_MAX_HIDDEN];
   rc = eas_hip_plan_dispatch(&s, by_groups, sz, tg, grid, block, hidden, EAS_HIP_MAX_HIDDEN);
   if (rc) return raise_status(rc);
@@ -924,6 +1024,20 @@ PyObject* py_plan_dispatch(PyObject*, PyObject* args, PyObject* kwargs) {
   for (uint32_t i = 0; h && i < s.hidden; ++i) PyTuple_SET_ITEM(h, i, PyLong_FromUnsignedLong(hidden[i]));
   if (!h) return nullptr;
   return Py_BuildValue("((III)(III)N)", grid[0], grid[1], grid[2], block[0], block[1], block[2], h);
+}
+
+// pending_info(pending) -> dict: the launch's completion batch (stream, launches, closed), or
+// released True once it was waited on.
+PyObject* py_pending_info(PyObject*, PyObject* args) {
+  PyObject* cap;
+  if (!PyArg_ParseTuple(args, "O", &cap)) return nullptr;
+  auto* p = static_cast<Pending*>(PyCapsule_GetPointer(cap, kPendingCap));
+  if (!p) return nullptr;
+  if (!p->batch) return Py_BuildValue("{s:O}", "released", Py_True);
+  const Batch* b = p->batch;
+  return Py_BuildValue("{s:O,s:K,s:i,s:i,s:O}", "released", Py_False, "stream",
+                       (unsigned long long)(uintptr_t)b->stream, "launches", b->launches, "limit", b->limit, "closed",
+                       b->closed ? Py_True : Py_False);
 }
 
 PyObject* py_synchronize(PyObject*, PyObject* args) {
@@ -1075,7 +1189,7 @@ PyMethodDef kMethods[] = {
     {"kernel_shape", py_kernel_shape, METH_VARARGS, "Launch shape attached to a loaded kernel."},
     {"launch_shape", py_launch_shape, METH_VARARGS, "Launch shape on a generated source's eas-launch line."},
     {"plan_dispatch", (PyCFunction)(void (*)(void))py_plan_dispatch, METH_VARARGS | METH_KEYWORDS,
-     "HIP dispatch (grid, block, hidden) of a reference-convention launch, without a GPU."},
+     "HIP dispatch (grid, block, hidden[, entry]) of a reference-convention launch, without a GPU."},
     {"compile", py_compile, METH_VARARGS,
      "compile(src, name, options=None): compile_to_code (DEFAULT_OPTIONS when none are given) + load."},
     {"kernel_attrs", py_kernel_attrs, METH_VARARGS, "Static resources of a loaded kernel."},
@@ -1089,20 +1203,21 @@ PyMethodDef kMethods[] = {
      "launch(kernel, argv, writable, threads_per_grid, threads_per_threadgroup=None, repeat=1): dispatch by "
      "threads and wait."},
     {"launch_async", (PyCFunction)(void (*)(void))py_launch_async, METH_VARARGS | METH_KEYWORDS,
-     "As launch; returns a pending capsule."},
+     "As launch; returns a pending capsule (batch=: launches per completion event, 1-16)."},
     {"launch_tg", (PyCFunction)(void (*)(void))py_launch_tg, METH_VARARGS | METH_KEYWORDS,
      "launch_tg(kernel, argv, writable, threadgroups, threads_per_threadgroup, repeat=1): dispatch by "
      "threadgroups and wait."},
     {"launch_tg_async", (PyCFunction)(void (*)(void))py_launch_tg_async, METH_VARARGS | METH_KEYWORDS,
-     "As launch_tg; returns a pending capsule."},
+     "As launch_tg; returns a pending capsule (batch= as for launch_async)."},
     {"launch_groups", (PyCFunction)(void (*)(void))py_launch_groups, METH_VARARGS | METH_KEYWORDS,
      "launch_groups(kernel, argv, writable, grid, block, repeat=1, lds=0, stream=None): HIP workgroups, argv "
      "ending with the hidden extents; waits."},
     {"launch_groups_async", (PyCFunction)(void (*)(void))py_launch_groups_async, METH_VARARGS | METH_KEYWORDS,
-     "As launch_groups; returns a pending capsule."},
+     "As launch_groups; returns a pending capsule (batch= as for launch_async)."},
     {"launch_timed", (PyCFunction)(void (*)(void))py_launch_timed, METH_VARARGS | METH_KEYWORDS,
      "Event-timed repeat launches; mean ms per launch."},
     {"synchronize", py_synchronize, METH_VARARGS, "Wait for a pending launch and drop its keepalives."},
+    {"pending_info", py_pending_info, METH_VARARGS, "Completion batch of a pending launch (stream, launches, closed)."},
     {"queue_synchronize", py_queue_synchronize, METH_VARARGS, "Wait for a stream (default: whole device)."},
     {"dlpack_import", py_dlpack_import, METH_VARARGS, "Zero-copy import of a kDLROCM DLPack capsule."},
     {"dlpack_export", py_dlpack_export, METH_VARARGS, "Export a buffer as a kDLROCM DLPack capsule."},

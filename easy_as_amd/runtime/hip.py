@@ -366,8 +366,12 @@ class HipRuntime:
             for buf, arr in copy_back:
                 mod.copy_to_host(buf, arr)
             return
-        self._pending.append(mod.launch_groups_async(kernel, argv, writable, plan.grid, plan.block, stream=stream))
         limit = self._max_pending()
+        # launches share a completion event per batch; with a bound, a batch holds at most `limit`
+        # launches, so waiting on the oldest pending launch leaves the later batches in flight
+        batch = min(16, limit) if limit else 16
+        self._pending.append(mod.launch_groups_async(kernel, argv, writable, plan.grid, plan.block, stream=stream,
+                                                     batch=batch))
         while limit and len(self._pending) > limit:
             mod.synchronize(self._pending.popleft())
 

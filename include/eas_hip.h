@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define EAS_HIP_ABI_VERSION 3
+#define EAS_HIP_ABI_VERSION 4
 
 typedef enum eas_hip_status {
   EAS_HIP_OK = 0,
@@ -124,7 +124,7 @@ typedef enum eas_hip_launch_kind {
   EAS_HIP_KIND_RAW = 0,    /* shape unknown: only eas_hip_launch (workgroups) runs it      */
   EAS_HIP_KIND_SPMD = 1,   /* a Metal thread is a program of block_size lanes (mk.arange)   */
   EAS_HIP_KIND_THREAD = 2, /* a Metal thread is a HIP thread, a threadgroup a workgroup     */
-  EAS_HIP_KIND_GEMM = 3    /* lifted MFMA GEMM: its plan needs M, N, K (eas_hip_launch only) */
+  EAS_HIP_KIND_GEMM = 3    /* lifted MFMA GEMM: planned from M, N, K and its buffers        */
 } eas_hip_launch_kind;
 
 typedef struct eas_hip_launch_shape {
@@ -160,25 +160,96 @@ int eas_hip_plan_dispatch(const eas_hip_launch_shape* shape, int by_groups, cons
                           const uint32_t tptg[3], uint32_t grid[3], uint32_t block[3], uint32_t* hidden,
                           int max_hidden);
 
+/* ---- lifted GEMMs ---------------------------------------------------------
+ * A kernel that the GEMM lift proved to be C = A @ B is compiled to several entry
+ * points, and each launch picks one from the matrix sizes, the buffers and the number
+ * of compute units.  Its source carries a second marker line with what that plan
+ * needs (`// eas-gemm: entry=... K=... tm=... ...`): the position of M, N (the row
+ * stride of B and C) and the tile-base scalars in the packed arguments, where A, B and
+ * C are, the reference's tile per threadgroup and the entry points present.  No
+ * counterpart in the reference, whose one pipeline per kernel runs any grid. */
+typedef enum eas_hip_gemm_entry {
+  EAS_HIP_GEMM_MAIN = 0,      /* the kernel's own name: 4 waves (skinny path, register-staged body, fp32 64 x 64) */
+  EAS_HIP_GEMM_PP = 1,        /* <name>__pp: 8 waves on 256 x 256 tiles                                          */
+  EAS_HIP_GEMM_T128 = 2,      /* <name>__t128: 128 x 128 tiles                                                   */
+  EAS_HIP_GEMM_T128X256 = 3,  /* <name>__t128x256                                                                 */
+  EAS_HIP_GEMM_T128X64 = 4,   /* <name>__t128x64                                                                  */
+  EAS_HIP_GEMM_T64X64 = 5,    /* <name>__t64x64                                                                   */
+  EAS_HIP_GEMM_NENTRIES = 6
+} eas_hip_gemm_entry;
+
+typedef struct eas_hip_gemm_shape {
+  char entry[128];            /* the kernel's own entry point; the others append their suffix      */
+  uint32_t entries;           /* bit e set: entry point e (eas_hip_gemm_entry) is in the code object */
+  uint32_t K;                 /* reduction length (a constexpr of the kernel)                        */
+  uint32_t tm, tn;            /* rows and columns of C per reference threadgroup                     */
+  uint32_t row_axis;          /* threadgroup axis (0 or 1) that indexes tile rows                    */
+  uint32_t bm, bn;            /* tile of the kernel's own entry                                      */
+  uint32_t threads, pp_threads, t128_threads; /* workgroup sizes: own, 8-wave, smaller-tile entries  */
+  uint32_t skinny_m, skinny_n;  /* launches of <= skinny_m rows: one workgroup per skinny_n columns  */
+  uint32_t skinny_cut, wide_m;  /* rows that always stay skinny; rows that may take 2 x skinny_n     */
+  uint32_t f32;               /* fp32 operands (the tiled `dot` GEMM), else 16-bit                   */
+  uint32_t col_masked;        /* columns bounded by N (else by the launched grid only)               */
+  int32_t m_off;              /* byte offset of the u32 M in the packed arguments; -1: no row bound  */
+  int32_t ldb_off;            /* byte offset of the u32 N (row stride of B and C)                    */
+  int32_t row_base_off, col_base_off; /* byte offsets of the u32 tile bases; -1: none                */
+  uint32_t a_arg, b_arg, c_arg;       /* argument positions of A, B and C                            */
+  uint32_t a_off, b_off;              /* byte offsets of A's and B's pointers                        */
+  uint32_t a_elem, b_elem, c_elem;    /* bytes per element of A, B and C                             */
+} eas_hip_gemm_shape;
+
+typedef struct eas_hip_gemm_plan {
+  int launch;                 /* 0: the launch covers no element of C; nothing runs     */
+  int entry;                  /* eas_hip_gemm_entry to launch                            */
+  uint32_t grid[3], block[3]; /* workgroups and threads per workgroup                    */
+  uint32_t hidden[4];         /* the covered rectangle: m_lo, m_hi, n_lo, n_hi           */
+} eas_hip_gemm_plan;
+
+/* Parse the `// eas-gemm:` marker line of a lifted GEMM's source.  No GPU needed. */
+int eas_hip_gemm_shape_parse(const char* src, eas_hip_gemm_shape* out);
+
+/* Attach a GEMM shape to a kernel with a GEMM launch shape, resolving every entry
+ * point it names in the kernel's code object. */
+int eas_hip_kernel_set_gemm(eas_hip_kernel* k, const eas_hip_gemm_shape* gemm);
+
+/* The launch plan of a lifted GEMM for a reference-convention launch, without
+ * launching (no GPU needed).  `size`, `tptg` and `by_groups` as for
+ * eas_hip_plan_dispatch; the grid must consist of whole threadgroups.  `kernarg`
+ * holds the kernel's own arguments (M, N, the tile bases and the A and B pointers
+ * are read from it), `arg_bytes[i]` the byte length of the buffer behind argument i
+ * (nargs entries).  The launch covers rows [m_lo, m_hi) and columns [n_lo, n_hi):
+ * the origin is tm * row_base (tn * col_base) when the kernel offsets its threadgroup
+ * ids by a scalar, the extent the launched grid, clamped to M (N) when the kernel
+ * bounds rows (columns).  A launch that would read or write past a buffer, or whose
+ * matrices exceed u32 indexing, is EAS_HIP_ERR_INVALID.  `choice` names the entry
+ * ("auto", "8wave", "tile128", "tile128x256", "tile128x64", "tile64", "4wave");
+ * NULL reads EAS_HIP_GEMM_ENTRY (default "auto"). */
+int eas_hip_plan_gemm(const eas_hip_launch_shape* shape, const eas_hip_gemm_shape* gemm, const void* kernarg,
+                      size_t kernarg_size, const uint64_t* arg_bytes, int nargs, int by_groups,
+                      const uint64_t size[3], const uint32_t tptg[3], int compute_units, const char* choice,
+                      eas_hip_gemm_plan* out);
+
 /* Enqueue `repeat` >= 1 launches by the reference's conventions: `kernarg` holds the
  * kernel's own arguments only (shape->arg_bytes when known); the hidden extents are
- * appended here.  Asynchronous.  Replaces `launch` / `launch_async`
- * (_metal.mm:1013-1222, 1381-1383) and `launch_tg` / `launch_tg_async`
- * (_metal.mm:1232-1379).  Needs a kernel with an SPMD or thread-mode shape. */
+ * appended here.  `arg_bytes` (nargs entries, one per kernel argument: the byte length
+ * of a buffer, 0 for a scalar) stands for the lengths the reference's buffer objects
+ * carry; a lifted GEMM needs it to check its extents and rejects NULL, the other kinds
+ * ignore it.  Asynchronous.  Replaces `launch` / `launch_async` (_metal.mm:1013-1222,
+ * 1381-1383) and `launch_tg` / `launch_tg_async` (_metal.mm:1232-1379). */
 int eas_hip_launch_threads(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
-                           const uint64_t threads_per_grid[3], const uint32_t threads_per_threadgroup[3],
-                           void* stream, int repeat);
+                           const uint64_t* arg_bytes, int nargs, const uint64_t threads_per_grid[3],
+                           const uint32_t threads_per_threadgroup[3], void* stream, int repeat);
 int eas_hip_launch_threadgroups(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size,
-                                const uint64_t threadgroups[3], const uint32_t threads_per_threadgroup[3],
-                                void* stream, int repeat);
+                                const uint64_t* arg_bytes, int nargs, const uint64_t threadgroups[3],
+                                const uint32_t threads_per_threadgroup[3], void* stream, int repeat);
 
 /* Enqueue `repeat` >= 1 launches of `k` on `stream` with a packed kernel-argument
  * blob (arguments at natural alignment, in the kernel's parameter order, then the
  * hidden u32 extents).  grid = workgroup counts, block = threads per workgroup.
- * Asynchronous.  The HIP-level dispatch under both reference launch forms: the
- * Python runtime plans every launch itself (a lifted GEMM's plan needs its
- * matrix sizes) and uses this one.  When the kernel's shape knows its argument
- * bytes, a blob of any other size is EAS_HIP_ERR_INVALID. */
+ * Asynchronous.  The HIP-level dispatch under both reference launch forms; the
+ * Python runtime plans its launches itself and uses this one (with a lifted GEMM
+ * entry point `k` loaded by that entry's name).  When the kernel's shape knows its
+ * argument bytes, a blob of any other size is EAS_HIP_ERR_INVALID. */
 int eas_hip_launch(const eas_hip_kernel* k, const void* kernarg, size_t kernarg_size, const uint32_t grid[3],
                    const uint32_t block[3], uint32_t dynamic_lds, void* stream, int repeat);
 

@@ -14,6 +14,8 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+import eas
+
 ROOT = Path(__file__).resolve().parents[1]
 sys.path.insert(0, str(ROOT))
 
@@ -153,6 +155,22 @@ def test_stamped_ws_source_stamps_only_its_entry(mnk, entry):
     with pytest.raises(RuntimeError, match="unexpected f16 GEMM source shape"):
         bench._stamped_ws_source(ck.src.replace("  __syncthreads();  // stage 0 landed\n  afrag_t", "  afrag_t"),
                                  entry)
+
+
+@pytest.mark.parametrize("mnk, entry", [((2048, 2048, 2048), "matmul_mma_kernel__t128"),
+                                        ((512, 14336, 1024), "matmul_mma_kernel__t128x256"),
+                                        ((2048, 1024, 2048), "matmul_mma_kernel__t128x64")])
+def test_stamped_ws_source_under_the_32x32_mfma(monkeypatch, mnk, entry):
+    # EAS_HIP_GEMM_MFMA=32 changes the 128 x 128 and 128 x 256 entries' body; the stamps follow it
+    monkeypatch.setenv("EAS_HIP_GEMM_MFMA", "32")
+    z = np.zeros(1, np.float16)
+    m, n, k = mnk
+    ck = eas.kernel(K.matmul_mma_kernel.fn).compile(z, z, np.zeros(1, np.float32), m, n, BM=32, BN=32, BK=8, K=k,
+                                                    NT=512)
+    assert "eas_gemm_t128<CT, K, 128, 32>" in ck.src
+    src = bench._stamped_ws_source(ck.src, entry)
+    assert src.count("EAS_WS_STAMP(0);") == 1 and src.count(", nullptr);") == 3
+    assert src.count(f"eas_gemm_t128<CT, K, {128 if entry.endswith('t128') else 256}, 32>") >= 1
 
 
 @pytest.mark.gpu

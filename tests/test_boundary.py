@@ -117,11 +117,17 @@ def test_launch_convention_errors(hip):
             hip.plan_dispatch(spmd.src, bad, (1, 1, 1))
     with pytest.raises(ValueError, match="2\\^32"):
         hip.plan_dispatch(thread.src, 1 << 33, 256)
-    # a lifted GEMM's plan needs its matrix sizes: the reference form is refused, with the way to launch it
+    # threadgroup counts whose thread total would wrap a u64 are refused, not truncated
+    for groups in ((1 << 54) // 256 * 256, (1 << 56) + 3, (1 << 32) // 256):
+        with pytest.raises(ValueError, match="2\\^32"):
+            hip.plan_dispatch(thread.src, groups, 256, by_groups=True)
+    most = ((1 << 32) - 1) // 256
+    assert hip.plan_dispatch(thread.src, most, 256, by_groups=True) == ((most, 1, 1), (256, 1, 1), (most * 256,))
+    # a lifted GEMM's plan reads M, N and its buffers from argv
     h = np.zeros(8, np.float16)
     gemm = K.matmul_mma_kernel.compile(h, h, f, 300, 520, BM=32, BN=32, BK=8, K=200, NT=512)
     assert gemm.geometry.kind == "gemm"
-    with pytest.raises(ValueError, match="launch_groups"):
+    with pytest.raises(TypeError, match="argv"):
         hip.plan_dispatch(gemm.src, (17 * 512, 10, 1), (512, 1, 1))
     # a source without an eas-launch line has no shape
     with pytest.raises(ValueError, match="eas-launch"):

@@ -10,6 +10,8 @@ this backend emits instead of the Metal text:
 * ``tests/test_dot_codegen_unique_vars.py``  repeated dot groups do not redeclare their index variables
 * ``tests/test_matmul_tiled.py:126``         the literal tiled lowering reads four B columns with one vector load
 * ``tests/test_mma_codegen.py:34-39``        the MMA kernel lowers to MFMA
+* ``tests/test_threadgroup_memory.py:60-75`` the barrier of a masked threadgroup copy is never inside a mask guard
+* ``tests/test_dot_dynamic_k.py:52-59``      a ``dot`` over a runtime K is a loop over K, not unrolled
 
 The last test compiles every emitted source with hiprtc for gfx950 (no GPU is
 needed for that), which is what proves a redeclaration or any other C++ error
@@ -359,3 +361,55 @@ def test_bf16_sources_compile_for_gfx950():
     mod = load_hip_ext(require=True)
     for name, src in _bf16_sources():
         assert mod.compile_to_code(src, f"{name}.hip", list(COMPILE_OPTIONS))[:4] == b"\x7fELF", name
+
+
+def _kernel_body(src: str, name: str) -> list[str]:
+    """The lines of kernel ``name``'s body (after its opening brace, up to its closing one)."""
+    lines = src.splitlines()
+    start = next(i for i, x in enumerate(lines) if re.search(rf"\b{name}\(", x) and "__global__" in x)
+    while not lines[start].rstrip().endswith("{"):
+        start += 1
+    body, depth = [], 1
+    for x in lines[start + 1:]:
+        depth += x.count("{") - x.count("}")
+        if depth <= 0:
+            break
+        body.append(x)
+    return body
+
+
+@pytest.mark.parametrize("n", [515, 256 * 2 + 3, 7])
+def test_barrier_of_a_masked_tg_copy_is_never_inside_a_mask_guard(n):
+    # reference: tests/test_threadgroup_memory.py:60-75 (the masked copy at N = 2*256 + 3).  Every
+    # thread of a workgroup must reach __syncthreads(): it sits at function scope (brace depth 1),
+    # no statement before it returns early, and the masked lanes are predicated instead.
+    a = np.zeros(n, np.float32)
+    ck = K.tg_copy_kernel.compile(a, np.empty_like(a), n, BLOCK=256)
+    assert ck.launch_mode == "thread" and ck.writes == frozenset({"out"})
+    body = _kernel_body(ck.src, "tg_copy_kernel")
+    depth, barriers = 1, 0
+    for x in body:
+        if "__syncthreads()" in x:
+            barriers += 1
+            assert depth == 1 and x.startswith("  __syncthreads();"), x
+        if barriers == 0:
+            assert not re.search(r"\breturn\b", x), f"early return before the barrier: {x}"
+        depth += x.count("{") - x.count("}")
+    assert barriers == 1
+    # the masked store and load stay guarded per thread
+    assert any(re.match(r"\s+if \(.*\) \{ out\[", x) for x in body)
+    assert re.search(r"__shared__ .*float v\d+\[256\];", "\n".join(body))
+
+
+def test_dot_over_a_runtime_k_is_a_loop_not_unrolled():
+    # reference: tests/test_dot_dynamic_k.py:52-59 (gemv with K a runtime scalar, M = 8, K = 11)
+    a, x, y = np.zeros(88, np.float32), np.zeros(11, np.float32), np.zeros(8, np.float32)
+    ck = K.gemv_dot_kernel.compile(a, x, y, 8, 11, 8, BLOCK=64)
+    body = "\n".join(_kernel_body(ck.src, "gemv_dot_kernel"))
+    loop = re.search(r"for \(uint32_t (k\d+) = 0; \1 < K; \+\+\1\)", body)
+    assert loop, body
+    # one fma in the loop body, whatever K is: the same source serves every K
+    assert body.count("__builtin_fmaf") == 1
+    for k in (7, 31, 64, 4096):
+        other = K.gemv_dot_kernel.compile(np.zeros(8 * k, np.float32), np.zeros(k, np.float32), y, 8, k, 8, BLOCK=64)
+        assert other.src == ck.src

@@ -130,11 +130,82 @@ def test_calls_shaped_for_another_convention_are_refused(hip):
     with pytest.raises(ValueError, match="does not match"):
         hip.launch_groups(pipeline, argv, writable, (10, 1, 1), (32, 1, 1))
     assert hip.kernel_shape(pipeline)["kind"] == "spmd"
-    # a lifted GEMM runs only through the workgroup form (its plan needs M, N, K)
+    # a lifted GEMM: a partial threadgroup, a buffer too short for the launch
     ha, hb = np.zeros(64 * 64, np.float16), np.zeros(64 * 64, np.float16)
     hc = np.zeros(64 * 64, np.float32)
     gk = K.matmul_mma_kernel.compile(ha, hb, hc, 64, 64, BM=32, BN=32, BK=8, K=64, NT=512)
     gp = hip.compile(gk.src, gk.geometry.entry)
     gargv, gw, _ = _argv(hip, gk, {"a": ha, "b": hb, "c": hc, "M": 64, "N": 64})
-    with pytest.raises(ValueError, match="launch_groups"):
-        hip.launch(gp, gargv, gw, (2 * 512, 2, 1), (512, 1, 1))
+    with pytest.raises(ValueError, match="whole threadgroups"):
+        hip.launch(gp, gargv, gw, (2 * 512 - 64, 2, 1), (512, 1, 1))
+    short, _, _ = _argv(hip, gk, {"a": ha[:-1], "b": hb, "c": hc, "M": 64, "N": 64})
+    with pytest.raises(ValueError, match="holds"):
+        hip.launch(gp, short, gw, (2 * 512, 2, 1), (512, 1, 1))
+
+
+# The reference's matmul kernels through the reference's launch, as metal.py:142-346 drives it:
+# compile(src, name) once, argv of buffer capsules and packed scalars, launch with threads per
+# grid (gx * BLOCK, gy, 1) and (BLOCK, 1, 1), or launch_tg with the threadgroup counts.  The
+# library plans the lifted GEMM (entry, workgroups, covered rectangle) from M, N and the buffers.
+# Every output against a float64 matmul of the same inputs: <= 1e-5 sqrt(K) relative to max|R|
+# (f16 products are exact in f32; the fp32 tiled bar of the configs).
+_REF_MATMULS = [
+    # (kernel, M, N, K, form)
+    ("mma", 4096, 4096, 4100, "launch"),
+    ("mma", 4096, 4096, 4096, "launch_tg"),
+    ("mma", 300, 520, 200, "launch"),
+    ("mma", 257, 264, 72, "async"),
+    ("mma", 16, 14336, 4096, "launch_tg"),
+    ("mma", 1024, 1024, 1024, "launch"),
+    ("tiled", 1024, 1024, 1024, "launch"),
+    ("tiled", 1024, 1024, 1024, "launch_tg"),
+    ("tiled", 300, 200, 64, "async"),
+]
+
+
+@pytest.mark.parametrize("case", _REF_MATMULS, ids=lambda c: f"{c[0]}-{c[1]}x{c[2]}x{c[3]}-{c[4]}")
+def test_lifted_matmuls_through_reference_launch(hip, case):
+    import math
+
+    import torch
+
+    kind, m, n, k, form = case
+    rng_a, rng_b = np.random.default_rng(0), np.random.default_rng(1)
+    if kind == "mma":
+        a = rng_a.uniform(-1, 1, m * k).astype(np.float16)
+        b = rng_b.uniform(-1, 1, k * n).astype(np.float16)
+        c = np.full(m * n, np.nan, np.float32)
+        ck = K.matmul_mma_kernel.compile(a, b, c, m, n, BM=32, BN=32, BK=8, K=k, NT=512)
+        args = {"a": a, "b": b, "c": c, "M": m, "N": n}
+        grid = K.mma_grid({"BM": 32, "BN": 32}, args)
+    else:
+        a = (rng_a.standard_normal(m * k, dtype=np.float32) / np.float32(math.sqrt(k))).astype(np.float32)
+        b = (rng_b.standard_normal(k * n, dtype=np.float32) / np.float32(math.sqrt(k))).astype(np.float32)
+        c = np.full(m * n, np.nan, np.float32)
+        ck = K.matmul_tiled_kernel.compile(a, b, c, m, n, 0, 0, BM=32, BN=32, BK=32, K=k, NT=256)
+        args = {"a": a, "b": b, "c": c, "M": m, "N": n, "PID_M_BASE": 0, "PID_N_BASE": 0}
+        grid = (K.cdiv(n, 32), K.cdiv(m, 32), 1)
+    assert ck.geometry.kind == "gemm"
+    print(f"reference launch of the lifted {kind} matmul {m}x{n}x{k} by {form}", flush=True)
+    _run(hip, ck, args, grid=grid, form=form)
+    ref = torch.from_numpy(a).cuda().double().reshape(m, k) @ torch.from_numpy(b).cuda().double().reshape(k, n)
+    got = torch.from_numpy(c).cuda().double().reshape(m, n)
+    assert bool(torch.isfinite(got).all())
+    err = float((got - ref).abs().max() / ref.abs().max())
+    assert err <= 1e-5 * math.sqrt(k), err
+
+
+def test_lifted_matmul_launch_covering_no_output_runs_nothing(hip):
+    # the tiled kernel offsets its threadgroup ids by PID_M_BASE: a base past M covers no row of C
+    m, n, k = 96, 64, 32
+    a, b = np.ones(m * k, np.float32), np.ones(k * n, np.float32)
+    c = np.full(m * n, 7.0, np.float32)
+    ck = K.matmul_tiled_kernel.compile(a, b, c, m, n, 0, 0, BM=32, BN=32, BK=32, K=k, NT=256)
+    args = {"a": a, "b": b, "c": c, "M": m, "N": n, "PID_M_BASE": 3, "PID_N_BASE": 0}
+    _run(hip, ck, args, grid=(2, 3, 1), form="launch")
+    assert np.all(c == 7.0)
+    # the rows from base 1 on: rows 32-95 hold K, rows 0-31 are untouched
+    args["PID_M_BASE"] = 1
+    _run(hip, ck, args, grid=(2, 3, 1), form="launch_tg")
+    out = c.reshape(m, n)
+    assert np.all(out[:32] == 7.0) and np.all(out[32:] == float(k))

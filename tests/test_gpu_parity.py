@@ -540,11 +540,53 @@ def test_in_flight_limit_bounds_pending_launches(monkeypatch, limit):
         assert max(seen) == limit and seen[:limit] == list(range(1, limit + 1))
     else:
         assert seen == list(range(1, 17))
+    # launches share completion events in batches of at most min(16, limit) launches, so waiting
+    # on the oldest pending launch waits for at most `limit` launches and leaves the rest in flight
+    mod = rt._mod()
+    for p in rt._pending:
+        info = mod.pending_info(p)
+        if not info["released"]:
+            assert info["limit"] == (min(16, limit) if limit else 16) and info["launches"] <= info["limit"], info
     rt.synchronize()
     assert len(rt._pending) == 0
     want = ops.add_f32(a, b)
     for o in outs:
         assert _bits_equal(o.numpy(), want)
+
+
+def test_async_batches_close_when_the_stream_changes(gpu_runtime):
+    """A completion batch belongs to one stream and is closed (its event recorded) as soon as an
+    async launch arrives on another stream, so it is never recorded on a stream long after its
+    last launch; launches on both streams complete, bit-exact."""
+    import torch
+
+    hip = gpu_runtime._mod()
+    n = 1 << 16
+    a, b = seeded_normal(0, n), seeded_normal(1, n)
+    ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    outs = [torch.zeros(n, device="cuda") for _ in range(6)]
+    ck = K.add_kernel.compile(ta, tb, outs[0], n, BLOCK=256)
+    side = torch.cuda.Stream()
+    gpu_runtime.synchronize()  # no batch left open by earlier launches
+    torch.cuda.synchronize()
+    pend = []
+    for i, o in enumerate(outs):
+        with torch.cuda.stream(side if i % 3 == 2 else torch.cuda.current_stream()):
+            gpu_runtime.run(ck, {"a": ta, "b": tb, "c": o, "N": n}, {"BLOCK": 256}, sync=False)
+        pend.append(gpu_runtime._pending[-1])
+    infos = [hip.pending_info(p) for p in pend]
+    # launches 0-1 on the main stream, 2 on the side stream, 3-4 main, 5 side: each stream switch
+    # closed the batch before it
+    assert [i["launches"] for i in infos] == [2, 2, 1, 2, 2, 1]
+    assert all(i["closed"] for i in infos[:5]) and not infos[5]["closed"]
+    assert len({i["stream"] for i in infos}) == 2
+    with pytest.raises(ValueError, match="batch"):
+        hip.launch_groups_async(gpu_runtime.kernel_handle(ck), [], [], (1, 1, 1), (64, 1, 1), batch=0)
+    gpu_runtime.synchronize()
+    torch.cuda.synchronize()
+    want = ops.add_f32(a, b)
+    for o in outs:
+        assert _bits_equal(o.cpu().numpy(), want)
 
 
 def test_launches_follow_torch_current_stream(gpu_runtime):

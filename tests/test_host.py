@@ -363,8 +363,9 @@ class _RecordingExt:
     def launch_groups(self, kernel, argv, writable, grid, block, stream=None):
         self.launches.append((kernel, list(argv), list(writable), grid, block))
 
-    def launch_groups_async(self, kernel, argv, writable, grid, block, stream=None):
+    def launch_groups_async(self, kernel, argv, writable, grid, block, stream=None, batch=16):
         self.launch_groups(kernel, argv, writable, grid, block, stream)
+        self.batches = getattr(self, "batches", []) + [batch]
         return ("pending", len(self.launches))
 
     def synchronize(self, pending):

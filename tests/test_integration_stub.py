@@ -54,3 +54,25 @@ def test_stub_runs_add_bit_exact():
     b = np.random.default_rng(1).standard_normal(n, dtype=np.float32)
     c = ns["run_add"](abi, a, b)
     assert np.array_equal(c.view(np.uint32), ops.add_f32(a, b).view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_stub_runs_lifted_matmul():
+    # the reference's simdgroup-MMA matmul, lifted to the MFMA GEMM, through the bare C ABI's
+    # reference-convention launch; every output against float64 (f16 products are exact in f32)
+    import importlib
+    import math
+
+    import kernels as K
+
+    importlib.import_module("easy_as_amd.runtime.hip_ext")._share_process_hip_runtime()
+    ns = _stub()
+    abi = ns["HipABI"](str(ROOT / "easy_as_amd" / "libeas_hip.so"))
+    for m, n, k in ((300, 520, 200), (512, 1024, 4100)):
+        a = np.random.default_rng(0).uniform(-1, 1, m * k).astype(np.float16)
+        b = np.random.default_rng(1).uniform(-1, 1, k * n).astype(np.float16)
+        ck = K.matmul_mma_kernel.compile(a, b, np.zeros(1, np.float32), m, n, BM=32, BN=32, BK=8, K=k, NT=512)
+        assert ck.geometry.kind == "gemm"
+        c = ns["run_matmul"](abi, ck, a, b, m, n).reshape(m, n)
+        ref = a.astype(np.float64).reshape(m, k) @ b.astype(np.float64).reshape(k, n)
+        assert float(np.abs(c - ref).max() / np.abs(ref).max()) <= 1e-5 * math.sqrt(k)
