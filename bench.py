@@ -368,8 +368,8 @@ def _stamped_pp_source(src: str, entry: str) -> str:
          + "  EAS_STAMP(0);\n  EAS_STAMP_XCD();\n"),
         ("    if (g == 1) __syncthreads();\n    for (int kt = 0; kt < KT; ++kt) stage(kt, kt % NSTAGE, b_fast);",
          "    if (g == 1) __syncthreads();\n    EAS_STAMP(1);\n    for (int kt = 0; kt < KT; ++kt) stage(kt, kt % NSTAGE, b_fast);"),
-        ("  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier\n",
-         "  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier\n  EAS_STAMP(2);\n"),
+        ("  // the K loop is done: no LDS is read or written below\n",
+         "  // the K loop is done: no LDS is read or written below\n  EAS_STAMP(2);\n"),
         ("(CT)acc16[i][j][r];\n        }\n  }\n}\n\n// Guard body",
          "(CT)acc16[i][j][r];\n        }\n  }\n  EAS_STAMP(3);\n  __builtin_amdgcn_s_waitcnt(0);\n"
          "  EAS_STAMP(4);\n}\n\n// Guard body"),

@@ -496,7 +496,8 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
   // and b(2kt+2) and by group 1 between b(2kt+2) and b(2kt+3).  Every wave waits for its own DMA
   // of stage kt+1 before b(2kt+2): group 0 at the end of its MFMA phase, group 1 at the end of its
   // load phase.  Stage kt+3 refills the buffer of stage kt-1, whose last reader (group 1) passed
-  // b(2kt) before any wave issues that DMA.  Both groups execute the same number of barriers.
+  // b(2kt) before any wave issues that DMA.  Both groups execute the same number of barriers: group 1
+  // one more before the loop, group 0 one more at the end of its last MFMA phase.
   // one stage of the K loop (s = kt % NSTAGE)
   auto stage = [&](const int kt, const int s, auto b_fast) {
     const int later = KT - 2 - kt < NSTAGE - 2 ? KT - 2 - kt : NSTAGE - 2;
@@ -555,7 +556,9 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
     }
     if (g == 0 && kt + 1 < KT) wait_stage(later);
     __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
+    // group 1's barrier after its last MFMA phase would only pair with one more of group 0's:
+    // both are left out (the counts stay equal), so group 0's C stores overlap that phase
+    if (g == 0 || kt + 1 < KT) __syncthreads();
   };
   auto k_loop = [&](auto b_fast) {
 #pragma unroll
@@ -572,7 +575,7 @@ static __device__ __forceinline__ void eas_gemm_pp(const eas_op_t* __restrict__ 
     k_loop(eas_bool_c<true>{});
   else
     k_loop(eas_bool_c<false>{});
-  if (g == 0) __syncthreads();  // pairs with group 1's last MFMA-phase barrier
+  // the K loop is done: no LDS is read or written below
   const bool full = (m0 + BM <= M) && (n0 + BN <= N);
   if constexpr (MI == 32) {
     // lane l, register r of a 32x32 tile holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32)
