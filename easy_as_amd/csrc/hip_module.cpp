@@ -900,6 +900,273 @@ PyObject* py_launch_timed(PyObject*, PyObject* args, PyObject* kwargs) {
   return PyFloat_FromDouble((double)ms);
 }
 
+// ---- the call memo's launch, in one native call ---------------------------------------
+//
+// A repeated eas call with the same argument types (torch GPU tensors and Python scalars, no
+// launch options) launches what its first call planned, but on the arguments it is given now.
+// fast_make records, per argument, what the first call's specialisation expects; fast_call
+// checks the new arguments against it (exact types, the tensor's dtype object, is_cuda,
+// contiguity), packs the device pointers and scalars, plans the dispatch from N as launch_tg
+// would (cached for the last N), launches on torch's current stream of the last tensor's device
+// and, when asynchronous, returns a pending capsule of the stream's batch.  Any argument it does
+// not take returns NotImplemented before anything is launched, and the caller takes its full
+// path, which launches or raises as it always does.
+
+enum FastKind { kFastTensor = 0, kFastU32 = 1, kFastF32 = 2, kFastBool = 3 };
+
+struct FastArg {
+  int kind;
+  PyObject* expect;  // tensor: its dtype object; scalar: its Python type (owned)
+  uint32_t offset;   // byte offset in the packed arguments
+};
+
+struct Fast {
+  PyObject* kernel = nullptr;       // kernel capsule (owned)
+  eas_hip_kernel* k = nullptr;
+  eas_hip_launch_shape shape{};
+  std::vector<FastArg> args;
+  int n_index = -1;                 // position of the u32 argument N
+  bool by_groups = true;            // SPMD: N lanes are ceil(N / BLOCK) programs; thread mode: N threads
+  bool sync = true;
+  int batch = kBatchLaunches;
+  PyObject* tensor_type = nullptr;  // torch.Tensor (owned)
+  PyObject* raw_stream = nullptr;   // callable: device index -> current raw stream (owned)
+  bool have_plan = false;
+  uint64_t plan_n = 0;
+  uint32_t grid[3] = {1, 1, 1}, block[3] = {1, 1, 1}, hidden[EAS_HIP_MAX_HIDDEN] = {};
+};
+
+const char* kFastCap = "eas._hip.fast";
+
+void free_fast(Fast* f) {
+  Py_XDECREF(f->kernel);
+  Py_XDECREF(f->tensor_type);
+  Py_XDECREF(f->raw_stream);
+  for (auto& a : f->args) Py_XDECREF(a.expect);
+  delete f;
+}
+
+void fast_destructor(PyObject* cap) {
+  auto* f = static_cast<Fast*>(PyCapsule_GetPointer(cap, kFastCap));
+  if (!f) {
+    PyErr_Clear();
+    return;
+  }
+  free_fast(f);
+}
+
+// fast_make(kernel, specs, n_index, sync, batch, tensor_type, raw_stream) -> fast capsule.
+// specs: one (kind, expect) per kernel argument, kind 0 tensor (expect: its torch dtype),
+// 1 u32 (int), 2 f32 (float), 3 bool; the kernel must have an SPMD or thread-mode launch shape.
+PyObject* py_fast_make(PyObject*, PyObject* args) {
+  PyObject *kcap, *specs, *tensor_type, *raw_stream;
+  int n_index, sync, batch;
+  if (!PyArg_ParseTuple(args, "OOipiOO", &kcap, &specs, &n_index, &sync, &batch, &tensor_type, &raw_stream))
+    return nullptr;
+  eas_hip_kernel* k = as_kernel(kcap);
+  if (!k) return nullptr;
+  eas_hip_launch_shape s;
+  int rc = eas_hip_kernel_get_shape(k, &s);
+  if (rc) return raise_status(rc);
+  if (s.kind != EAS_HIP_KIND_SPMD && s.kind != EAS_HIP_KIND_THREAD) {
+    PyErr_SetString(PyExc_ValueError, "fast_make: the kernel needs an SPMD or thread-mode launch shape");
+    return nullptr;
+  }
+  if (batch < 1 || batch > kBatchLaunches || !PyCallable_Check(raw_stream)) {
+    PyErr_SetString(PyExc_ValueError, "fast_make: bad batch or stream getter");
+    return nullptr;
+  }
+  PyObject* seq = PySequence_Fast(specs, "specs must be a sequence");
+  if (!seq) return nullptr;
+  auto* f = new Fast;
+  f->shape = s;
+  uint32_t off = 0;
+  bool ok = true;
+  const Py_ssize_t n = PySequence_Fast_GET_SIZE(seq);
+  for (Py_ssize_t i = 0; ok && i < n; ++i) {
+    int kind;
+    PyObject* expect;
+    if (!PyArg_ParseTuple(PySequence_Fast_GET_ITEM(seq, i), "iO", &kind, &expect)) {
+      ok = false;
+      break;
+    }
+    const uint32_t size = kind == kFastTensor ? 8 : kind == kFastBool ? 1 : 4;
+    if (kind < kFastTensor || kind > kFastBool) {
+      PyErr_SetString(PyExc_ValueError, "fast_make: unknown argument kind");
+      ok = false;
+      break;
+    }
+    off = (off + size - 1) / size * size;
+    Py_INCREF(expect);
+    f->args.push_back({kind, expect, off});
+    off += size;
+  }
+  Py_DECREF(seq);
+  if (ok && (n_index < 0 || n_index >= (int)f->args.size() || f->args[n_index].kind != kFastU32)) {
+    PyErr_SetString(PyExc_ValueError, "fast_make: N must be a u32 argument");
+    ok = false;
+  }
+  if (ok && s.arg_bytes && off != s.arg_bytes) {
+    PyErr_Format(PyExc_ValueError, "fast_make: %u bytes of arguments, the kernel takes %u", off, s.arg_bytes);
+    ok = false;
+  }
+  if (!ok) {
+    free_fast(f);
+    return nullptr;
+  }
+  f->n_index = n_index;
+  f->by_groups = s.kind == EAS_HIP_KIND_SPMD;
+  f->sync = sync != 0;
+  f->batch = batch;
+  Py_INCREF(kcap);
+  f->kernel = kcap;
+  f->k = k;
+  Py_INCREF(tensor_type);
+  f->tensor_type = tensor_type;
+  Py_INCREF(raw_stream);
+  f->raw_stream = raw_stream;
+  PyObject* cap = PyCapsule_New(f, kFastCap, fast_destructor);
+  if (!cap) free_fast(f);
+  return cap;
+}
+
+PyObject* g_s_dtype = nullptr;
+PyObject* g_s_is_cuda = nullptr;
+PyObject* g_s_is_contiguous = nullptr;
+PyObject* g_s_data_ptr = nullptr;
+PyObject* g_s_get_device = nullptr;
+
+// The boolean result of calling obj.name(): 1, 0, or -1 on error.
+int call_true(PyObject* obj, PyObject* name) {
+  PyObject* r = PyObject_CallMethodNoArgs(obj, name);
+  if (!r) return -1;
+  int t = r == Py_True;
+  Py_DECREF(r);
+  return t;
+}
+
+// fast_call(fast, args: tuple) -> None (launched and, if synchronous, done), a pending capsule
+// (asynchronous), or NotImplemented (an argument this specialisation's fast path does not take;
+// nothing was launched).
+PyObject* py_fast_call(PyObject*, PyObject* const* argv, Py_ssize_t nargv) {
+  if (nargv != 2 || !PyTuple_Check(argv[1])) {
+    PyErr_SetString(PyExc_TypeError, "fast_call(fast, args: tuple)");
+    return nullptr;
+  }
+  auto* f = static_cast<Fast*>(PyCapsule_GetPointer(argv[0], kFastCap));
+  if (!f) return nullptr;
+  PyObject* args = argv[1];
+  const size_t n = f->args.size();
+  if ((size_t)PyTuple_GET_SIZE(args) != n) Py_RETURN_NOTIMPLEMENTED;
+  uint8_t blob[512];
+  const size_t arg_bytes = f->shape.arg_bytes, total = (arg_bytes + 3) / 4 * 4 + 4 * (size_t)f->shape.hidden;
+  if (total > sizeof(blob)) Py_RETURN_NOTIMPLEMENTED;
+  memset(blob, 0, total);
+  PyObject* last_tensor = nullptr;
+  uint64_t nval = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const FastArg& a = f->args[i];
+    PyObject* obj = PyTuple_GET_ITEM(args, (Py_ssize_t)i);
+    if (a.kind == kFastTensor) {
+      if (Py_TYPE(obj) != (PyTypeObject*)f->tensor_type) Py_RETURN_NOTIMPLEMENTED;
+      PyObject* dt = PyObject_GetAttr(obj, g_s_dtype);
+      if (!dt) return nullptr;
+      Py_DECREF(dt);  // dtypes are singletons held by torch; only their identity is compared
+      if (dt != a.expect) Py_RETURN_NOTIMPLEMENTED;
+      PyObject* cuda = PyObject_GetAttr(obj, g_s_is_cuda);
+      if (!cuda) return nullptr;
+      Py_DECREF(cuda);
+      if (cuda != Py_True) Py_RETURN_NOTIMPLEMENTED;
+      int contiguous = call_true(obj, g_s_is_contiguous);
+      if (contiguous < 0) return nullptr;
+      if (!contiguous) Py_RETURN_NOTIMPLEMENTED;
+      PyObject* p = PyObject_CallMethodNoArgs(obj, g_s_data_ptr);
+      if (!p) return nullptr;
+      uint64_t ptr = PyLong_AsUnsignedLongLong(p);
+      Py_DECREF(p);
+      if (PyErr_Occurred()) return nullptr;
+      memcpy(blob + a.offset, &ptr, 8);
+      last_tensor = obj;
+      continue;
+    }
+    if ((PyObject*)Py_TYPE(obj) != a.expect) Py_RETURN_NOTIMPLEMENTED;
+    if (a.kind == kFastU32) {
+      unsigned long long v = PyLong_AsUnsignedLongLong(obj);
+      if (PyErr_Occurred() || v > 0xFFFFFFFFull) {
+        PyErr_Clear();  // the full path raises the packing error
+        Py_RETURN_NOTIMPLEMENTED;
+      }
+      const uint32_t u = (uint32_t)v;
+      memcpy(blob + a.offset, &u, 4);
+      if ((int)i == f->n_index) nval = v;
+    } else if (a.kind == kFastF32) {
+      const float x = (float)PyFloat_AS_DOUBLE(obj);
+      memcpy(blob + a.offset, &x, 4);
+    } else {
+      blob[a.offset] = obj == Py_True ? 1 : 0;
+    }
+  }
+  if (!last_tensor) Py_RETURN_NOTIMPLEMENTED;  // without a GPU tensor there is no torch stream to follow
+  if (nval == 0) Py_RETURN_NONE;               // a zero extent launches nothing
+  if (!f->have_plan || f->plan_n != nval) {
+    const uint32_t block = f->shape.block_size;
+    const uint64_t size[3] = {f->by_groups ? (nval + block - 1) / block : nval, 1, 1};
+    static const uint32_t kAuto[3] = {0, 0, 0};
+    int rc = eas_hip_plan_dispatch(&f->shape, f->by_groups, size, kAuto, f->grid, f->block, f->hidden,
+                                   EAS_HIP_MAX_HIDDEN);
+    if (rc) {
+      PyErr_Clear();
+      Py_RETURN_NOTIMPLEMENTED;  // the full path reports the size error
+    }
+    f->plan_n = nval;
+    f->have_plan = true;
+  }
+  memcpy(blob + (arg_bytes + 3) / 4 * 4, f->hidden, 4 * f->shape.hidden);
+  PyObject* dev = PyObject_CallMethodNoArgs(last_tensor, g_s_get_device);
+  if (!dev) return nullptr;
+  PyObject* sobj = PyObject_CallOneArg(f->raw_stream, dev);
+  Py_DECREF(dev);
+  if (!sobj) return nullptr;
+  void* stream = PyLong_AsVoidPtr(sobj);
+  Py_DECREF(sobj);
+  if (PyErr_Occurred()) return nullptr;
+  int rc = eas_hip_launch(f->k, blob, total, f->grid, f->block, 0, stream, 1);
+  if (rc) return raise_status(rc);
+  if (f->sync) {
+    Py_BEGIN_ALLOW_THREADS
+    rc = eas_hip_stream_synchronize(stream);
+    Py_END_ALLOW_THREADS
+    if (rc) return raise_status(rc);
+    Py_RETURN_NONE;
+  }
+  auto* pending = new Pending{nullptr, {}};
+  for (size_t i = 0; i < n; ++i) {
+    if (f->args[i].kind != kFastTensor) continue;
+    PyObject* obj = PyTuple_GET_ITEM(args, (Py_ssize_t)i);
+    Py_INCREF(obj);
+    pending->keepalive.push_back(obj);
+  }
+  Py_INCREF(f->kernel);
+  pending->keepalive.push_back(f->kernel);
+  Batch* b = join_batch(stream, f->batch, &rc);
+  pending->batch = b;
+  if (b->launches >= b->limit) {
+    int crc = close_batch(b);
+    if (!rc) rc = crc;
+  }
+  if (rc) {
+    release_pending(pending);
+    delete pending;
+    return raise_status(rc);
+  }
+  PyObject* cap = PyCapsule_New(pending, kPendingCap, pending_destructor);
+  if (!cap) {
+    release_pending(pending);
+    delete pending;
+  }
+  return cap;
+}
+
 const char* kind_name(int kind) {
   switch (kind) {
     case EAS_HIP_KIND_SPMD: return "spmd";
@@ -1217,6 +1484,9 @@ PyMethodDef kMethods[] = {
     {"launch_timed", (PyCFunction)(void (*)(void))py_launch_timed, METH_VARARGS | METH_KEYWORDS,
      "Event-timed repeat launches; mean ms per launch."},
     {"synchronize", py_synchronize, METH_VARARGS, "Wait for a pending launch and drop its keepalives."},
+    {"fast_make", py_fast_make, METH_VARARGS, "The call memo's native launch for one specialisation."},
+    {"fast_call", (PyCFunction)(void (*)(void))py_fast_call, METH_FASTCALL,
+     "fast_call(fast, args): launch the memoized specialisation, or NotImplemented."},
     {"pending_info", py_pending_info, METH_VARARGS, "Completion batch of a pending launch (stream, launches, closed)."},
     {"queue_synchronize", py_queue_synchronize, METH_VARARGS, "Wait for a stream (default: whole device)."},
     {"dlpack_import", py_dlpack_import, METH_VARARGS, "Zero-copy import of a kDLROCM DLPack capsule."},
@@ -1229,6 +1499,12 @@ PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_hip", "MI355X (gfx950) HIP backe
 }  // namespace
 
 PyMODINIT_FUNC PyInit__hip(void) {
+  g_s_dtype = PyUnicode_InternFromString("dtype");
+  g_s_is_cuda = PyUnicode_InternFromString("is_cuda");
+  g_s_is_contiguous = PyUnicode_InternFromString("is_contiguous");
+  g_s_data_ptr = PyUnicode_InternFromString("data_ptr");
+  g_s_get_device = PyUnicode_InternFromString("get_device");
+  if (!g_s_dtype || !g_s_is_cuda || !g_s_is_contiguous || !g_s_data_ptr || !g_s_get_device) return nullptr;
   PyObject* m = PyModule_Create(&kModule);
   if (m) PyModule_AddIntConstant(m, "ABI_VERSION", eas_hip_abi_version());
   if (m && PyModule_AddObject(m, "DEFAULT_OPTIONS", default_options()) != 0) {

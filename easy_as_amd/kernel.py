@@ -86,6 +86,8 @@ class Kernel:
         self._n_lead = lead
         self._memo_kw = frozenset(self.meta_params) | {"_sync"}
         self._memo: dict[Any, tuple[CompiledKernel, dict[str, Any], bool]] = {}
+        # the runtime's one-native-call launch of a memoized specialisation, by keyword items
+        self._fast: dict[Any, Callable[[tuple[Any, ...]], Any]] = {}
 
     def _set_autotune_spec(self, spec: AutotuneSpec) -> None:
         self._autotune_spec = spec
@@ -255,7 +257,14 @@ class Kernel:
         key = None
         if self._memo_ok and len(args) == self._n_lead and self._autotune_spec is None:
             try:
-                key = (tuple(kwargs.items()), tuple(map(_light_key, args)))
+                kw = tuple(kwargs.items())
+                fast = self._fast.get(kw)
+            except TypeError:  # a keyword value the memo does not key
+                kw = fast = None
+            if fast is not None and fast(args) is not NotImplemented:
+                return
+            try:
+                key = (kw, tuple(map(_light_key, args)))
                 hit = self._memo.get(key)
             except TypeError:  # an argument or keyword value the memo does not key
                 key = hit = None
@@ -264,12 +273,20 @@ class Kernel:
                 get_runtime().run(ck, dict(zip(self._names, args)), meta, sync=sync)
                 return
         ck, meta, runtime_args, opts, raw = self._prepare(args, dict(kwargs))
-        get_runtime().run(ck, runtime_args, meta, **opts)
+        rt = get_runtime()
+        rt.run(ck, runtime_args, meta, **opts)
         if key is not None and kwargs.keys() <= self._memo_kw and all(
                 raw[o] is None for o in ("nthreads", "grid", "shape", "tptg")):
             if len(self._memo) >= _MEMO_LIMIT:
                 self._memo.clear()
             self._memo[key] = (ck, meta, opts["sync"])
+            make = getattr(rt, "fast_launcher", None)
+            if key[0] not in self._fast and callable(make):
+                fast = make(ck, self._names[:self._n_lead], args, opts["sync"])
+                if fast is not None:
+                    if len(self._fast) >= _MEMO_LIMIT:
+                        self._fast.clear()
+                    self._fast[key[0]] = fast
 
     def to_hip(self, /, *args: Any, **kwargs: Any) -> str:
         """The generated gfx950 HIP C++ source for this specialisation (reference: ``to_msl``)."""

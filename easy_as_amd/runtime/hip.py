@@ -24,7 +24,7 @@ from typing import Any, Mapping
 import numpy as np
 
 from ..ir import DType, IRModule
-from .grid import infer_grid, infer_nthreads
+from .grid import grid_ndim, infer_grid, infer_nthreads
 from .hip_ext import load_hip_ext
 
 TARGET_ARCH = "gfx950"
@@ -329,15 +329,68 @@ class HipRuntime:
         self._arg_specs[id(ir)] = (ir, writes, spec)  # holding ir keeps its id unique
         return spec
 
-    def _current_stream(self, device_index: int) -> int:
-        """torch's current stream on a device, as a raw hipStream_t address."""
+    def _stream_getter(self) -> Any:
+        """device index -> torch's current stream on it, as a raw hipStream_t address."""
         raw = self._raw_stream
         if raw is None:
             torch = self._torch_mod()
             raw = getattr(torch._C, "_cuda_getCurrentRawStream", None) or (
                 lambda i: torch.cuda.current_stream(i).cuda_stream)
             self._raw_stream = raw
-        return int(raw(device_index))
+        return raw
+
+    def _current_stream(self, device_index: int) -> int:
+        """torch's current stream on a device, as a raw hipStream_t address."""
+        return int(self._stream_getter()(device_index))
+
+    def fast_launcher(self, ck: Any, names: tuple[str, ...], args: tuple[Any, ...], sync: bool) -> Any:
+        """A one-native-call launch of ``ck`` for later calls shaped like ``args`` (the call memo's
+        hit path), or None when this specialisation does not take one.  It takes SPMD and
+        thread-mode kernels sized by their u32 argument ``N`` (1-D launches) whose arguments are
+        torch GPU tensors and int, float or bool scalars, passed positionally in the kernel's
+        argument order.  The returned callable launches what ``run(ck, ...)`` would launch for
+        ``args`` (same dispatch, kernel arguments, stream and completion batching, and the
+        EAS_MAX_IN_FLIGHT bound) and returns None, or returns NotImplemented without launching
+        when an argument does not match (another type, dtype or device kind, a non-contiguous
+        tensor, a scalar out of range): the caller then takes the full path."""
+        torch = self._torch_mod()
+        geo = ck.geometry
+        if torch is None or geo is None or geo.kind not in ("spmd", "thread") or grid_ndim(ck.ir) > 1:
+            return None
+        mod = self._mod()
+        if not callable(getattr(mod, "fast_make", None)) or tuple(a.name for a in ck.ir.args) != tuple(names):
+            return None
+        scalar_kinds = {DType.U32: (1, int), DType.F32: (2, float), DType.BOOL: (3, bool)}
+        specs, n_index = [], None
+        for i, (a, v) in enumerate(zip(ck.ir.args, args)):
+            if a.kind == "buffer":
+                if type(v) is not torch.Tensor or not v.is_cuda or v.dtype != self._torch_dtypes.get(a.dtype):
+                    return None
+                specs.append((0, v.dtype))
+                continue
+            kind = scalar_kinds.get(a.dtype)
+            if kind is None or type(v) is not kind[1]:
+                return None
+            specs.append(kind)
+            if a.name == "N" and kind[0] == 1:
+                n_index = i
+        if n_index is None:
+            return None
+        limit = self._max_pending()
+        fast = mod.fast_make(self.kernel_handle(ck), specs, n_index, bool(sync), min(16, limit) if limit else 16,
+                             torch.Tensor, self._stream_getter())
+        call, pending, synchronize = mod.fast_call, self._pending, mod.synchronize
+
+        def launch(call_args: tuple[Any, ...]) -> Any:
+            p = call(fast, call_args)
+            if p is None or p is NotImplemented:
+                return p
+            pending.append(p)
+            while limit and len(pending) > limit:
+                synchronize(pending.popleft())
+            return None
+
+        return launch
 
     # -- launching ------------------------------------------------------------------
     def run(

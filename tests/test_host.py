@@ -457,6 +457,51 @@ def test_call_memo_still_rejects_bad_arguments(monkeypatch, tmp_path):
         k(a, a, np.ones(128, np.float32)[::2], 64, BLOCK=64)  # same light key, not contiguous
 
 
+class _FastRuntime:
+    """A runtime with a fast launcher: records full-path runs and fast calls, and declines
+    (NotImplemented) calls whose first argument is the `decline` object."""
+
+    def __init__(self):
+        self.runs, self.fast_calls, self.made = [], [], []
+        self.decline = object()
+
+    def run(self, ck, runtime_args, meta, **opts):
+        self.runs.append((ck, dict(runtime_args), dict(meta), opts))
+
+    def fast_launcher(self, ck, names, args, sync):
+        self.made.append((ck, names, args, sync))
+
+        def launch(call_args):
+            self.fast_calls.append((ck, call_args, sync))
+            return NotImplemented if call_args[0] is self.decline else None
+
+        return launch
+
+
+def test_call_memo_takes_the_runtime_fast_launch(monkeypatch):
+    rt = _FastRuntime()
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    k = eas.kernel(K.add_kernel.fn)
+    a = np.ones(64, np.float32)
+    k(a, a, a, 64, BLOCK=64, _sync=False)
+    # the first call runs the full path and makes the fast launch for its keyword items
+    assert len(rt.runs) == 1 and len(rt.made) == 1 and not rt.fast_calls
+    ck, names, args, sync = rt.made[0]
+    assert names == ("a", "b", "c", "N") and args[3] == 64 and sync is False
+    k(a, a, a, 100, BLOCK=64, _sync=False)
+    assert len(rt.runs) == 1 and rt.fast_calls[-1][1][3] == 100
+    # declined: the memo's full-path launch runs the call
+    b = np.ones(64, np.float32)
+    rt.decline = b
+    k(b, a, a, 64, BLOCK=64, _sync=False)
+    assert len(rt.runs) == 2 and rt.runs[-1][1]["a"] is b and rt.runs[-1][3]["sync"] is False
+    # other keyword items have their own fast launch; options other than _sync never make one
+    k(a, a, a, 64, BLOCK=128, _sync=False)
+    assert len(rt.made) == 2 and set(k._fast) == {(("BLOCK", 64), ("_sync", False)), (("BLOCK", 128), ("_sync", False))}
+    k(a, a, a, 64, BLOCK=32, _grid=(1, 1, 1))
+    assert len(rt.made) == 2
+
+
 class _FillingExt(_RecordingExt):
     """Copies back a fixed byte pattern, so a test sees which host memory a result reaches."""
 
