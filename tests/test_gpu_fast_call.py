@@ -88,11 +88,13 @@ def test_f32_scalar_and_calls_the_fast_launch_declines(gpu_runtime):
     c_np = np.zeros(n, np.float32)
     k(a_np, b_np, c_np, n, 2.0, BLOCK=256)
     assert _bits_equal(c_np, ops.fmaf(a_np, np.float32(2.0), b_np))
-    # another dtype: a new specialisation on the full path
+    # another dtype (f16 tensors, an f16 scalar): a new specialisation on the full path
     h = [torch.from_numpy(x.astype(np.float16)).cuda() for x in (a_np, b_np)]
     hc = torch.zeros(n, dtype=torch.float16, device="cuda")
-    k(h[0], h[1], hc, n, 2.0, BLOCK=256)
-    assert len(k._cache) == 2
+    k(h[0], h[1], hc, n, np.float16(2.0), BLOCK=256)
+    assert len(k._cache) == 3  # f32 GPU tensors, NumPy host arrays, f16 GPU tensors
+    want16 = (a_np.astype(np.float16) * np.float16(2.0)).astype(np.float16) + b_np.astype(np.float16)
+    assert np.allclose(hc.cpu().numpy().astype(np.float32), want16.astype(np.float32), rtol=2e-3, atol=2e-3)
     # the full path's errors: a non-contiguous tensor, a u32 out of range
     with pytest.raises(ValueError, match="contiguous"):
         k(a, b, torch.zeros(2 * n, device="cuda")[::2], n, 2.0, BLOCK=256)
@@ -108,8 +110,11 @@ def test_f32_scalar_and_calls_the_fast_launch_declines(gpu_runtime):
 def test_fast_launches_keep_the_in_flight_bound(monkeypatch):
     import torch
 
+    import importlib
+
     from easy_as_amd.runtime.hip import HipRuntime
-    import easy_as_amd.kernel as eas_kernel
+
+    eas_kernel = importlib.import_module("easy_as_amd.kernel")  # the module, not the kernel() it exports
 
     monkeypatch.setenv("EAS_MAX_IN_FLIGHT", "3")
     rt = HipRuntime()
