@@ -163,6 +163,21 @@ def _interleaved_event_ms(rt, ck, rargs, meta, fn, steps: int, torch, **launch) 
     return sorted(ours)[EVENT_TRIALS // 2], sorted(theirs)[EVENT_TRIALS // 2]
 
 
+def _dispatch_probe(rt, workgroups: int, threads: int, trials: int = EVENT_TRIALS) -> float:
+    """Workgroups per ns the command processor dispatches on this box: an empty kernel of
+    ``workgroups`` workgroups of ``threads`` threads (the add's launch shape), timed with HIP
+    events, 20 launches per trial, median of ``trials``.  An elementwise kernel whose
+    workgroups arrive at close to this rate is bound by dispatch, not by HBM."""
+    from easy_as_amd.runtime.hip import compile_code
+
+    mod = rt._mod()
+    src = 'extern "C" __global__ void eas_dispatch_probe() {}\n'
+    k = mod.load(compile_code(mod, src, "eas_dispatch_probe"), "eas_dispatch_probe")
+    ms = sorted(mod.launch_timed(k, [], [], (workgroups, 1, 1), (threads, 1, 1), repeat=20, warmup=5)
+                for _ in range(trials))[trials // 2]
+    return workgroups / (ms * 1e6)
+
+
 def _torch_event_ms(fn, steps: int, warmup: int, torch) -> float:
     """ms per call of a torch operation on torch's current stream: the median of EVENT_TRIALS
     trials of ``steps`` back-to-back calls between torch events (the vendor comparison), after
@@ -989,7 +1004,7 @@ def main() -> int:
         else:
             exact, parity = True, "not checked (--no-cpu-baseline skips the oracle)"
         geo = ck.geometry
-        res = {"wall_ms": wall_ms, "ev_ms": ev_ms, "GB/s": round(per * N_ELEM / ev_ms / 1e6, 1),
+        res = {"ck": ck, "rargs": rargs, "wall_ms": wall_ms, "ev_ms": ev_ms, "GB/s": round(per * N_ELEM / ev_ms / 1e6, 1),
                "frac": round(per * N_ELEM / ev_ms / 1e6 / HBM_PEAK_GBS, 4), "ms_per_launch": round(ev_ms, 5),
                "parity": parity, "parity_ok": exact,
                "launch": f"{geo.wg_size} threads per workgroup, "
@@ -1001,6 +1016,20 @@ def main() -> int:
 
     prim = elementwise(args.workload, args.block)
     wall_ms, ev_ms, exact, parity = prim["wall_ms"], prim["ev_ms"], prim["parity_ok"], prim["parity"]
+    # the workgroups per ns the kernel needs, beside what this box's command processor dispatches
+    # (an empty kernel of the same launch shape, this session): a box that dispatches slowly shows
+    # here instead of only as a lower bandwidth
+    from easy_as_amd.runtime.hip import plan_launch
+
+    kplan = plan_launch(prim["ck"], prim["rargs"])
+    need = kplan.grid[0] / (ev_ms * 1e6)
+    probe = _dispatch_probe(rt, kplan.grid[0], kplan.block[0])
+    dispatch = {"workgroups": kplan.grid[0], "threads_per_workgroup": kplan.block[0],
+                "kernel_workgroups_per_ns": round(need, 3), "probe_workgroups_per_ns": round(probe, 3),
+                "kernel_over_probe": round(need / probe, 3),
+                "probe": "empty kernel, same workgroup count and size, HIP events, median of 5 x 20 launches"}
+    _log(f"dispatch: {args.workload} needs {need:.3f} workgroups/ns; an empty kernel of the same shape "
+         f"dispatches {probe:.3f}/ns ({100 * need / probe:.1f} %)")
     # vendor comparison on the same device-resident inputs: the torch (ROCm) operation
     tfn = {"add": lambda: torch.add(ins[0], ins[1], out=out),
            "fma": lambda: torch.addcmul(ins[2], ins[0], ins[1], out=out),
@@ -1016,7 +1045,8 @@ def main() -> int:
         other = 1024 if args.block != 1024 else 256
         for wl, blk in (("add", other), ("fma", 256), ("fma", 1024)):
             r = elementwise(wl, blk)
-            extra[f"{wl}_block{blk}"] = {k: v for k, v in r.items() if k not in ("wall_ms", "ev_ms", "parity_ok")}
+            extra[f"{wl}_block{blk}"] = {k: v for k, v in r.items()
+                                         if k not in ("wall_ms", "ev_ms", "parity_ok", "ck", "rargs")}
             exact = exact and r["parity_ok"]
         cpu_fma = None if args.no_cpu_baseline else _cpu_baseline("fma", hosts)
         if cpu_fma is not None:
@@ -1093,6 +1123,7 @@ def main() -> int:
         "parity": parity,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+        "dispatch": dispatch,
         "cpu_baseline": None if args.no_cpu_baseline else _cpu_baseline(args.workload, hosts[:nin]),
         "vendor": vendor,
         "settle": {"untimed_launches_before_warmup": list(SETTLE_LOG),

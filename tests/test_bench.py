@@ -255,3 +255,14 @@ def test_loadcost_runs(capsys):
     # MFMAs alone run at one per 64 clocks; loads a sibling issues with SGPR addressing are free
     assert 1000 < rows["lc_w4_mfma"]["simd_clocks_per_16_mfma_median"] < 1100
     assert rows["lc_w8_salu_producers2"]["loads_per_16_sibling_mfma"] == 2.0
+
+
+@pytest.mark.gpu
+def test_dispatch_probe_measures_a_rate():
+    # the empty kernel the add line is compared with: 2^21 workgroups of 32 threads (the add's
+    # launch at N = 2^28) dispatch at a few workgroups per ns on one MI355X
+    from easy_as_amd.runtime import get_runtime
+
+    print("dispatch probe", flush=True)
+    rate = bench._dispatch_probe(get_runtime("hip"), 1 << 21, 32, trials=3)
+    assert 1.0 < rate < 50.0, rate
