@@ -312,3 +312,45 @@ def test_reference_dispatch_of_the_lifted_kernels_is_planned(hip):
         plan = plan_launch(ck, args, grid=grid)
         assert hip.plan_dispatch(ck.src, tpg, tptg, argv=_argv(hip, ck, args)) == \
             (plan.grid, plan.block, plan.hidden, plan.entry)
+
+
+def test_random_launches_plan_alike(hip):
+    # 300 seeded random launches: kernel kind, M, N, K, partial and oversized grids, tile bases,
+    # operand alignment, a short buffer now and then, CU count and entry override; both planners
+    # must give the same plan, the same refusal, or both nothing
+    import random
+
+    r = random.Random(7)
+    f = np.zeros(8, np.float32)
+    kernels = {}
+    choices = ("auto", "auto", "auto", "8wave", "tile128", "tile128x256", "tile128x64", "tile64", "4wave")
+    planned = 0
+    for case in range(300):
+        kind = r.choice(("mma", "mma16out", "mma32in", "tiled"))
+        m, n = r.choice((1, 7, 16, 17, 64, 100, 128, 129, 300, 1000, 4096)), r.choice((1, 8, 65, 130, 520, 4096, 16390))
+        k = r.choice((2, 33, 36, 100, 4100))
+        key = (kind, k)
+        if key not in kernels:
+            if kind == "tiled":
+                kernels[key] = K.matmul_tiled_kernel.compile(f, f, f, 64, 64, 0, 0, BM=32, BN=32, BK=32, K=k, NT=256)
+            elif kind == "mma32in":
+                kernels[key] = _mma(k=k, a=np.float32)
+            else:
+                kernels[key] = _mma("matmul_mma_f16out_kernel" if kind == "mma16out" else "matmul_mma_kernel", k,
+                                    np.float16, np.float16 if kind == "mma16out" else np.float32)
+        ck = kernels[key]
+        if ck.geometry is None or ck.geometry.kind != "gemm":
+            continue  # not lifted (the literal lowering runs it): no GEMM plan to compare
+        extra = {}
+        if kind == "tiled":
+            extra = {"PID_M_BASE": r.choice((0, 0, 1, 5)), "PID_N_BASE": r.choice((0, 0, 2, 7))}
+        args = _args(ck, m, n, k, extra=extra, short=r.choice((None,) * 8 + ("a", "b", "c")),
+                     misalign=r.choice((None,) * 6 + ("a", "b")))
+        full = (K.cdiv(n, 32), K.cdiv(m, 32), 1)
+        groups = r.choice((full, full, (max(1, full[0] // 2), full[1], 1), (full[0] + 3, full[1] + 2, 1),
+                           (1, 1, 1)))
+        c, py = _both(hip, ck, args, groups, cus=r.choice((256, 256, 80, 304)), choice=r.choice(choices),
+                      by_groups=r.random() < 0.5)
+        assert _agree(c, py), (case, kind, m, n, k, groups, extra, c, py)
+        planned += 1
+    assert planned > 200
