@@ -907,12 +907,13 @@ PyObject* py_launch_timed(PyObject*, PyObject* args, PyObject* kwargs) {
 // fast_make records, per argument, what the first call's specialisation expects; fast_call
 // checks the new arguments against it (exact types, the tensor's dtype object, is_cuda,
 // contiguity), packs the device pointers and scalars, plans the dispatch from N as launch_tg
-// would (cached for the last N), launches on torch's current stream of the last tensor's device
-// and, when asynchronous, returns a pending capsule of the stream's batch.  Any argument it does
+// would (cached for the last N), launches on torch's current stream of the last torch tensor's
+// device (the default stream when every buffer is an eas.Tensor) and, when asynchronous, returns a
+// pending capsule of the stream's batch.  Any argument it does
 // not take returns NotImplemented before anything is launched, and the caller takes its full
 // path, which launches or raises as it always does.
 
-enum FastKind { kFastTensor = 0, kFastU32 = 1, kFastF32 = 2, kFastBool = 3 };
+enum FastKind { kFastTensor = 0, kFastU32 = 1, kFastF32 = 2, kFastBool = 3, kFastEasTensor = 4 };
 
 struct FastArg {
   int kind;
@@ -930,6 +931,7 @@ struct Fast {
   bool sync = true;
   int batch = kBatchLaunches;
   PyObject* tensor_type = nullptr;  // torch.Tensor (owned)
+  PyObject* eas_type = nullptr;     // eas.Tensor (owned)
   PyObject* raw_stream = nullptr;   // callable: device index -> current raw stream (owned)
   bool have_plan = false;
   uint64_t plan_n = 0;
@@ -941,6 +943,7 @@ const char* kFastCap = "eas._hip.fast";
 void free_fast(Fast* f) {
   Py_XDECREF(f->kernel);
   Py_XDECREF(f->tensor_type);
+  Py_XDECREF(f->eas_type);
   Py_XDECREF(f->raw_stream);
   for (auto& a : f->args) Py_XDECREF(a.expect);
   delete f;
@@ -955,13 +958,15 @@ void fast_destructor(PyObject* cap) {
   free_fast(f);
 }
 
-// fast_make(kernel, specs, n_index, sync, batch, tensor_type, raw_stream) -> fast capsule.
-// specs: one (kind, expect) per kernel argument, kind 0 tensor (expect: its torch dtype),
-// 1 u32 (int), 2 f32 (float), 3 bool; the kernel must have an SPMD or thread-mode launch shape.
+// fast_make(kernel, specs, n_index, sync, batch, tensor_type, raw_stream, eas_type) -> fast capsule.
+// specs: one (kind, expect) per kernel argument, kind 0 torch tensor (expect: its torch dtype),
+// 1 u32 (int), 2 f32 (float), 3 bool, 4 eas.Tensor on the GPU (expect: its NumPy dtype); the kernel
+// must have an SPMD or thread-mode launch shape.
 PyObject* py_fast_make(PyObject*, PyObject* args) {
-  PyObject *kcap, *specs, *tensor_type, *raw_stream;
+  PyObject *kcap, *specs, *tensor_type, *raw_stream, *eas_type;
   int n_index, sync, batch;
-  if (!PyArg_ParseTuple(args, "OOipiOO", &kcap, &specs, &n_index, &sync, &batch, &tensor_type, &raw_stream))
+  if (!PyArg_ParseTuple(args, "OOipiOOO", &kcap, &specs, &n_index, &sync, &batch, &tensor_type, &raw_stream,
+                        &eas_type))
     return nullptr;
   eas_hip_kernel* k = as_kernel(kcap);
   if (!k) return nullptr;
@@ -990,8 +995,8 @@ PyObject* py_fast_make(PyObject*, PyObject* args) {
       ok = false;
       break;
     }
-    const uint32_t size = kind == kFastTensor ? 8 : kind == kFastBool ? 1 : 4;
-    if (kind < kFastTensor || kind > kFastBool) {
+    const uint32_t size = (kind == kFastTensor || kind == kFastEasTensor) ? 8 : kind == kFastBool ? 1 : 4;
+    if (kind < kFastTensor || kind > kFastEasTensor) {
       PyErr_SetString(PyExc_ValueError, "fast_make: unknown argument kind");
       ok = false;
       break;
@@ -1023,6 +1028,8 @@ PyObject* py_fast_make(PyObject*, PyObject* args) {
   f->k = k;
   Py_INCREF(tensor_type);
   f->tensor_type = tensor_type;
+  Py_INCREF(eas_type);
+  f->eas_type = eas_type;
   Py_INCREF(raw_stream);
   f->raw_stream = raw_stream;
   PyObject* cap = PyCapsule_New(f, kFastCap, fast_destructor);
@@ -1035,6 +1042,10 @@ PyObject* g_s_is_cuda = nullptr;
 PyObject* g_s_is_contiguous = nullptr;
 PyObject* g_s_data_ptr = nullptr;
 PyObject* g_s_get_device = nullptr;
+PyObject* g_s_device_attr = nullptr;  // eas.Tensor._device
+PyObject* g_s_dtype_attr = nullptr;   // eas.Tensor._dtype
+PyObject* g_s_hip_attr = nullptr;     // eas.Tensor._hip (its storage; .buf the buffer capsule)
+PyObject* g_s_buf = nullptr;
 
 // The boolean result of calling obj.name(): 1, 0, or -1 on error.
 int call_true(PyObject* obj, PyObject* name) {
@@ -1089,6 +1100,32 @@ PyObject* py_fast_call(PyObject*, PyObject* const* argv, Py_ssize_t nargv) {
       last_tensor = obj;
       continue;
     }
+    if (a.kind == kFastEasTensor) {
+      // an eas.Tensor's device, dtype and storage are fixed when it is made
+      if (Py_TYPE(obj) != (PyTypeObject*)f->eas_type) Py_RETURN_NOTIMPLEMENTED;
+      PyObject* dev = PyObject_GetAttr(obj, g_s_device_attr);
+      if (!dev) return nullptr;
+      const int on_gpu = PyUnicode_Check(dev) && PyUnicode_CompareWithASCIIString(dev, "hip") == 0;
+      Py_DECREF(dev);
+      if (!on_gpu) Py_RETURN_NOTIMPLEMENTED;
+      PyObject* dt = PyObject_GetAttr(obj, g_s_dtype_attr);
+      if (!dt) return nullptr;
+      const int same = PyObject_RichCompareBool(dt, a.expect, Py_EQ);
+      Py_DECREF(dt);
+      if (same < 0) return nullptr;
+      if (!same) Py_RETURN_NOTIMPLEMENTED;
+      PyObject* st = PyObject_GetAttr(obj, g_s_hip_attr);
+      if (!st) return nullptr;
+      PyObject* cap = PyObject_GetAttr(st, g_s_buf);
+      Py_DECREF(st);
+      if (!cap) return nullptr;
+      Buffer* b = as_buffer(cap);
+      Py_DECREF(cap);  // the tensor holds its storage, and the storage its buffer
+      if (!b) Py_RETURN_NOTIMPLEMENTED;
+      const uint64_t ptr = (uint64_t)(uintptr_t)b->ptr;
+      memcpy(blob + a.offset, &ptr, 8);
+      continue;
+    }
     if ((PyObject*)Py_TYPE(obj) != a.expect) Py_RETURN_NOTIMPLEMENTED;
     if (a.kind == kFastU32) {
       unsigned long long v = PyLong_AsUnsignedLongLong(obj);
@@ -1106,8 +1143,7 @@ PyObject* py_fast_call(PyObject*, PyObject* const* argv, Py_ssize_t nargv) {
       blob[a.offset] = obj == Py_True ? 1 : 0;
     }
   }
-  if (!last_tensor) Py_RETURN_NOTIMPLEMENTED;  // without a GPU tensor there is no torch stream to follow
-  if (nval == 0) Py_RETURN_NONE;               // a zero extent launches nothing
+  if (nval == 0) Py_RETURN_NONE;  // a zero extent launches nothing
   if (!f->have_plan || f->plan_n != nval) {
     const uint32_t block = f->shape.block_size;
     const uint64_t size[3] = {f->by_groups ? (nval + block - 1) / block : nval, 1, 1};
@@ -1122,14 +1158,17 @@ PyObject* py_fast_call(PyObject*, PyObject* const* argv, Py_ssize_t nargv) {
     f->have_plan = true;
   }
   memcpy(blob + (arg_bytes + 3) / 4 * 4, f->hidden, 4 * f->shape.hidden);
-  PyObject* dev = PyObject_CallMethodNoArgs(last_tensor, g_s_get_device);
-  if (!dev) return nullptr;
-  PyObject* sobj = PyObject_CallOneArg(f->raw_stream, dev);
-  Py_DECREF(dev);
-  if (!sobj) return nullptr;
-  void* stream = PyLong_AsVoidPtr(sobj);
-  Py_DECREF(sobj);
-  if (PyErr_Occurred()) return nullptr;
+  void* stream = nullptr;  // torch's current stream of the last torch tensor's device, else the default
+  if (last_tensor) {
+    PyObject* dev = PyObject_CallMethodNoArgs(last_tensor, g_s_get_device);
+    if (!dev) return nullptr;
+    PyObject* sobj = PyObject_CallOneArg(f->raw_stream, dev);
+    Py_DECREF(dev);
+    if (!sobj) return nullptr;
+    stream = PyLong_AsVoidPtr(sobj);
+    Py_DECREF(sobj);
+    if (PyErr_Occurred()) return nullptr;
+  }
   int rc = eas_hip_launch(f->k, blob, total, f->grid, f->block, 0, stream, 1);
   if (rc) return raise_status(rc);
   if (f->sync) {
@@ -1141,7 +1180,7 @@ PyObject* py_fast_call(PyObject*, PyObject* const* argv, Py_ssize_t nargv) {
   }
   auto* pending = new Pending{nullptr, {}};
   for (size_t i = 0; i < n; ++i) {
-    if (f->args[i].kind != kFastTensor) continue;
+    if (f->args[i].kind != kFastTensor && f->args[i].kind != kFastEasTensor) continue;
     PyObject* obj = PyTuple_GET_ITEM(args, (Py_ssize_t)i);
     Py_INCREF(obj);
     pending->keepalive.push_back(obj);
@@ -1504,7 +1543,13 @@ PyMODINIT_FUNC PyInit__hip(void) {
   g_s_is_contiguous = PyUnicode_InternFromString("is_contiguous");
   g_s_data_ptr = PyUnicode_InternFromString("data_ptr");
   g_s_get_device = PyUnicode_InternFromString("get_device");
-  if (!g_s_dtype || !g_s_is_cuda || !g_s_is_contiguous || !g_s_data_ptr || !g_s_get_device) return nullptr;
+  g_s_device_attr = PyUnicode_InternFromString("_device");
+  g_s_dtype_attr = PyUnicode_InternFromString("_dtype");
+  g_s_hip_attr = PyUnicode_InternFromString("_hip");
+  g_s_buf = PyUnicode_InternFromString("buf");
+  if (!g_s_dtype || !g_s_is_cuda || !g_s_is_contiguous || !g_s_data_ptr || !g_s_get_device || !g_s_device_attr ||
+      !g_s_dtype_attr || !g_s_hip_attr || !g_s_buf)
+    return nullptr;
   PyObject* m = PyModule_Create(&kModule);
   if (m) PyModule_AddIntConstant(m, "ABI_VERSION", eas_hip_abi_version());
   if (m && PyModule_AddObject(m, "DEFAULT_OPTIONS", default_options()) != 0) {

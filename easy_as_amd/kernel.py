@@ -21,6 +21,7 @@ from .autotune import AutotuneSpec, Config
 from .compiler import CompiledKernel, _arg_key, _torch, compile as _compile
 from .meta import constexpr
 from .runtime import get_runtime
+from .tensor import Tensor
 
 _OPTION_NAMES = ("_sync", "_shape", "_grid", "_tptg", "_nthreads")
 _MEMO_LIMIT = 64
@@ -36,6 +37,8 @@ def _light_key(v: Any) -> Any:
         return t
     if t is np.ndarray:
         return (t, v.dtype)
+    if t is Tensor:  # an eas.Tensor's dtype and device are fixed when it is made
+        return (t, v.dtype, v.device)
     torch = _torch()
     if torch is not None and t is torch.Tensor:
         return (t, v.dtype, v.is_cuda)

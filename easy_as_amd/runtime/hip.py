@@ -347,15 +347,17 @@ class HipRuntime:
         """A one-native-call launch of ``ck`` for later calls shaped like ``args`` (the call memo's
         hit path), or None when this specialisation does not take one.  It takes SPMD and
         thread-mode kernels sized by their u32 argument ``N`` (1-D launches) whose arguments are
-        torch GPU tensors and int, float or bool scalars, passed positionally in the kernel's
-        argument order.  The returned callable launches what ``run(ck, ...)`` would launch for
+        torch GPU tensors, eas.Tensors on the GPU and int, float or bool scalars, passed
+        positionally in the kernel's argument order.  The returned callable launches what ``run(ck, ...)`` would launch for
         ``args`` (same dispatch, kernel arguments, stream and completion batching, and the
         EAS_MAX_IN_FLIGHT bound) and returns None, or returns NotImplemented without launching
         when an argument does not match (another type, dtype or device kind, a non-contiguous
         tensor, a scalar out of range): the caller then takes the full path."""
+        from ..tensor import Tensor as EasTensor
+
         torch = self._torch_mod()
         geo = ck.geometry
-        if torch is None or geo is None or geo.kind not in ("spmd", "thread") or grid_ndim(ck.ir) > 1:
+        if geo is None or geo.kind not in ("spmd", "thread") or grid_ndim(ck.ir) > 1:
             return None
         mod = self._mod()
         if not callable(getattr(mod, "fast_make", None)) or tuple(a.name for a in ck.ir.args) != tuple(names):
@@ -364,7 +366,14 @@ class HipRuntime:
         specs, n_index = [], None
         for i, (a, v) in enumerate(zip(ck.ir.args, args)):
             if a.kind == "buffer":
-                if type(v) is not torch.Tensor or not v.is_cuda or v.dtype != self._torch_dtypes.get(a.dtype):
+                if type(v) is EasTensor:
+                    want = _NP_DTYPES.get(a.dtype)
+                    if v.device != "hip" or want is None or v.dtype != np.dtype(want):
+                        return None
+                    specs.append((4, v.dtype))
+                    continue
+                if torch is None or type(v) is not torch.Tensor or not v.is_cuda \
+                        or v.dtype != self._torch_dtypes.get(a.dtype):
                     return None
                 specs.append((0, v.dtype))
                 continue
@@ -377,8 +386,10 @@ class HipRuntime:
         if n_index is None:
             return None
         limit = self._max_pending()
+        # without torch every buffer is an eas.Tensor, and the launch goes on the default stream
+        tensor_type, streams = (torch.Tensor, self._stream_getter()) if torch is not None else (type(None), id)
         fast = mod.fast_make(self.kernel_handle(ck), specs, n_index, bool(sync), min(16, limit) if limit else 16,
-                             torch.Tensor, self._stream_getter())
+                             tensor_type, streams, EasTensor)
         call, pending, synchronize = mod.fast_call, self._pending, mod.synchronize
 
         def launch(call_args: tuple[Any, ...]) -> Any:

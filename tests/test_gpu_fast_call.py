@@ -1,6 +1,6 @@
 """GPU: the call memo's native launch (``HipRuntime.fast_launcher`` over ``_hip.fast_call``).
 
-A repeated call of a kernel with torch GPU tensors and Python scalars (the reference's
+A repeated call of a kernel with torch GPU tensors or eas.Tensors and Python scalars (the reference's
 add and fma kernels, eas/runtime/metal.py:244-352 on each call) is launched by one native
 call after its first full-path call.  Each test checks the outputs against the oracle bit
 for bit, and that calls the fast launch does not take (another dtype or argument kind, a
@@ -138,3 +138,64 @@ def test_fast_launches_keep_the_in_flight_bound(monkeypatch):
     want = ops.add_f32(a_np, b_np)
     for o in outs:
         assert _bits_equal(o.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("sync", [True, False])
+def test_eas_gpu_tensors_through_the_fast_launch(gpu_runtime, monkeypatch, sync):
+    """eas.Tensors on the GPU (the reference's own device buffers) take the fast launch on the
+    default stream, alone and beside torch GPU tensors (then on torch's current stream)."""
+    import torch
+
+    k = eas.kernel(K.add_kernel.fn)
+    n_max = (1 << 18) + 3
+    a_np, b_np = seeded_normal(0, n_max), seeded_normal(1, n_max)
+    a, b = eas.tensor(a_np, device="hip"), eas.tensor(b_np, device="hip")
+    c = eas.tensor(np.full(n_max, np.nan, np.float32), device="hip")
+    k(a, b, c, 1031, BLOCK=256, _sync=sync)  # full path; makes the fast launch
+    assert len(k._fast) == 1
+    want = ops.add_f32(a_np, b_np)
+    gpu_runtime.synchronize()
+    got = c.numpy()
+    assert _bits_equal(got[:1031], want[:1031]) and np.all(np.isnan(got[1031:]))
+    _no_full_path(monkeypatch, gpu_runtime)
+    for n in (4099, 1, n_max):
+        k(a, b, c, n, BLOCK=256, _sync=sync)
+        gpu_runtime.synchronize()
+        got = c.numpy()
+        assert _bits_equal(got[:n], want[:n]), n
+    # a torch GPU tensor for c: another memo key, run by the full path first and by the memo
+    # after, on torch's current stream
+    monkeypatch.undo()
+    tc = torch.full((n_max,), float("nan"), device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        k(a, b, tc, 777, BLOCK=256, _sync=sync)
+        k(a, b, tc, 4099, BLOCK=256, _sync=sync)
+    gpu_runtime.synchronize()
+    s.synchronize()
+    got = tc.cpu().numpy()
+    assert _bits_equal(got[:4099], want[:4099]) and np.all(np.isnan(got[4099:]))
+
+
+def test_eas_tensors_the_fast_launch_declines(gpu_runtime):
+    """Host eas.Tensors and GPU ones of another dtype take the full path, with its results and
+    errors."""
+    k = eas.kernel(K.add_kernel.fn)
+    n = 2048
+    a_np, b_np = seeded_normal(0, n), seeded_normal(1, n)
+    a, b = eas.tensor(a_np, device="hip"), eas.tensor(b_np, device="hip")
+    c = eas.empty(n, device="hip")
+    k(a, b, c, n, BLOCK=256)
+    assert len(k._fast) == 1
+    # host eas.Tensors: staged and copied back by the full path
+    hc = eas.tensor(np.zeros(n, np.float32))
+    k(eas.tensor(a_np), eas.tensor(b_np), hc, n, BLOCK=256)
+    assert _bits_equal(hc.numpy(), ops.add_f32(a_np, b_np))
+    # f16 GPU tensors: the full path's f16 specialisation
+    h = [eas.tensor(x.astype(np.float16), device="hip") for x in (a_np, b_np)]
+    hc16 = eas.empty(n, device="hip", dtype=np.float16)
+    k(h[0], h[1], hc16, n, BLOCK=256)
+    assert _bits_equal(hc16.numpy(), ops.add_f16(a_np.astype(np.float16), b_np.astype(np.float16)))
+    # a GPU tensor of another dtype in one slot: the full path's dtype error
+    with pytest.raises(TypeError):
+        k(a, b, hc16, n, BLOCK=256)

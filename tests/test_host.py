@@ -502,6 +502,61 @@ def test_call_memo_takes_the_runtime_fast_launch(monkeypatch):
     assert len(rt.made) == 2
 
 
+class _FastMakingExt(_RecordingExt):
+    """Records the native fast launches HipRuntime.fast_launcher makes and calls."""
+
+    def __init__(self):
+        super().__init__()
+        self.made, self.calls = [], []
+
+    def fast_make(self, kernel, specs, n_index, sync, batch, tensor_type, streams, eas_type):
+        self.made.append((kernel, list(specs), n_index, sync, batch, tensor_type, eas_type))
+        return ("fast", len(self.made))
+
+    def fast_call(self, fast, args):
+        """Declines as the native call does: an eas.Tensor argument must be on the GPU and of the
+        recorded dtype."""
+        specs = self.made[fast[1] - 1][1]
+        for (kind, expect), v in zip(specs, args):
+            if kind == 4 and (getattr(v, "device", None) != "hip" or v.dtype != expect):
+                return NotImplemented
+        self.calls.append((fast, args))
+
+
+def test_eas_gpu_tensors_take_the_native_fast_launch(monkeypatch, tmp_path):
+    """eas.Tensor arguments key the call memo by dtype and device; GPU ones are passed to the
+    native fast launch as their own argument kind, host ones keep the full path (staging)."""
+    from easy_as_amd.tensor import Tensor, _HipStorage
+
+    monkeypatch.setenv("EAS_HIP_CACHE_DIR", str(tmp_path))
+    ext = _FastMakingExt()
+    rt = HipRuntime(ext=ext)
+    monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
+    gpu = [Tensor(shape=(64,), dtype=np.float32, device="hip", hip=_HipStorage(("dev", i), 256)) for i in range(3)]
+    k = eas.kernel(K.add_kernel.fn)
+    k(*gpu, 64, BLOCK=64)
+    assert len(ext.launches) == 1 and ext.launches[0][1][:3] == [("dev", 0), ("dev", 1), ("dev", 2)]
+    assert len(ext.made) == 1
+    _, specs, n_index, sync, _, _, eas_type = ext.made[0]
+    assert specs == [(4, np.dtype(np.float32))] * 3 + [(1, int)] and n_index == 3 and sync and eas_type is Tensor
+    k(*gpu, 1000, BLOCK=64)  # the memo hit goes through the fast launch
+    assert len(ext.launches) == 1 and ext.calls[-1][1] == (*gpu, 1000)
+    # host eas.Tensors: another memo key, staged on the full path, no fast launch
+    host = [eas.tensor(np.ones(64, np.float32)) for _ in range(3)]
+    k(*host, 64, BLOCK=64)
+    k(*host, 64, BLOCK=64)
+    assert len(k._memo) == 2 and len(ext.launches) == 3 and len(ext.made) == 1 and len(ext.calls) == 1
+    # GPU tensors of another dtype: the fast launch declines them and the full path runs them
+    f16 = [Tensor(shape=(64,), dtype=np.float16, device="hip", hip=_HipStorage(("dev", i), 128)) for i in range(3)]
+    k(*f16, 64, BLOCK=64)
+    assert len(ext.launches) == 4 and len(ext.calls) == 1 and len(k._memo) == 3
+    # no fast launch is made for host eas.Tensors, nor for GPU ones of another dtype than the kernel's
+    ck32 = k.compile(*gpu, 64, BLOCK=64)
+    assert rt.fast_launcher(ck32, ("a", "b", "c", "N"), (*host, 64), True) is None
+    assert rt.fast_launcher(ck32, ("a", "b", "c", "N"), (*f16, 64), True) is None
+    assert rt.fast_launcher(ck32, ("a", "b", "c", "N"), (*gpu, 64), True) is not None
+
+
 class _FillingExt(_RecordingExt):
     """Copies back a fixed byte pattern, so a test sees which host memory a result reaches."""
 
