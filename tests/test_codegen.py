@@ -12,6 +12,7 @@ this backend emits instead of the Metal text:
 * ``tests/test_mma_codegen.py:34-39``        the MMA kernel lowers to MFMA
 * ``tests/test_threadgroup_memory.py:60-75`` the barrier of a masked threadgroup copy is never inside a mask guard
 * ``tests/test_dot_dynamic_k.py:52-59``      a ``dot`` over a runtime K is a loop over K, not unrolled
+* ``tests/test_local_and_lane_id.py:32-39``  local, lane and simdgroup ids come from the thread index
 
 The last test compiles every emitted source with hiprtc for gfx950 (no GPU is
 needed for that), which is what proves a redeclaration or any other C++ error
@@ -413,3 +414,23 @@ def test_dot_over_a_runtime_k_is_a_loop_not_unrolled():
     for k in (7, 31, 64, 4096):
         other = K.gemv_dot_kernel.compile(np.zeros(8 * k, np.float32), np.zeros(k, np.float32), y, 8, k, 8, BLOCK=64)
         assert other.src == ck.src
+
+
+def test_local_lane_and_simdgroup_ids_come_from_the_thread_index():
+    # reference: tests/test_local_and_lane_id.py:32-39 (the Metal kernels declare
+    # [[thread_position_in_threadgroup]] and [[thread_index_in_simdgroup]]).  HIP has those as
+    # builtins: the local id is threadIdx.x, and the 32-lane simdgroup of the Metal model maps onto
+    # half of a wave64, lane = threadIdx.x & 31 and simdgroup = threadIdx.x >> 5.  The launch's
+    # thread count (Metal's non-uniform grid) is a hidden u32 argument after the user's.
+    out = np.zeros(256, np.float32)
+    want = {"local_id_kernel": r"= threadIdx\.x;", "lane_id_kernel": r"= threadIdx\.x & 31u;",
+            "sg_id_kernel": r"= threadIdx\.x >> 5;"}
+    for name, pattern in want.items():
+        ck = getattr(K, name).compile(out, 256, BLOCK=256)
+        assert ck.launch_mode == "thread"
+        head = ck.src[ck.src.index(f"void __launch_bounds__(256) {name}("):]
+        params = head[:head.index("{")]
+        assert re.search(r"float\* __restrict__ out,\s*const uint32_t N,\s*const uint32_t __eas_nthreads\)", params)
+        body = "\n".join(_kernel_body(ck.src, name))
+        assert re.search(pattern, body), (name, body)
+

@@ -347,6 +347,21 @@ def test_naive_matmul_bit_exact_vs_oracle(gpu_runtime):
     assert ops.rel_err(c.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
 
 
+def test_naive_matmul_on_gpu_eas_tensors(gpu_runtime):
+    # reference: tests/test_matmul.py:63-93 (the same kernel on device eas.Tensors, M=8, N=48,
+    # K=16, BLOCK=32 over an (M, N tiles) grid)
+    m, n, k, block = 8, 48, 16, 32
+    a2, b2 = seeded_normal(0, m * k).reshape(m, k), seeded_normal(1, k * n).reshape(k, n)
+    a, b = eas.tensor(a2.reshape(-1), device="hip"), eas.tensor(b2.reshape(-1), device="hip")
+    c = eas.empty(m * n, device="hip")
+    K.matmul_kernel(a, b, c, m, n, BLOCK=block, K=k, _grid=(m, K.cdiv(n, block)))
+    ref = interp.run_kernel(K.matmul_kernel, a2.reshape(-1), b2.reshape(-1), np.zeros(m * n, np.float32), m, n,
+                            BLOCK=block, K=k, _grid=(m, K.cdiv(n, block)))["c"]
+    got = c.numpy()
+    assert _bits_equal(got, ref)
+    assert ops.rel_err(got.reshape(m, n), ops.matmul_ref(a2, b2)) <= 1e-5 * math.sqrt(k)
+
+
 @pytest.mark.parametrize("mnk", [(33, 65, 48), (64, 64, 32), (17, 130, 31)])
 def test_tiled_matmul_literal_bit_exact(gpu_runtime, monkeypatch, mnk):
     # the literal lowering (lift disabled) keeps the reference's fma order: bit-exact vs the oracle
