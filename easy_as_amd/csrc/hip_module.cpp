@@ -21,6 +21,7 @@
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
 
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <string>
@@ -1137,7 +1138,9 @@ PyObject* py_fast_call(PyObject*, PyObject* const* argv, Py_ssize_t nargv) {
       memcpy(blob + a.offset, &u, 4);
       if ((int)i == f->n_index) nval = v;
     } else if (a.kind == kFastF32) {
-      const float x = (float)PyFloat_AS_DOUBLE(obj);
+      const double d = PyFloat_AS_DOUBLE(obj);
+      const float x = (float)d;
+      if (std::isinf(x) && !std::isinf(d)) Py_RETURN_NOTIMPLEMENTED;  // the full path raises OverflowError
       memcpy(blob + a.offset, &x, 4);
     } else {
       blob[a.offset] = obj == Py_True ? 1 : 0;

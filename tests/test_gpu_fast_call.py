@@ -100,6 +100,11 @@ def test_f32_scalar_and_calls_the_fast_launch_declines(gpu_runtime):
         k(a, b, torch.zeros(2 * n, device="cuda")[::2], n, 2.0, BLOCK=256)
     with pytest.raises(OverflowError):
         k(a, b, c, 1 << 32, 2.0, BLOCK=256)
+    with pytest.raises(OverflowError):  # an f32 scalar beyond the f32 range
+        k(a, b, c, n, 1e39, BLOCK=256)
+    k(a, b, c, n, float("inf"), BLOCK=256)  # infinities pack as they are
+    assert np.all(a_np != 0)  # so every output is an infinity, no NaN
+    assert _bits_equal(c.cpu().numpy(), ops.fmaf(a_np, np.float32(np.inf), b_np))
     # a zero extent launches nothing
     c.fill_(5.0)
     k(a, b, c, 0, 2.0, BLOCK=256)
