@@ -46,12 +46,17 @@ def _cdiv(a: int, b: int) -> int:
 _NP_DTYPES = {DType.F16: np.float16, DType.F32: np.float32}
 
 
+class ScalarRangeError(struct.error, OverflowError):
+    """A u32 scalar outside [0, 2^32).  The reference's ``struct.pack("<I", ...)`` raises
+    ``struct.error`` for it (``metal.py:28-30``); this is both that and an ``OverflowError``."""
+
+
 def pack_scalar(dtype: DType, value: Any) -> bytes:
     """Kernel-argument bytes of a scalar (reference ``metal.py:28-38``)."""
     if dtype == DType.U32:
         v = int(value)
         if not 0 <= v < (1 << 32):
-            raise OverflowError(f"u32 scalar out of range: {v}")
+            raise ScalarRangeError(f"u32 scalar out of range: {v}")
         return struct.pack("<I", v)
     if dtype == DType.F16:
         return np.float16(value).tobytes()

@@ -619,8 +619,14 @@ def test_scalar_packing_errors(monkeypatch, tmp_path):
     rt = HipRuntime(ext=_RecordingExt())
     monkeypatch.setattr(eas_kernel, "get_runtime", lambda *a, **k: rt)
     x = np.zeros(8, np.float32)
-    with pytest.raises((OverflowError, ValueError, struct.error)):
+    # the reference's struct.pack raises struct.error (metal.py:28-30); the error here is also an OverflowError
+    with pytest.raises(struct.error) as info:
         K.add_kernel(x, x, x, 1 << 32, BLOCK=256)
+    assert isinstance(info.value, OverflowError)
+    with pytest.raises(ValueError, match="nthreads must be >= 0"):  # the grid rule comes first (grid.py:26-28)
+        K.add_kernel(x, x, x, -1, BLOCK=256)
+    with pytest.raises(OverflowError):  # an f32 beyond the f32 range, as struct.pack("<f") reports it
+        K.axpy_kernel(x, x, x, 8, 1e39, BLOCK=256)
     with pytest.raises(TypeError):
         K.add_kernel(x.astype(np.float64), x, x, 8, BLOCK=256)
 
