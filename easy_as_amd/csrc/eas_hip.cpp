@@ -433,8 +433,6 @@ static int check_shape(const eas_hip_launch_shape* s) {
     return fail(EAS_HIP_ERR_INVALID, "launch shape has a zero or oversized dimension");
   if ((s->kind == EAS_HIP_KIND_SPMD || s->kind == EAS_HIP_KIND_THREAD) && s->hidden != 1)
     return fail(EAS_HIP_ERR_INVALID, "spmd and thread kernels take exactly one hidden extent");
-  if (s->kind == EAS_HIP_KIND_THREAD && s->wg_size != s->block_size)
-    return fail(EAS_HIP_ERR_INVALID, "a thread-mode kernel's workgroup is its BLOCK");
   if (s->kind == EAS_HIP_KIND_GEMM && s->hidden != 4)
     return fail(EAS_HIP_ERR_INVALID, "a lifted GEMM takes four hidden extents (m_lo, m_hi, n_lo, n_hi)");
   return EAS_HIP_OK;
@@ -843,7 +841,9 @@ int eas_hip_plan_dispatch(const eas_hip_launch_shape* s, int by_groups, const ui
     uint64_t live = by_groups ? size[0] * s->block_size : size[0];
     if (live > 0xFFFFFFFFull || groups_x * s->block_size > 0xFFFFFFFFull)
       return fail(EAS_HIP_ERR_INVALID, "%s x exceeds 2^32 threads", what);
-    grid[0] = (uint32_t)groups_x;
+    // one workgroup per threadgroup (programs_per_wg = split = 1, wg_size = BLOCK), or a kernel
+    // emitted as lanes: threadgroups mapped like SPMD programs
+    grid[0] = (uint32_t)((groups_x + s->programs_per_wg - 1) / s->programs_per_wg * s->split);
     hidden[0] = (uint32_t)live;
   } else {
     // SPMD: a Metal thread is a program; the reference dispatches them as threads with

@@ -163,8 +163,11 @@ def plan_launch(
             raise ValueError(f"spmd launch of {groups[0]} programs exceeds 2^32 threads along x")
         return LaunchPlan((nblocks, groups[1], groups[2]), (geo.wg_size, 1, 1), (groups[0],))
     if geo.kind == "thread":
+        # one workgroup per threadgroup, or (a kernel emitted as lanes) the SPMD mapping of one
+        # program per threadgroup; the hidden extent is the live thread count either way
         live = live_x if live_x is not None else groups[0] * block
-        return LaunchPlan(groups, (block, 1, 1), (live,))  # type: ignore[arg-type]
+        nblocks = _cdiv(groups[0], geo.programs_per_wg * geo.unroll) * geo.split
+        return LaunchPlan((nblocks, groups[1], groups[2]), (geo.wg_size, 1, 1), (live,))
     if geo.kind == "gemm":
         from ..codegen.gemm_lift import plan_gemm
 

@@ -131,8 +131,10 @@ typedef struct eas_hip_launch_shape {
   int kind;                 /* eas_hip_launch_kind                                        */
   uint32_t block_size;      /* the kernel's BLOCK (lanes per program, threads per group)   */
   uint32_t wg_size;         /* HIP threads per workgroup                                   */
-  uint32_t programs_per_wg; /* SPMD: programs each group of `split` workgroups runs         */
-  uint32_t split;           /* SPMD: workgroups a program's lanes are spread over (>= 1)   */
+  uint32_t programs_per_wg; /* programs (SPMD) or threadgroups (thread mode emitted as lanes)
+                               each group of `split` workgroups runs; 1 for one workgroup per
+                               threadgroup                                                  */
+  uint32_t split;           /* workgroups a program's (threadgroup's) lanes are spread over */
   uint32_t arg_bytes;       /* packed bytes of the kernel's own arguments (0: not checked) */
   uint32_t hidden;          /* u32 extents that follow them (<= EAS_HIP_MAX_HIDDEN)        */
 } eas_hip_launch_shape;

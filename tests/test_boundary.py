@@ -95,13 +95,22 @@ def test_launch_by_threads_matches_every_spmd_mapping(hip, monkeypatch, env):
             assert hip.plan_dispatch(ck.src, tpg, tptg) == (plan.grid, plan.block, plan.hidden), (env, block, n)
 
 
-def test_non_uniform_last_threadgroup():
-    # 1000 threads of BLOCK 256: four workgroups, the hidden extent stops the last 24 threads
+def test_non_uniform_last_threadgroup(monkeypatch):
+    # 1000 threads of BLOCK 256: four threadgroups, the hidden extent stops the last 24 threads.
+    # Emitted as lanes (the default for this element stream), each threadgroup is two workgroups
+    # of 32 threads carrying 16-byte vectors; one thread per Metal thread, one workgroup each.
     hip = load_hip_ext(require=True)
     ck = K.simple_fma_kernel.compile(_f(), _f(), _f(), _f(), 8, BLOCK=256)
-    assert hip.plan_dispatch(ck.src, 1000, 256) == ((4, 1, 1), (256, 1, 1), (1000,))
+    assert ck.geometry.params.get("lanes") and ck.launch_mode == "thread"
+    assert hip.plan_dispatch(ck.src, 1000, 256) == ((8, 1, 1), (32, 1, 1), (1000,))
+    assert plan_launch(ck, {"N": 1000}).grid == (8, 1, 1)
+    monkeypatch.setenv("EAS_HIP_THREAD_LANES", "0")
+    one = eas.kernel(K.simple_fma_kernel.fn).compile(_f(), _f(), _f(), _f(), 8, BLOCK=256)
+    assert not one.geometry.params.get("lanes")
+    assert hip.plan_dispatch(one.src, 1000, 256) == ((4, 1, 1), (256, 1, 1), (1000,))
     # the int form of threads_per_threadgroup and its omission mean the same
-    assert hip.plan_dispatch(ck.src, 1000) == hip.plan_dispatch(ck.src, (1000,), (256, 1, 1))
+    for c in (ck, one):
+        assert hip.plan_dispatch(c.src, 1000) == hip.plan_dispatch(c.src, (1000,), (256, 1, 1))
 
 
 def test_launch_convention_errors(hip):
@@ -122,7 +131,9 @@ def test_launch_convention_errors(hip):
         with pytest.raises(ValueError, match="2\\^32"):
             hip.plan_dispatch(thread.src, groups, 256, by_groups=True)
     most = ((1 << 32) - 1) // 256
-    assert hip.plan_dispatch(thread.src, most, 256, by_groups=True) == ((most, 1, 1), (256, 1, 1), (most * 256,))
+    want = plan_launch(thread, {"N": 8}, grid=(most, 1, 1))
+    assert want.hidden == (most * 256,)
+    assert hip.plan_dispatch(thread.src, most, 256, by_groups=True) == (want.grid, want.block, want.hidden)
     # a lifted GEMM's plan reads M, N and its buffers from argv
     h = np.zeros(8, np.float16)
     gemm = K.matmul_mma_kernel.compile(h, h, f, 300, 520, BM=32, BN=32, BK=8, K=200, NT=512)
@@ -168,7 +179,7 @@ def test_malformed_launch_lines_are_rejected(hip):
     assert (unrolled["programs_per_wg"], unrolled["split"]) == (4, 2)
     for bad in ("// eas-launch: block=256\n", "// eas-launch: kind=warp block=256 wg=32 hidden=1\n",
                 "// eas-launch: kind=spmd block=256 wg=2048 hidden=1\n",
-                "// eas-launch: kind=thread block=256 wg=128 hidden=1\n",
+                "// eas-launch: kind=thread block=256 wg=128 hidden=2\n",
                 "// eas-launch: kind=spmd block=256 wg=32 hidden=9\n",
                 "// eas-launch: kind=spmd block=x wg=32 hidden=1\n"):
         with pytest.raises(ValueError):

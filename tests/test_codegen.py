@@ -134,9 +134,11 @@ def test_spmd_mode_block_size_and_program_ids_only():
     assert "__pid < __eas_nprog" in ck.src
 
 
-def test_fma_emitted_with_early_return_for_single_store_mask():
+def test_fma_emitted_with_early_return_for_single_store_mask(monkeypatch):
+    # the one-thread-per-thread emitter (the lanes form is checked below)
+    monkeypatch.setenv("EAS_HIP_THREAD_LANES", "0")
     z = _f(256)
-    ck = simple_fma_kernel.compile(z, z, z, z.copy(), 256, BLOCK=256)
+    ck = eas.kernel(simple_fma_kernel.fn).compile(z, z, z, z.copy(), 256, BLOCK=256)
     assert "__builtin_fmaf(" in ck.src
     assert re.search(r"\bif \(!v\d+\) return;", ck.src)
     assert not re.search(r"\bif \(v\d+\) \{", ck.src)
@@ -218,11 +220,29 @@ def test_pp_mfma_switch_is_validated(monkeypatch):
         eas.kernel(K.matmul_mma_kernel.fn).compile(h, h, f, 4096, 4096, BM=32, BN=32, BK=8, K=4096, NT=512)
 
 
+def _one_thread_per_thread(kern, *args, **meta):
+    """``kern`` compiled on the one-thread-per-thread emitter (``EAS_HIP_THREAD_LANES=0``)."""
+    import os
+
+    old = os.environ.get("EAS_HIP_THREAD_LANES")
+    os.environ["EAS_HIP_THREAD_LANES"] = "0"
+    try:
+        return eas.kernel(kern.fn).compile(*args, **meta)
+    finally:
+        if old is None:
+            del os.environ["EAS_HIP_THREAD_LANES"]
+        else:
+            os.environ["EAS_HIP_THREAD_LANES"] = old
+
+
 def _sources() -> list[tuple[str, str]]:
     h, f = _h(256), _f(256)
     cks = [
         ("add_f16_kernel", add_f16_kernel.compile(h, h, h.copy(), 256, BLOCK=256)),
         ("simple_fma_kernel", simple_fma_kernel.compile(f, f, f, f.copy(), 256, BLOCK=256)),
+        ("simple_fma_kernel_one_thread", _one_thread_per_thread(simple_fma_kernel, f, f, f, f.copy(), 256, BLOCK=256)),
+        ("add2d_hw_kernel", K.add2d_hw_kernel.compile(f, f, f.copy(), 4, 64, BLOCK=32)),
+        ("grid_callable_kernel", K.grid_callable_kernel.compile(f, 4, 64, BLOCK=64)),
         ("matmul_with_fma", matmul_with_fma.compile(f, f, f.copy(), 32, 64, BLOCK=32, K=8)),
         ("dot_f16_scalar_kernel", dot_f16_scalar_kernel.compile(h, h, f, 8, BLOCK=128)),
         ("dot_f16_tn4_kernel", dot_f16_tn4_kernel.compile(h, h, f, 8, BLOCK=128)),
@@ -433,4 +453,52 @@ def test_local_lane_and_simdgroup_ids_come_from_the_thread_index():
         assert re.search(r"float\* __restrict__ out,\s*const uint32_t N,\s*const uint32_t __eas_nthreads\)", params)
         body = "\n".join(_kernel_body(ck.src, name))
         assert re.search(pattern, body), (name, body)
+
+
+def test_thread_element_streams_are_emitted_as_lanes():
+    # The reference's thread-mode fma (tests/test_fma.py:13-23): one program of BLOCK lanes per
+    # threadgroup, 16-byte nontemporal vectors, and every lane-varying access masked by the live
+    # thread count, which stays the kernel's one hidden argument after the user's.
+    f = _f(256)
+    ck = simple_fma_kernel.compile(f, f, f, f.copy(), 256, BLOCK=256)
+    one = _one_thread_per_thread(simple_fma_kernel, f, f, f, f.copy(), 256, BLOCK=256)
+    assert ck.launch_mode == one.launch_mode == "thread" and ck.block_size == one.block_size == 256
+    geo = ck.geometry
+    assert geo.kind == "thread" and geo.params["lanes"] and geo.params["lanes_per_thread"] == 4
+    assert (geo.wg_size, geo.split) == (32, 2)  # four HBM streams: 512-byte chunks, as the SPMD fma
+    sig = lambda c: c.src[c.src.index("simple_fma_kernel("):c.src.index("{", c.src.index("simple_fma_kernel("))]
+    assert sig(ck).replace("__launch_bounds__(32)", "") == sig(one).replace("__launch_bounds__(256)", "")
+    assert sig(ck).rstrip().endswith("const uint32_t __eas_nthreads)")
+    body = ck.src.split('extern "C"', 1)[1]
+    assert body.count("__builtin_nontemporal_load((const eas_f32x4*)") == 3
+    assert body.count("__builtin_nontemporal_store((eas_f32x4)") == 1
+    assert "__builtin_fmaf(" in body and "__eas_nprog = __eas_nthreads / 256u" in body
+    live = re.search(r"bool (v\d+)\[4\];\n  \1\[0\] = v\d+\[0\] < __eas_nthreads;", body)
+    assert live, "the live-thread mask"
+    # every global access is guarded by a mask that includes it
+    masks = set(re.findall(r"(v\d+)\[0\] = v\d+\[0\] && " + live.group(1) + r"\[0\];", body))
+    for m in re.findall(r"if \((v\d+)\[0\] && \1\[1\]", body):
+        assert m in masks or m == live.group(1), m
+    assert len(re.findall(r"if \((v\d+)\[0\] && \1\[1\]", body)) == 4  # three loads, one store
+
+
+@pytest.mark.parametrize("case", ["local_id", "barrier", "dot", "shared_address_load", "lanes_off"])
+def test_kernels_that_stay_one_thread_per_thread(case, monkeypatch):
+    f, h = _f(256), _h(256)
+    if case == "local_id":  # a Metal thread's position in its threadgroup
+        ck = K.local_id_kernel.compile(f, 256, BLOCK=256)
+    elif case == "barrier":  # threadgroup memory shared between threads
+        ck = K.tg_copy_kernel.compile(f, f.copy(), 256, BLOCK=256)
+    elif case == "dot":
+        ck = dot_f16_tn4_kernel.compile(h, h, f, 8, BLOCK=128)
+    elif case == "shared_address_load":  # a row of A at one address, under each thread's own mask
+        ck = K.matmul_kernel.compile(f, f, f.copy(), 8, 48, BLOCK=32, K=4)
+    else:
+        monkeypatch.setenv("EAS_HIP_THREAD_LANES", "0")
+        ck = eas.kernel(simple_fma_kernel.fn).compile(f, f, f, f.copy(), 256, BLOCK=256)
+    assert ck.launch_mode == "thread" and not ck.geometry.params.get("lanes")
+    assert ck.geometry.wg_size == ck.block_size and "__gid" in ck.src
+    monkeypatch.setenv("EAS_HIP_THREAD_LANES", "2")
+    with pytest.raises(ValueError, match="EAS_HIP_THREAD_LANES must be 0 or 1"):
+        eas.kernel(simple_fma_kernel.fn).compile(f, f, f, f.copy(), 256, BLOCK=256)
 

@@ -101,3 +101,46 @@ def test_random_spmd_program_under_every_mapping(seed, env, gpu_runtime, monkeyp
     k(*args, BLOCK=c["BLOCK"], **c["options"])
     for name, got in (("out", args[4]), ("out16", args[5])):
         assert F.same_values(got, ref[name]), f"seed {seed} {env}: {name} differs\n{c['src']}"
+
+
+def _lanes_seeds() -> list[int]:
+    """The thread-mode cases the emitter takes as lanes of one program per threadgroup (element
+    streams without barriers, threadgroup memory, thread positions or dot)."""
+    seeds = []
+    for seed in range(1, 200, 2):
+        c = F.case(seed)
+        if c["mode"] != "thread":
+            continue
+        opts = {k: v for k, v in c["options"].items() if not k.startswith("_")}
+        if F.build(c["src"]).compile(*F.inputs(seed, c["N"]), BLOCK=c["BLOCK"], **opts).geometry.params.get("lanes"):
+            seeds.append(seed)
+    return seeds
+
+
+def test_some_thread_cases_are_emitted_as_lanes():
+    seeds = _lanes_seeds()
+    assert len(seeds) >= 15, seeds
+
+
+_LANES_ENVS = [{"EAS_HIP_THREAD_LANES": "0"}, {"EAS_HIP_SPMD_WG": "256"}, {"EAS_HIP_SPMD_LPT": "16"},
+               {"EAS_HIP_SPMD_UNROLL": "2", "EAS_HIP_SPMD_WG": "32"}]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("env", _LANES_ENVS, ids=lambda e: ",".join(f"{k[8:]}={v}" for k, v in e.items()))
+def test_random_thread_program_as_lanes_and_one_thread_per_thread(env, gpu_runtime, monkeypatch):
+    """The thread-mode cases emitted as lanes, again with the conversion off (one HIP thread per
+    Metal thread) and under other workgroup mappings of the lanes: the same bits as the oracle."""
+    seeds = _lanes_seeds()
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    for seed in seeds:
+        c = F.case(seed)
+        print(f"fuzz seed {seed} {env}: N={c['N']} BLOCK={c['BLOCK']} {c['options']}", flush=True)
+        k = F.build(c["src"])
+        args = F.inputs(seed, c["N"])
+        ref = _run_oracle(c, args)
+        k(*args, BLOCK=c["BLOCK"], **c["options"])
+        for name, got in (("out", args[4]), ("out16", args[5])):
+            assert F.same_values(got, ref[name]), f"seed {seed} {env}: {name} differs\n{c['src']}"
+

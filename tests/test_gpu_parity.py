@@ -96,6 +96,47 @@ def test_fma_thread_mode_and_explicit(gpu_runtime):
     assert _bits_equal(d2, ops.fmaf(a, b, c))
 
 
+@eas.kernel
+def _thread_add_f16(a, b, c, N, BLOCK: eas.constexpr):
+    offs = mk.program_id(0) * BLOCK + mk.tid(0, BLOCK)
+    m = offs < N
+    mk.store(c, offs, mk.load(a, offs, m) + mk.load(b, offs, m), m)
+
+
+@pytest.mark.parametrize("lanes", ["1", "0"])
+@pytest.mark.parametrize("block", [32, 64, 256, 1024])
+def test_thread_mode_element_streams(gpu_runtime, monkeypatch, block, lanes):
+    """Thread-mode element kernels emitted as lanes of one program per threadgroup (the default)
+    and one thread per Metal thread give the same bits: odd sizes, a thread count below the
+    kernel's own bound (only that many threads exist), explicit threadgroup grids, f16."""
+    monkeypatch.setenv("EAS_HIP_THREAD_LANES", lanes)
+    fma, add16 = eas.kernel(K.simple_fma_kernel.fn), eas.kernel(_thread_add_f16.fn)
+    n_max = 5 * block + 7
+    a, b, c = seeded_normal(0, n_max), seeded_normal(1, n_max), seeded_normal(2, n_max)
+    want = ops.fmaf(a, b, c)
+    for n in (1, block - 1, block, 3 * block + 1, n_max):
+        d = np.full(n_max + 5, np.nan, np.float32)
+        fma(a, b, c, d, n, BLOCK=block)
+        assert _bits_equal(d[:n], want[:n]) and np.all(np.isnan(d[n:])), (block, n)
+    assert fma.compile(a, b, c, d, 8, BLOCK=block).geometry.params.get("lanes", False) == (lanes == "1")
+    # 900 threads of a kernel bounded by N = n_max: the threads past 900 do not exist
+    nt = min(900, n_max - 1)
+    d = np.full(n_max, np.nan, np.float32)
+    fma(a, b, c, d, n_max, BLOCK=block, _nthreads=nt)
+    assert _bits_equal(d[:nt], want[:nt]) and np.all(np.isnan(d[nt:])), (block, nt)
+    # an explicit grid of threadgroups: every thread of them exists; the kernel's mask stops at N
+    d = np.full(n_max, np.nan, np.float32)
+    fma(a, b, c, d, 2 * block + 3, BLOCK=block, _grid=(2, 1, 1))
+    assert _bits_equal(d[:2 * block], want[:2 * block]) and np.all(np.isnan(d[2 * block:]))
+    d = np.full(n_max, np.nan, np.float32)
+    fma(a, b, c, d, 2 * block + 3, BLOCK=block, _grid=(4, 1, 1))
+    assert _bits_equal(d[:2 * block + 3], want[:2 * block + 3]) and np.all(np.isnan(d[2 * block + 3:]))
+    h1, h2 = a.astype(np.float16), b.astype(np.float16)
+    o = np.full(n_max, np.float16(7), np.float16)
+    add16(h1, h2, o, n_max - 2, BLOCK=block)
+    assert _bits_equal(o[:n_max - 2], ops.add_f16(h1[:n_max - 2], h2[:n_max - 2])) and np.all(o[n_max - 2:] == 7)
+
+
 def test_fma_known_answer_differs_from_two_roundings(gpu_runtime):
     # (1+2^-23)(1-2^-23) - 1 = -2^-46 exactly; mul-then-add gives 0.
     e = np.float32(2.0 ** -23)
@@ -227,6 +268,13 @@ def test_add_and_fma_n2e28_every_output_bit_exact(gpu_runtime, inputs_n2e28, blo
     step = 1 << 26
     for s in range(0, n, step):
         assert _bits_equal(got[s:s + step], ops.fmaf(a[s:s + step], b[s:s + step], c[s:s + step])), s
+    # the reference's own fma kernel, thread mode (tests/test_fma.py:13-23), emitted as lanes
+    out.fill_(float("nan"))
+    K.simple_fma_kernel(ta, tb, tc, out, n, BLOCK=block)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for s in range(0, n, step):
+        assert _bits_equal(got[s:s + step], ops.fmaf(a[s:s + step], b[s:s + step], c[s:s + step])), ("thread", s)
     del ta, tb, tc, out
     torch.cuda.empty_cache()
 

@@ -206,18 +206,26 @@ def test_spmd_workgroup_override_is_validated(monkeypatch):
         eas.kernel(K.add_kernel.fn).compile(z, z, z, 1, BLOCK=256)
 
 
-def test_plan_zero_extent_and_tptg_rules():
+def test_plan_zero_extent_and_tptg_rules(monkeypatch):
     ck = _add_ck()
     assert plan_launch(ck, {"N": 0}) is None
     assert plan_launch(ck, {"N": 10}, grid=(0, 1, 1)) is None
     with pytest.raises(ValueError):
         plan_launch(ck, {"N": 10}, tptg=(256, 1, 1))  # SPMD kernels take (1,1,1)
     tck = K.tptg_independent_kernel.compile(np.zeros(1, np.float32), 10, BLOCK=64)
-    assert tck.launch_mode == "thread"
+    assert tck.launch_mode == "thread" and tck.geometry.params.get("lanes")
+    # 1000 threads in 16 threadgroups of 64: as lanes, 16 threads of 16-byte vectors per
+    # threadgroup, 16 threadgroups per 256-thread workgroup; one thread per Metal thread, one
+    # workgroup per threadgroup
     plan = plan_launch(tck, {"N": 1000}, tptg=(64, 1, 1))
+    assert plan.grid == (1, 1, 1) and plan.block == (256, 1, 1) and plan.hidden == (1000,)
+    monkeypatch.setenv("EAS_HIP_THREAD_LANES", "0")
+    one = eas.kernel(K.tptg_independent_kernel.fn).compile(np.zeros(1, np.float32), 10, BLOCK=64)
+    plan = plan_launch(one, {"N": 1000}, tptg=(64, 1, 1))
     assert plan.grid == (16, 1, 1) and plan.block == (64, 1, 1) and plan.hidden == (1000,)
-    with pytest.raises(ValueError):
-        plan_launch(tck, {"N": 1000}, tptg=(1, 1, 1))
+    for c in (tck, one):
+        with pytest.raises(ValueError):
+            plan_launch(c, {"N": 1000}, tptg=(1, 1, 1))
 
 
 def test_plan_lifted_gemm_covers_the_reference_rectangle():

@@ -32,7 +32,11 @@ def _simple_add_tid(a, b, c, N, BLOCK: eas.constexpr):
 
 def test_thread_id_rewrite_applies_and_env_disables(monkeypatch):
     ck = _simple_add_tid.compile(f32(4), f32(4), f32(4), 4, BLOCK=256)
-    assert "thread_id" in _ops(ck) and "__gid" in ck.src
+    # emitted as lanes of one program per threadgroup, the thread id is the program's base plus a lane
+    assert "thread_id" in _ops(ck) and ck.geometry.params.get("lanes") and "__pid" in ck.src
+    with monkeypatch.context() as mp:  # one thread per Metal thread: the global thread index
+        mp.setenv("EAS_HIP_THREAD_LANES", "0")
+        assert "__gid" in eas.kernel(_simple_add_tid.fn).compile(f32(4), f32(4), f32(4), 4, BLOCK=256).src
     monkeypatch.setenv("EAS_DISABLE_THREAD_ID_REWRITE", "1")
     ck2 = eas.kernel(_simple_add_tid.fn).compile(f32(4), f32(4), f32(4), 4, BLOCK=256)
     assert "thread_id" not in _ops(ck2)
@@ -147,7 +151,11 @@ def test_bool_where_lowers_to_logical_and():
     assert "&&" in ck.src
 
 
-def test_nested_where_chain_inlines_to_single_if():
+def test_nested_where_chain_inlines_to_single_if(monkeypatch):
+    # the one-thread-per-thread emitter's folding of a single store's boolean mask (a kernel
+    # emitted as lanes keeps its masks per lane instead)
+    monkeypatch.setenv("EAS_HIP_THREAD_LANES", "0")
+
     @eas.kernel
     def k(out, N, BLOCK: eas.constexpr):
         tid = mk.tid(0, BLOCK)
