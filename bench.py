@@ -54,6 +54,8 @@ PRIMARY_BLOCK = 256
 WORKLOADS = {
     "add": ("add_kernel", 2, 12),
     "fma": ("fma_kernel", 3, 16),
+    # the reference's own fma kernel, thread mode (tests/test_fma.py:13-23)
+    "fma_thread": ("simple_fma_kernel", 3, 16),
     "copy": ("copy_kernel", 1, 8),
     "read": ("read_kernel", 1, 4),
     "write": ("fill_kernel", 0, 4),
@@ -863,6 +865,7 @@ def _cpu_baseline(workload: str, hosts: list[np.ndarray]) -> dict:
     timed beside it on a 2^26 sample."""
     from oracle import ops
 
+    workload = "fma" if workload == "fma_thread" else workload
     n = hosts[0].size if hosts else N_ELEM
     out = np.empty(n, np.float32)
     tmp = np.empty(n, np.float32) if workload == "fma" else None
@@ -1004,12 +1007,17 @@ def main() -> int:
         else:
             exact, parity = True, "not checked (--no-cpu-baseline skips the oracle)"
         geo = ck.geometry
+        unit = "threadgroup" if ck.launch_mode == "thread" else "program"  # what a group of lanes is
         res = {"ck": ck, "rargs": rargs, "wall_ms": wall_ms, "ev_ms": ev_ms, "GB/s": round(per * N_ELEM / ev_ms / 1e6, 1),
                "frac": round(per * N_ELEM / ev_ms / 1e6 / HBM_PEAK_GBS, 4), "ms_per_launch": round(ev_ms, 5),
                "parity": parity, "parity_ok": exact,
                "launch": f"{geo.wg_size} threads per workgroup, "
-                         + (f"{geo.split} workgroups per program" if geo.split > 1
-                            else f"{geo.programs_per_wg} program(s) per workgroup")}
+                         + (f"{geo.split} workgroups per {unit}" if geo.split > 1
+                            else f"{geo.programs_per_wg} {unit}(s) per workgroup")}
+        if ck.launch_mode == "thread":
+            res["kernel"] = (f"{kn}, thread mode (mk.tid), "
+                             + ("emitted as lanes of one program per threadgroup" if geo.params.get("lanes")
+                                else "one HIP thread per Metal thread"))
         _log(f"{workload} BLOCK={block}: wall {wall_ms:.4f} ms/step, event {ev_ms:.4f} ms/launch, "
              f"{res['GB/s']} GB/s, {res['launch']}, parity {parity}")
         return res
@@ -1033,8 +1041,10 @@ def main() -> int:
     # vendor comparison on the same device-resident inputs: the torch (ROCm) operation
     tfn = {"add": lambda: torch.add(ins[0], ins[1], out=out),
            "fma": lambda: torch.addcmul(ins[2], ins[0], ins[1], out=out),
+           "fma_thread": lambda: torch.addcmul(ins[2], ins[0], ins[1], out=out),
            "copy": lambda: out.copy_(ins[0]), "read": lambda: ins[0].sum(), "write": lambda: out.fill_(1.0)}
-    texpr = {"add": "torch.add(a, b, out=c)", "fma": "torch.addcmul(c, a, b, out=d)", "copy": "c.copy_(a)",
+    texpr = {"add": "torch.add(a, b, out=c)", "fma": "torch.addcmul(c, a, b, out=d)",
+             "fma_thread": "torch.addcmul(c, a, b, out=d)", "copy": "c.copy_(a)",
              "read": "a.sum()", "write": "c.fill_(1.0)"}[args.workload]
     tms = _torch_event_ms(tfn[args.workload], args.steps, args.warmup, torch)
     vendor = {"op": texpr, "GB/s": round(per_elem * N_ELEM / tms / 1e6, 1), "ms_per_launch": round(tms, 5)}
@@ -1043,7 +1053,7 @@ def main() -> int:
     if not args.no_extra and args.workload == "add":
         # configs[1] in full: add at the other BLOCK and fma at both, each timed and checked
         other = 1024 if args.block != 1024 else 256
-        for wl, blk in (("add", other), ("fma", 256), ("fma", 1024)):
+        for wl, blk in (("add", other), ("fma", 256), ("fma", 1024), ("fma_thread", 256), ("fma_thread", 1024)):
             r = elementwise(wl, blk)
             extra[f"{wl}_block{blk}"] = {k: v for k, v in r.items()
                                          if k not in ("wall_ms", "ev_ms", "parity_ok", "ck", "rargs")}
@@ -1102,10 +1112,12 @@ def main() -> int:
         traffic = json.loads(pmc.read_text()).get("traffic_bytes_per_launch")
     value = bytes_per_launch / (wall_ms * 1e-3) / 1e9
     achieved = bytes_per_launch / (ev_ms * 1e-3) / 1e9
-    expr = {"add": "c=a+b", "fma": "d=a*b+c (fused, one rounding)", "copy": "c=a", "read": "read a",
-            "write": "c=1"}[args.workload]
+    expr = {"add": "c=a+b", "fma": "d=a*b+c (fused, one rounding)", "fma_thread": "d=a*b+c (fused, one rounding)",
+            "copy": "c=a", "read": "read a", "write": "c=1"}[args.workload]
+    style = ("thread-mode (mk.tid, masked tail)" if args.workload == "fma_thread"
+             else "SPMD (mk.arange, masked tail)")
     line = {
-        "metric": f"fp32 {args.workload} GB/s @N=2^28 (eas SPMD kernel, one MI355X)",
+        "metric": f"fp32 {args.workload} GB/s @N=2^28 (eas {style.split(' ')[0]} kernel, one MI355X)",
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -1117,7 +1129,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f32",
         "data": f"synthetic (N(0,1) float32, seeds {list(range(nin))})",
-        "config": {"workload": f"fp32 {args.workload} {expr} via @eas.kernel SPMD (mk.arange, masked tail), "
+        "config": {"workload": f"fp32 {args.workload} {expr} via @eas.kernel {style}, "
                                f"N=2^28, BLOCK={args.block}",
                    "N": N_ELEM, "BLOCK": args.block, "parallelism": "single GPU"},
         "parity": parity,
