@@ -502,3 +502,34 @@ def test_kernels_that_stay_one_thread_per_thread(case, monkeypatch):
     with pytest.raises(ValueError, match="EAS_HIP_THREAD_LANES must be 0 or 1"):
         eas.kernel(simple_fma_kernel.fn).compile(f, f, f, f.copy(), 256, BLOCK=256)
 
+
+_MAPPING_ENVS = [{}, {"EAS_HIP_SPMD_WG": "32"}, {"EAS_HIP_SPMD_WG": "64"}, {"EAS_HIP_SPMD_WG": "1024"},
+                 {"EAS_HIP_SPMD_LPT": "16"}, {"EAS_HIP_SPMD_UNROLL": "2"}]
+_BLOCKS = sorted(set(range(1, 65)) | {96, 100, 127, 128, 160, 200, 250, 256, 384, 500, 512, 640, 768, 1000, 1024})
+
+
+@pytest.mark.parametrize("env", _MAPPING_ENVS, ids=lambda e: ",".join(f"{k[13:]}={v}" for k, v in e.items()) or "default")
+def test_every_lane_of_a_program_has_a_thread(env, monkeypatch):
+    """A program's BLOCK lanes are covered by its T threads (lanes_per_thread each), and those T
+    threads by its workgroups: `split` workgroups of `wg` threads, or `ppw` programs of T threads
+    in one workgroup.  Before this was checked a BLOCK such as 200 or 1000 (T = 50 or 250 over
+    32-thread workgroups) left lanes without a thread."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    f = _f(16)
+    for kern, args in ((K.add_kernel, (f, f, f, 8)), (K.copy_kernel, (f, f, 8)), (K.fill_kernel, (f, 8)),
+                       (K.fma_kernel, (f, f, f, f, 8)), (K.simple_fma_kernel, (f, f, f, f, 8))):
+        for block in _BLOCKS:
+            if kern is K.simple_fma_kernel and block > 1024:
+                continue
+            geo = eas.kernel(kern.fn).compile(*args, BLOCK=block).geometry
+            if not geo.params.get("lanes_per_thread"):
+                assert kern is K.simple_fma_kernel and block == 1  # one thread per Metal thread
+                continue
+            T, lpt = geo.params["threads_per_program"], geo.params["lanes_per_thread"]
+            assert T * lpt == block, (kern.name, block, env)
+            if geo.split > 1:
+                assert geo.programs_per_wg == 1 and geo.split * geo.wg_size == T, (kern.name, block, env, geo)
+            else:
+                assert geo.wg_size == T * geo.programs_per_wg <= 1024, (kern.name, block, env, geo)
+

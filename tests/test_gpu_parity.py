@@ -103,6 +103,21 @@ def _thread_add_f16(a, b, c, N, BLOCK: eas.constexpr):
     mk.store(c, offs, mk.load(a, offs, m) + mk.load(b, offs, m), m)
 
 
+@pytest.mark.parametrize("block", [3, 100, 200, 1000])
+def test_blocks_that_are_not_powers_of_two(gpu_runtime, block):
+    """SPMD add and fma and the thread-mode fma at BLOCKs whose thread count per program the
+    default 32-thread workgroup does not divide (200, 1000) or does not fill (3, 100): every lane."""
+    n = 7 * block + 5
+    a, b, c = seeded_normal(0, n), seeded_normal(1, n), seeded_normal(2, n)
+    out = np.full(n + 3, np.nan, np.float32)
+    eas.kernel(K.add_kernel.fn)(a, b, out, n, BLOCK=block)
+    assert _bits_equal(out[:n], ops.add_f32(a, b)) and np.all(np.isnan(out[n:])), block
+    for kern in (K.fma_kernel, K.simple_fma_kernel):
+        out = np.full(n + 3, np.nan, np.float32)
+        eas.kernel(kern.fn)(a, b, c, out, n, BLOCK=block)
+        assert _bits_equal(out[:n], ops.fmaf(a, b, c)) and np.all(np.isnan(out[n:])), (kern.name, block)
+
+
 @pytest.mark.parametrize("lanes", ["1", "0"])
 @pytest.mark.parametrize("block", [32, 64, 256, 1024])
 def test_thread_mode_element_streams(gpu_runtime, monkeypatch, block, lanes):
