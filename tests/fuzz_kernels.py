@@ -272,7 +272,9 @@ def case(seed: int) -> dict:
     would read slots no thread wrote), the others often a partial last group."""
     r = random.Random(10_000 + seed)
     mode = "spmd" if seed % 2 == 0 else "thread"
-    block = r.choice((64, 128, 256))
+    # seeds from 200 on also take BLOCKs that are not powers of two, and the extremes, so the
+    # emitters' workgroup mappings meet thread counts their workgroup sizes do not divide
+    block = r.choice((64, 128, 256)) if seed < 200 else r.choice((32, 96, 100, 200, 384, 1000, 1024))
     n = r.randrange(1, 9000)
     options: dict = {}
     if mode == "thread" and r.random() < 0.4:

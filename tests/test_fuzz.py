@@ -15,8 +15,8 @@ import pytest
 import fuzz_kernels as F
 from oracle import interp
 
-CPU_SEEDS = range(24)
-GPU_SEEDS = range(200)
+CPU_SEEDS = list(range(24)) + list(range(200, 212))
+GPU_SEEDS = range(260)
 
 
 
@@ -107,7 +107,7 @@ def _lanes_seeds() -> list[int]:
     """The thread-mode cases the emitter takes as lanes of one program per threadgroup (element
     streams without barriers, threadgroup memory, thread positions or dot)."""
     seeds = []
-    for seed in range(1, 200, 2):
+    for seed in range(1, 260, 2):
         c = F.case(seed)
         if c["mode"] != "thread":
             continue
