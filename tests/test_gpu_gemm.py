@@ -406,3 +406,39 @@ def test_baseline_shapes_every_output_vs_float64(gpu_runtime, case):
     assert bool(torch.isfinite(got).all())
     err = float((got - ref).abs().max() / ref.abs().max())
     assert err <= (2e-3 if out16 else 1e-5 * math.sqrt(k)), err
+
+
+_MMA_TILES = [(8, 8, 8), (16, 16, 8), (64, 32, 8), (8, 64, 8), (64, 16, 8), (32, 32, 32)]
+_TILED_TILES = [(16, 16, 8), (32, 64, 16), (64, 64, 8), (8, 32, 32), (64, 16, 4), (32, 32, 8)]
+
+
+@pytest.mark.parametrize("mnk", [(300, 520, 200), (77, 130, 33)])
+@pytest.mark.parametrize("kind,tile", [("mma", t) for t in _MMA_TILES] + [("tiled", t) for t in _TILED_TILES])
+def test_lift_over_tile_parameters(gpu_runtime, kind, tile, mnk):
+    """The reference kernels at tile shapes other than the examples' (8 x 8 to 64 x 64, BK 4-32):
+    the lift accepts each, the launch plan maps the reference grid onto its own tile per
+    threadgroup, and every output matches float64, with nothing written past C."""
+    m, n, k = mnk
+    bm, bn, bk = tile
+    pad = 37
+    if kind == "mma":
+        nt = (bm // 8) * (bn // 8) * 32
+        a, b = _inputs(m, n, k)
+        c = np.full(m * n + pad, np.nan, np.float32)
+        ck = K.matmul_mma_kernel.compile(a, b, c, m, n, BM=bm, BN=bn, BK=bk, K=k, NT=nt)
+        _mma(K.matmul_mma_kernel, a, b, c, m, n, k, bm, bn, bk)
+        ref = ops.matmul_ref(a.reshape(m, k).astype(np.float32), b.reshape(k, n).astype(np.float32))
+    else:
+        nt = bm * (bn // 4)
+        a, b = _inputs(m, n, k, np.float32)
+        c = np.full(m * n + pad, np.nan, np.float32)
+        ck = K.matmul_tiled_kernel.compile(a, b, c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt)
+        K.matmul_tiled_kernel(a, b, c, m, n, 0, 0, BM=bm, BN=bn, BK=bk, K=k, NT=nt,
+                              _grid=(K.cdiv(n, bn), K.cdiv(m, bm), 1), _tptg=(nt, 1, 1))
+        ref = ops.matmul_ref(a.reshape(m, k), b.reshape(k, n))
+    assert ck.geometry.kind == "gemm", (kind, tile)
+    assert np.all(np.isnan(c[m * n:])), "wrote past C"
+    assert np.isfinite(c[:m * n]).all(), "an output was not written"
+    err = ops.rel_err(np.asarray(c[:m * n], np.float64).reshape(m, n), ref)
+    assert err <= 1e-5 * math.sqrt(k), (kind, tile, mnk, err)
+
