@@ -7,7 +7,9 @@ at N = 2^28).  When the kernel uses nothing that ties a Metal thread to a HIP th
 threadgroup memory, local/lane/simdgroup id, dot or MMA), the threads of one threadgroup are
 independent element computations, and the SPMD emitter's mapping applies: the threadgroup
 becomes a program of BLOCK lanes (``tid`` becomes ``arange``, ``thread_id(0)`` becomes
-``program_id(0) * BLOCK + arange``), each HIP thread carries 16-byte vectors of several lanes,
+``program_id(0) * BLOCK + arange``; a thread's position in its threadgroup is its lane, so
+``local_id(0)`` is the lane, ``lane_id`` the lane mod 32 and ``sg_id`` the lane / 32, the
+32-lane simdgroups of the Metal model), each HIP thread carries 16-byte vectors of several lanes,
 and small workgroups keep every HBM stream in short chunks.
 
 What a launch means does not change: the grid counts threadgroups (or a 1-D thread count), the
@@ -28,8 +30,8 @@ import os
 from ..ir import Arg, DType, Inst, IRModule, ValueRef, validate_ir
 
 # ops a Metal thread of such a kernel may use: element arithmetic, its ids, its own loads/stores
-_ALLOWED = frozenset({"arg", "const", "tid", "thread_id", "program_id", "add", "mul", "floordiv", "mod",
-                      "lt", "and", "or", "not", "where", "cast", "fma", "load", "store"})
+_ALLOWED = frozenset({"arg", "const", "tid", "thread_id", "program_id", "local_id", "lane_id", "sg_id", "add",
+                      "mul", "floordiv", "mod", "lt", "and", "or", "not", "where", "cast", "fma", "load", "store"})
 # each lane-varying instruction is emitted once per lane a HIP thread carries
 _MAX_INSTS = 256
 NTHREADS = "__eas_nthreads"
@@ -46,7 +48,8 @@ def enabled() -> bool:
 def as_lanes(ir: IRModule, block: int) -> IRModule | None:
     """The program-of-lanes form of thread-mode ``ir`` (one program per threadgroup of ``block``
     threads, an extra u32 argument ``__eas_nthreads`` last), or None when the kernel does not
-    qualify: it uses an op outside the element-stream set, is longer than the emitter unrolls,
+    qualify: it uses an op outside the element-stream set (a barrier, threadgroup memory, dot
+    or MMA), is longer than the emitter unrolls,
     has no lane-varying store, or stores a lane-varying value at a shared offset."""
     if not enabled() or block < 2 or block > 1024 or len(ir.insts) > _MAX_INSTS:
         return None  # (a BLOCK above 1024 is the thread emitter's error to raise)
@@ -61,6 +64,8 @@ def as_lanes(ir: IRModule, block: int) -> IRModule | None:
         return ref
 
     insts: list[Inst] = []
+    c32 = fresh(DType.U32, 1)
+    c0 = fresh(DType.U32, 1)
     nth = fresh(DType.U32, 1)
     pid = fresh(DType.U32, 1)
     cb = fresh(DType.U32, 1)
@@ -74,7 +79,9 @@ def as_lanes(ir: IRModule, block: int) -> IRModule | None:
             Inst("mul", base, (pid, cb)),
             Inst("arange", lane, (0, block)),
             Inst("add", x, (base, lane)),
-            Inst("lt", live, (x, nth))]
+            Inst("lt", live, (x, nth)),
+            Inst("const", c32, (32,)),
+            Inst("const", c0, (0,))]
     new: dict[int, ValueRef] = {}
     consts_true: set[int] = set()
     live_masks: dict[int, ValueRef] = {}  # mask id -> mask && live, made once
@@ -102,6 +109,16 @@ def as_lanes(ir: IRModule, block: int) -> IRModule | None:
         if op == "tid":
             ref = ValueRef(out.id, DType.U32, block)
             insts.append(Inst("arange", ref, (int(inst.args[0]), block)))
+            new[out.id] = ref
+            continue
+        if op in ("local_id", "lane_id", "sg_id"):
+            if op == "local_id" and int(inst.args[0]) != 0:  # threadgroups are (BLOCK, 1, 1)
+                ref = ValueRef(out.id, DType.U32, 1)
+                insts.append(Inst("const", ref, (0,)))
+            else:  # the lane (its own SSA value: lane + 0), lane mod 32, lane / 32
+                ref = ValueRef(out.id, DType.U32, block)
+                src = {"local_id": ("add", c0), "lane_id": ("mod", c32), "sg_id": ("floordiv", c32)}[op]
+                insts.append(Inst(src[0], ref, (lane, src[1])))
             new[out.id] = ref
             continue
         if op == "thread_id":

@@ -439,14 +439,15 @@ def test_dot_over_a_runtime_k_is_a_loop_not_unrolled():
 def test_local_lane_and_simdgroup_ids_come_from_the_thread_index():
     # reference: tests/test_local_and_lane_id.py:32-39 (the Metal kernels declare
     # [[thread_position_in_threadgroup]] and [[thread_index_in_simdgroup]]).  HIP has those as
-    # builtins: the local id is threadIdx.x, and the 32-lane simdgroup of the Metal model maps onto
-    # half of a wave64, lane = threadIdx.x & 31 and simdgroup = threadIdx.x >> 5.  The launch's
-    # thread count (Metal's non-uniform grid) is a hidden u32 argument after the user's.
+    # builtins: on the one-thread-per-thread emitter the local id is threadIdx.x, and the 32-lane
+    # simdgroup of the Metal model maps onto half of a wave64, lane = threadIdx.x & 31 and
+    # simdgroup = threadIdx.x >> 5.  The launch's thread count (Metal's non-uniform grid) is a
+    # hidden u32 argument after the user's.  (Emitted as lanes, the position is the lane: below.)
     out = np.zeros(256, np.float32)
     want = {"local_id_kernel": r"= threadIdx\.x;", "lane_id_kernel": r"= threadIdx\.x & 31u;",
             "sg_id_kernel": r"= threadIdx\.x >> 5;"}
     for name, pattern in want.items():
-        ck = getattr(K, name).compile(out, 256, BLOCK=256)
+        ck = _one_thread_per_thread(getattr(K, name), out, 256, BLOCK=256)
         assert ck.launch_mode == "thread"
         head = ck.src[ck.src.index(f"void __launch_bounds__(256) {name}("):]
         params = head[:head.index("{")]
@@ -482,12 +483,22 @@ def test_thread_element_streams_are_emitted_as_lanes():
     assert len(re.findall(r"if \((v\d+)\[0\] && \1\[1\]", body)) == 4  # three loads, one store
 
 
-@pytest.mark.parametrize("case", ["local_id", "barrier", "dot", "shared_address_load", "lanes_off"])
+def test_thread_positions_as_lanes():
+    # a thread's position in its (BLOCK, 1, 1) threadgroup is its lane of the program:
+    # local id = lane, lane id = lane % 32, simdgroup id = lane / 32 (32-lane simdgroups)
+    out = _f(256)
+    for name, op in (("local_id_kernel", "+ v"), ("lane_id_kernel", "% v"), ("sg_id_kernel", "/ v")):
+        ck = eas.kernel(getattr(K, name).fn).compile(out, 256, BLOCK=256)
+        assert ck.launch_mode == "thread" and ck.geometry.params.get("lanes"), name
+        body = ck.src.split('extern "C"', 1)[1]
+        lane = re.search(r"(v\d+)\[0\] = 0u \+ __lbase;", body).group(1)
+        assert re.search(rf"= {lane}\[0\] {re.escape(op)}\d+;", body), (name, op)
+
+
+@pytest.mark.parametrize("case", ["barrier", "dot", "shared_address_load", "lanes_off"])
 def test_kernels_that_stay_one_thread_per_thread(case, monkeypatch):
     f, h = _f(256), _h(256)
-    if case == "local_id":  # a Metal thread's position in its threadgroup
-        ck = K.local_id_kernel.compile(f, 256, BLOCK=256)
-    elif case == "barrier":  # threadgroup memory shared between threads
+    if case == "barrier":  # threadgroup memory shared between threads
         ck = K.tg_copy_kernel.compile(f, f.copy(), 256, BLOCK=256)
     elif case == "dot":
         ck = dot_f16_tn4_kernel.compile(h, h, f, 8, BLOCK=128)
