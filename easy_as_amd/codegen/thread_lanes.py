@@ -48,9 +48,9 @@ def enabled() -> bool:
 def as_lanes(ir: IRModule, block: int) -> IRModule | None:
     """The program-of-lanes form of thread-mode ``ir`` (one program per threadgroup of ``block``
     threads, an extra u32 argument ``__eas_nthreads`` last), or None when the kernel does not
-    qualify: it uses an op outside the element-stream set (a barrier, threadgroup memory, dot
-    or MMA), is longer than the emitter unrolls,
-    has no lane-varying store, or stores a lane-varying value at a shared offset."""
+    qualify.  That is when it uses an op outside the element-stream set (a barrier,
+    threadgroup memory, dot or MMA), is longer than the emitter unrolls, has no lane-varying
+    store, or reads or writes a shared address under a per-thread mask or value."""
     if not enabled() or block < 2 or block > 1024 or len(ir.insts) > _MAX_INSTS:
         return None  # (a BLOCK above 1024 is the thread emitter's error to raise)
     if any(i.op not in _ALLOWED for i in ir.insts) or any(a.name == NTHREADS for a in ir.args):
