@@ -282,7 +282,7 @@ def case(seed: int) -> dict:
         n = max(2048, n)
         src = thread_source(seed, exchange=False)
     elif mode == "thread":
-        n = max(2048, n - n % block)
+        n = max(-(-2048 // block) * block, n - n % block)  # whole threadgroups, at least 2048 threads
         src = thread_source(seed)
     elif seed % 4 == 2:
         # 2-D grid: enough programs for N, laid out grid_x wide

@@ -55,6 +55,16 @@ def test_random_program_compiles_and_runs_in_the_oracle(seed):
     assert compile_code(mod, ck.src, ck.ir.name)[:4] == b"\x7fELF"
 
 
+def test_exchange_cases_run_whole_threadgroups():
+    # a threadgroup-memory exchange reads slots other threads wrote: a partial last threadgroup
+    # would read slots no thread wrote, so those cases need N to be a multiple of BLOCK (the
+    # BLOCKs from seed 200 on do not all divide 2048)
+    for seed in range(0, 460):
+        c = F.case(seed)
+        if "mk.barrier()" in c["src"] and c["mode"] == "thread":
+            assert c["N"] % c["BLOCK"] == 0 and c["N"] >= 2048, (seed, c["N"], c["BLOCK"])
+
+
 def test_same_values_treats_nans_alike_and_nothing_else():
     a = np.array([1.0, np.nan, -0.0], np.float32)
     assert F.same_values(a, np.array([1.0, -np.nan, -0.0], np.float32))
