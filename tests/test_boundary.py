@@ -95,6 +95,39 @@ def test_launch_by_threads_matches_every_spmd_mapping(hip, monkeypatch, env):
             assert hip.plan_dispatch(ck.src, tpg, tptg) == (plan.grid, plan.block, plan.hidden), (env, block, n)
 
 
+def test_random_launches_plan_alike(hip, monkeypatch):
+    """400 seeded launches of SPMD, lanes and one-thread-per-thread kernels over random BLOCKs,
+    workgroup mappings, sizes and explicit grids: the C planner (by threads, as `launch`, and by
+    threadgroups, as `launch_tg`) gives the dispatch `plan_launch` gives."""
+    import random
+
+    r = random.Random(7)
+    f = _f()
+    envs = [{}, {"EAS_HIP_SPMD_WG": "64"}, {"EAS_HIP_SPMD_WG": "1024"}, {"EAS_HIP_SPMD_LPT": "16"},
+            {"EAS_HIP_SPMD_UNROLL": "2"}, {"EAS_HIP_THREAD_LANES": "0"}]
+    kerns = [(K.add_kernel, (f, f, f)), (K.fill_kernel, (f,)), (K.simple_fma_kernel, (f, f, f, f)),
+             (K.tptg_independent_kernel, (f,)), (K.lane_id_kernel, (f,)), (K.tg_copy_kernel, (f, f))]
+    for case in range(400):
+        env = r.choice(envs)
+        with monkeypatch.context() as mp:
+            for k, v in env.items():
+                mp.setenv(k, v)
+            kern, bufs = r.choice(kerns)
+            block = r.choice((1, 2, 3, 32, 64, 96, 100, 200, 256, 384, 1000, 1024))
+            ck = eas.kernel(kern.fn).compile(*bufs, 8, BLOCK=block)
+        n = r.choice((1, block - 1 or 1, block, 7 * block + 3, r.randrange(1, 1 << 22), (1 << 28) + 5))
+        grid = None if r.random() < 0.6 else (r.randrange(1, 5000), r.randrange(1, 4), r.randrange(1, 3))
+        args = {"N": n}
+        what = (case, kern.name, block, env, n, grid)
+        plan = plan_launch(ck, args, grid=grid)
+        tpg, tptg = reference_dispatch(ck, args, grid=grid)
+        assert hip.plan_dispatch(ck.src, tpg, tptg) == (plan.grid, plan.block, plan.hidden), what
+        if ck.launch_mode == "thread" and grid is None:
+            continue  # by threadgroups a 1-D launch has every thread of them live: another launch
+        groups = grid or (-(-n // block), 1, 1)  # threadgroups, or SPMD programs
+        assert hip.plan_dispatch(ck.src, groups, tptg, by_groups=True) == (plan.grid, plan.block, plan.hidden), what
+
+
 def test_non_uniform_last_threadgroup(monkeypatch):
     # 1000 threads of BLOCK 256: four threadgroups, the hidden extent stops the last 24 threads.
     # Emitted as lanes (the default for this element stream), each threadgroup is two workgroups
